@@ -1,0 +1,292 @@
+"""Pins the CPU oracle beyond the golden vectors: fp64 brute force with the
+gamma_K accumulation bound, the reference GEMM's known-answer shapes
+(test/gemm_kernel_test.dart:45-97), closed-form special cases, the exact
+accumulation order the Dart SIMD kernel uses (an independent numpy float32
+emulation), DynamicQuantizeLinear's IEEE rules, and exact integer brute force
+for MatMulInteger."""
+import numpy as np
+import pytest
+
+from oracle import refcpu
+from onnx_runtime_dart_amd import synth
+
+U = 2.0 ** -24
+
+
+def gamma(k):
+    return k * U / (1 - k * U)
+
+
+def rand_mmnb(rng, m, k, n, bs, with_zp, scale_lo=0.005, scale_hi=0.02):
+    nb = (k + bs - 1) // bs
+    b = rng.integers(0, 256, size=(n, nb, bs // 2), dtype=np.uint8)
+    s = rng.uniform(scale_lo, scale_hi, size=(n, nb)).astype(np.float32)
+    z = rng.integers(0, 256, size=((n * nb + 1) // 2,), dtype=np.uint8) if with_zp else None
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    return a, b, s, z
+
+
+def seq_f32(a, w):
+    """Independent numpy emulation of the Dart order: per output, k-sequential
+    acc = fl32(acc + fl32(a*w)) from +0."""
+    m, k = a.shape
+    acc = np.zeros((m, w.shape[1]), dtype=np.float32)
+    for kk in range(k):
+        acc = acc + (a[:, kk:kk + 1] * w[kk:kk + 1, :])
+    return acc
+
+
+# ---------------------------------------------------------------- GEMM KAT
+def test_gemm_kernel_exhaustive_small_vs_f64():
+    # gemm_kernel_test.dart:45-60 (every m,k,n in 1..6, tol 1e-5)
+    rng = np.random.default_rng(11)
+    for m in range(1, 7):
+        for k in range(1, 7):
+            for n in range(1, 7):
+                a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+                b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+                out = refcpu.matmul_kernel(a, b, m, k, n)
+                want = a.astype(np.float64) @ b.astype(np.float64)
+                assert np.max(np.abs(out - want)) <= 1e-5, (m, k, n)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 384, 384), (33, 65, 17), (7, 128, 5),
+                                   (128, 64, 128), (5, 1, 9), (64, 384, 1),
+                                   (1, 40, 151), (1, 128, 19), (1, 896, 512)])
+def test_gemm_kernel_shapes_vs_f64_and_order(m, k, n):
+    # gemm_kernel_test.dart:62-78 (tol 1e-4), plus the exact Dart order.
+    rng = np.random.default_rng(m * 10007 + k * 101 + n)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    out = refcpu.matmul_kernel(a, b, m, k, n)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.max(np.abs(out - want)) < 1e-4
+    emu = seq_f32(a, b)
+    if m == 1 and n % 4:
+        nf = n - n % 4
+        np.testing.assert_array_equal(out[:, :nf], emu[:, :nf])
+        # _gemvScalar's tail columns accumulate in double (:300-308)
+        tail = (a.astype(np.float64) @ b[:, nf:].astype(np.float64))
+        np.testing.assert_array_equal(out[:, nf:], tail.astype(np.float32))
+    else:
+        np.testing.assert_array_equal(out, emu)
+
+
+def test_gemv_double_tail_is_observable():
+    # The f64 tail is a real difference from f32 accumulation on some inputs,
+    # so the test above discriminates the two orders.
+    rng = np.random.default_rng(5)
+    differs = False
+    for _ in range(20):
+        a = rng.standard_normal((1, 512)).astype(np.float32)
+        b = rng.standard_normal((512, 3)).astype(np.float32)
+        out = refcpu.matmul_kernel(a, b, 1, 512, 3)
+        differs |= bool(np.any(out != seq_f32(a, b)))
+    assert differs
+
+
+# --------------------------------------------------- MatMulNBits vs fp64
+@pytest.mark.parametrize("m,k,n,bs,zp", [
+    (1, 1024, 1024, 32, True),     # single-node config shape
+    (1, 1024, 2048, 128, False),   # decode q projection
+    (4, 1024, 1024, 128, False),
+    (8, 3072, 64, 128, False),
+    (3, 200, 37, 64, True),        # partial block, odd N
+    (1, 40, 5, 32, False),         # K < 2 blocks, m == 1 scalar tail
+    (17, 256, 24, 32, True),
+])
+def test_mmnb_within_gamma_bound_of_f64(m, k, n, bs, zp):
+    rng = np.random.default_rng(k * 7 + n + m)
+    a, b, s, z = rand_mmnb(rng, m, k, n, bs, zp)
+    y = refcpu.matmul_nbits(a, b, s, z, k, n, 4, bs)
+    y64, absdot = refcpu.matmul_nbits_f64(a, b, s, z, k, n, bs)
+    err = np.abs(y.astype(np.float64) - y64)
+    assert np.all(err <= gamma(k) * absdot + 1e-30)
+
+
+def test_mmnb_is_dequant_then_dart_gemm():
+    # Composition: the op equals the Dart GEMM order over the binary32 W.
+    rng = np.random.default_rng(3)
+    for (m, k, n, bs) in [(5, 96, 12, 32), (1, 128, 16, 64), (1, 64, 7, 32)]:
+        a, b, s, z = rand_mmnb(rng, m, k, n, bs, True)
+        w = refcpu.dequant(b, s, z, k, n, bs)
+        y = refcpu.matmul_nbits(a, b, s, z, k, n, 4, bs)
+        np.testing.assert_array_equal(y, refcpu.matmul_kernel(a, w, m, k, n))
+
+
+def test_dequant_closed_forms():
+    rng = np.random.default_rng(9)
+    k, n, bs = 96, 6, 32
+    nb = 3
+    # all-zero nibbles, implicit zero point 8 -> W = -8 * scale exactly
+    b = np.zeros((n, nb, bs // 2), np.uint8)
+    s = rng.uniform(0.1, 2, (n, nb)).astype(np.float32)
+    w = refcpu.dequant(b, s, None, k, n, bs)
+    want = (-8.0 * s[:, np.arange(k) // bs]).T.astype(np.float32)
+    np.testing.assert_array_equal(w, want)
+    # unit scales, zp 8 -> integer matrix q - 8; low nibble is the even k
+    b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
+    s = np.ones((n, nb), np.float32)
+    w = refcpu.dequant(b, s, None, k, n, bs)
+    q = np.stack([b & 0xF, b >> 4], axis=-1).reshape(n, k).astype(np.int64)
+    np.testing.assert_array_equal(w, (q - 8).T.astype(np.float32))
+    # explicit zero points, odd N*nBlocks: the last nibble sits alone
+    n2, nb2 = 3, 1
+    b = rng.integers(0, 256, (n2, nb2, bs // 2), dtype=np.uint8)
+    z = np.array([0x21, 0x03], np.uint8)  # zps 1, 2, 3 (flat, low first)
+    s = np.ones((n2, nb2), np.float32)
+    w = refcpu.dequant(b, s, z, bs, n2, bs)
+    q = np.stack([b & 0xF, b >> 4], axis=-1).reshape(n2, bs).astype(np.int64)
+    np.testing.assert_array_equal(w, (q - np.array([[1], [2], [3]])).T.astype(np.float32))
+
+
+def test_partial_block_ignores_padding_nibbles():
+    rng = np.random.default_rng(4)
+    k, n, bs = 40, 5, 32
+    a, b, s, z = rand_mmnb(rng, 2, k, n, bs, False)
+    y1 = refcpu.matmul_nbits(a, b, s, None, k, n, 4, bs)
+    b2 = b.copy()
+    b2[:, 1, 4:] ^= 0xFF  # bytes beyond k = 40 inside the last blob
+    y2 = refcpu.matmul_nbits(a, b2, s, None, k, n, 4, bs)
+    np.testing.assert_array_equal(y1, y2)
+
+
+def test_bits_other_than_4_unsupported():
+    with pytest.raises(refcpu.OracleError):
+        refcpu.matmul_nbits(np.zeros((1, 32), np.float32),
+                            np.zeros((1, 1, 16), np.uint8),
+                            np.ones(1, np.float32), None, 32, 1, 8, 32)
+
+
+@pytest.mark.parametrize("m,n", [(1, 1024), (1, 19), (1, 151), (3, 70), (8, 33)])
+def test_column_sliced_threads_bitwise_equal(m, n):
+    # parallel_pool_test.dart:27-100's invariant for the CPU baseline.
+    rng = np.random.default_rng(m + n)
+    k, bs = 256, 32
+    a, b, s, z = rand_mmnb(rng, m, k, n, bs, True)
+    y1 = refcpu.matmul_nbits(a, b, s, z, k, n, 4, bs)
+    for t in (2, 3, 8):
+        yt = refcpu.matmul_nbits(a, b, s, z, k, n, 4, bs, threads=t)
+        np.testing.assert_array_equal(y1, yt)
+
+
+# ------------------------------------------------ DynamicQuantizeLinear
+def test_dql_scale_and_zero_point_sequence():
+    rng = np.random.default_rng(12)
+    for _ in range(50):
+        x = (rng.standard_normal(257) * rng.uniform(0.01, 50)).astype(np.float32)
+        y, scale, zp = refcpu.dynamic_quantize_linear(x)
+        mn = min(0.0, float(x.min()))
+        mx = max(0.0, float(x.max()))
+        assert scale == np.float32((mx - mn) / 255.0)
+        zpf = np.float32(-mn / float(scale))
+        assert zp == int(np.round(np.clip(np.float64(zpf), 0, 255)))
+        # quantization property: |(y - zp) * scale - x| <= scale/2 in range
+        deq = (y.astype(np.float64) - zp) * float(scale)
+        inside = (y > 0) & (y < 255)
+        assert np.all(np.abs(deq - x)[inside] <= float(scale) * 0.5 * (1 + 1e-6))
+
+
+def test_dql_ties_round_half_even():
+    # scale = 1 exactly: x = [-255/255*..] choose mx - mn = 255 -> scale 1.0
+    x = np.array([0.0, 255.0, 0.5, 1.5, 2.5, 3.5, 100.5, 101.5], np.float32)
+    y, scale, zp = refcpu.dynamic_quantize_linear(x)
+    assert scale == np.float32(1.0) and zp == 0
+    assert y.tolist() == [0, 255, 0, 2, 2, 4, 100, 102]
+
+
+def test_dql_special_ranges():
+    y, scale, zp = refcpu.dynamic_quantize_linear(np.zeros(7, np.float32))
+    assert scale == 0.0 and zp == 0 and not y.any()
+    y, scale, zp = refcpu.dynamic_quantize_linear(-np.arange(1, 9, dtype=np.float32))
+    assert zp == 255 and y[-1] == 0
+    y, scale, zp = refcpu.dynamic_quantize_linear(np.arange(1, 9, dtype=np.float32))
+    assert zp == 0 and y[-1] == 255
+    y, scale, zp = refcpu.dynamic_quantize_linear(np.zeros(0, np.float32))
+    assert y.size == 0 and scale == 0.0 and zp == 0
+
+
+def test_dql_scale_uses_double_sequence():
+    # fl32(fl64(mx - mn) / 255) differs from the all-float32 formula on some
+    # inputs; the oracle follows the Dart double sequence
+    # (onnx_ops.dart:2566-2568).  No reference fixture distinguishes the two.
+    rng = np.random.default_rng(77)
+    found = 0
+    for _ in range(400):
+        x = rng.standard_normal(16).astype(np.float32) * np.float32(3.7)
+        _, scale, _ = refcpu.dynamic_quantize_linear(x)
+        mn, mx = min(0.0, float(x.min())), max(0.0, float(x.max()))
+        dart = np.float32((mx - mn) / 255.0)
+        f32 = np.float32(np.float32(np.float32(mx) - np.float32(mn)) / np.float32(255.0))
+        assert scale == dart
+        found += int(dart != f32)
+    assert found > 0
+
+
+# --------------------------------------------------------- MatMulInteger
+def brute_mmi(a, b, az, bz):
+    a64 = a.astype(np.int64)
+    b64 = b.astype(np.int64)
+    m = a.shape[-2]
+    n = b.shape[-1]
+    if az is not None:
+        az = np.asarray(az, np.int64).ravel()
+        a64 = a64 - (az[:, None] if az.size == m and m != 1 else az[0])
+    if bz is not None:
+        bz = np.asarray(bz, np.int64).ravel()
+        b64 = b64 - (bz[None, :] if bz.size == n and n != 1 else bz[0])
+    return np.matmul(a64, b64)
+
+
+@pytest.mark.parametrize("adt,bdt,az,bz,batch", [
+    (np.uint8, np.int8, "s", "s", None),
+    (np.uint8, np.int8, "row", "col", None),
+    (np.uint8, np.uint8, None, None, None),
+    (np.int8, np.int8, "s", None, None),
+    (np.uint8, np.int8, "s", "s", (3, 1)),
+    (np.uint8, np.int8, None, "col", (1, 2)),
+])
+def test_matmulinteger_brute_force(adt, bdt, az, bz, batch):
+    rng = np.random.default_rng(21)
+    m, k, n = 9, 70, 13
+    info = lambda dt: np.iinfo(dt)
+    ab, bb = (batch or (None, None))
+    ash = ((ab,) if ab else ()) + (m, k)
+    bsh = ((bb,) if bb else ()) + (k, n)
+    a = rng.integers(info(adt).min, info(adt).max + 1, ash).astype(adt)
+    b = rng.integers(info(bdt).min, info(bdt).max + 1, bsh).astype(bdt)
+    azv = {None: None, "s": np.array(rng.integers(0, 256), np.int64) if adt == np.uint8 else np.int64(-7),
+           "row": rng.integers(0, 256, m)}[az]
+    bzv = {None: None, "s": np.int64(5), "col": rng.integers(-128, 128, n)}[bz]
+    y = refcpu.matmul_integer(a, b, azv, bzv)
+    np.testing.assert_array_equal(y, brute_mmi(a, b, azv, bzv))
+
+
+def test_matmulinteger_rejects_bad_zero_point_length():
+    a = np.zeros((4, 3), np.uint8)
+    b = np.zeros((3, 5), np.int8)
+    with pytest.raises(NotImplementedError):
+        refcpu.matmul_integer(a, b, np.zeros(2, np.int64), None)
+    with pytest.raises(NotImplementedError):
+        refcpu.matmul_integer(a, b, None, np.zeros(3, np.int64))
+
+
+def test_rescale_closed_form():
+    rng = np.random.default_rng(2)
+    acc = rng.integers(-(1 << 30), 1 << 30, (6, 10)).astype(np.int64)
+    a_s = np.float32(0.0123)
+    b_s = rng.uniform(0.001, 0.1, 10).astype(np.float32)
+    y = refcpu.rescale(acc, a_s, b_s)
+    want = acc.astype(np.float32) * (a_s * b_s)[None, :]
+    np.testing.assert_array_equal(y, want)
+    y1 = refcpu.rescale(acc, a_s, b_s[:1])
+    np.testing.assert_array_equal(y1, acc.astype(np.float32) * (a_s * b_s[0]))
+
+
+def test_synth_generator_is_seeded_and_shaped():
+    p1 = synth.mmnb_problem(m=1, k=1024, n=1024, block=32, zp=True, seed=0)
+    p2 = synth.mmnb_problem(m=1, k=1024, n=1024, block=32, zp=True, seed=0)
+    assert p1.b_q.shape == (1024, 32, 16) and p1.scales.shape == (1024, 32)
+    assert p1.zero_points.shape == (1024 * 32 // 2,)
+    np.testing.assert_array_equal(p1.b_q, p2.b_q)
+    np.testing.assert_array_equal(p1.a, p2.a)
