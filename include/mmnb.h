@@ -1,0 +1,210 @@
+/*
+ * mmnb.h -- C ABI of libmmnb: MI355X (gfx950) kernels for the quantized
+ * matrix-multiply path of onnx_runtime_dart.
+ *
+ *   MatMulNBits            int4 block-quantized weights, fp32 activations
+ *   DynamicQuantizeLinear  fp32 -> uint8 with data-derived scale/zero point
+ *   MatMulInteger          uint8/int8 x uint8/int8 -> int32, exact
+ *
+ * Plain C types only (pointers, sizes, status codes): this is the surface a
+ * dart:ffi binding (or ctypes, or C++) calls.  Each operator entry point
+ * names the reference function it replaces; paths are relative to the
+ * onnx_runtime_dart source tree.
+ *
+ * Conventions
+ *  - Every function returns an int status: MMNB_OK (0) or a negative code.
+ *    mmnb_last_error() returns a message for the calling thread's last
+ *    failure.  The codes map onto the reference's exception types:
+ *    MMNB_ERR_ARG -> ArgumentError / AssertionError, MMNB_ERR_UNSUPPORTED ->
+ *    UnsupportedError; device and allocation failures have no reference
+ *    counterpart (the reference never leaves the CPU).
+ *  - "host" entry points take host buffers and are synchronous: they return
+ *    after the result is back in the caller's memory (the reference ops are
+ *    pure synchronous functions).
+ *  - "_dev" entry points take device pointers and enqueue work on the
+ *    context's stream without waiting; call mmnb_synchronize() before
+ *    reading results.  Device buffers come from mmnb_device_alloc().
+ *  - Weight packs live in device memory (HBM) from mmnb_pack_* until
+ *    mmnb_pack_free(): weights are uploaded once and stay resident across
+ *    calls, like the initializer Tensors the reference keeps for the
+ *    lifetime of a model (onnx_graph.dart:90-93, :553).
+ *  - A context may be used from several threads; calls on one context are
+ *    serialised by an internal mutex.
+ */
+#ifndef MMNB_H
+#define MMNB_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MMNB_OK 0
+#define MMNB_ERR_ARG (-1)
+#define MMNB_ERR_UNSUPPORTED (-2)
+#define MMNB_ERR_DEVICE (-3)
+#define MMNB_ERR_OOM (-4)
+
+#define MMNB_ABI_VERSION 1
+
+typedef struct mmnb_ctx mmnb_ctx;
+typedef struct mmnb_pack mmnb_pack;
+
+/* ---- library / context ------------------------------------------------ */
+
+/* ABI version of the loaded library (MMNB_ABI_VERSION). */
+int mmnb_abi_version(void);
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char *mmnb_last_error(void);
+
+/* Open a context on HIP device `device` (one stream, default priority).
+ * Replaces: nothing in the reference (its ops run on the calling isolate);
+ * the Dart binding opens one context per process and keeps it alive while
+ * any OnnxModel holds a pack (OnnxModel.fromBytes,
+ * lib/onnx_runtime_dart.dart:65-88). */
+int mmnb_init(int device, mmnb_ctx **out);
+
+/* Release the context, its stream and scratch memory.  Packs must be freed
+ * first.  Mirrors OnnxModel.dispose (lib/onnx_runtime_dart.dart:140). */
+int mmnb_shutdown(mmnb_ctx *ctx);
+
+/* Device name, compute-unit count and HBM bytes of the context's GPU. */
+int mmnb_device_info(mmnb_ctx *ctx, char *name, size_t name_len,
+                     int *compute_units, int64_t *hbm_bytes);
+
+/* ---- MatMulNBits ------------------------------------------------------- */
+
+/* Upload a MatMulNBits weight to HBM.
+ *   b_q          uint8 [n, ceil(k/block_size), block_size/2], low nibble =
+ *                even k (onnx_qlinear_ops.dart:121, :144-145)
+ *   scales       fp32, n*ceil(k/block_size) values read flat (:123, :131)
+ *   zero_points  NULL (zero point 8, :132) or packed uint4, nibble index
+ *                col*n_blocks+blk, low nibble first (:133-137)
+ *   bits         must be 4 (:117-119 -> MMNB_ERR_UNSUPPORTED)
+ * The lengths are element counts of the caller's buffers and are checked.
+ * Replaces: the per-call dequantisation of opMatMulNBits
+ * (onnx_qlinear_ops.dart:127-149); the pack is what the Dart binding caches
+ * per `bQ` Tensor (Expando keyed on the initializer). */
+int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
+                    const float *scales, int64_t scales_len,
+                    const uint8_t *zero_points, int64_t zero_points_len,
+                    int64_t k, int64_t n, int64_t bits, int64_t block_size,
+                    mmnb_pack **out);
+
+/* y[m, n] = a[m, k] * dequant(B)^T, fp32 in and out, host buffers,
+ * synchronous.  m = len(a) / k as in the reference (:152).
+ * Replaces: opMatMulNBits (lib/src/onnx_qlinear_ops.dart:114-156), called
+ * from the _dispatch arm 'MatMulNBits' (lib/src/onnx_graph.dart:1584-1596). */
+int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
+                      int64_t m, float *y);
+
+/* Device-buffer form of mmnb_matmul_nbits (asynchronous on the context
+ * stream): d_a fp32 [m, k] row-major, d_y fp32 [m, n].
+ * Replaces: the same op, for callers that keep activations in HBM
+ * (a decoder loop feeding one node's output to the next). */
+int mmnb_matmul_nbits_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
+                          const float *d_a, int64_t m, float *d_y);
+
+/* ---- DynamicQuantizeLinear --------------------------------------------- */
+
+/* y = saturate(roundEven(x / scale) + zp), scale = fl32((max(0,x) -
+ * min(0,x)) / 255.0) in double, zp = roundEven(clamp(fl32(-min/scale))).
+ * Host buffers, synchronous; zero_point is returned as int64 like
+ * Tensor.scalarInt.
+ * Replaces: opDynamicQuantizeLinear (lib/src/onnx_ops.dart:2556-2583),
+ * _dispatch arm 'DynamicQuantizeLinear' (lib/src/onnx_graph.dart:1561-1562). */
+int mmnb_dynamic_quantize_linear(mmnb_ctx *ctx, const float *x, int64_t n,
+                                 uint8_t *y, float *scale,
+                                 int64_t *zero_point);
+
+/* Device-buffer form: d_scale (1 float) and d_zero_point (1 int32) are
+ * written on the device, so a following MatMulInteger can consume them
+ * without a host round trip. */
+int mmnb_dynamic_quantize_linear_dev(mmnb_ctx *ctx, const float *d_x,
+                                     int64_t n, uint8_t *d_y, float *d_scale,
+                                     int32_t *d_zero_point);
+
+/* ---- MatMulInteger ----------------------------------------------------- */
+
+/* Upload a MatMulInteger right-hand operand B [b_batch, k, n] (int8 when
+ * b_is_signed, else uint8) with its zero point: NULL/0 (none), 1 (scalar)
+ * or n (per column, only when n != 1); other lengths are
+ * MMNB_ERR_UNSUPPORTED (onnx_qlinear_ops.dart:35-43).
+ * Replaces: the B side of opMatMulInteger; the Dart binding caches the pack
+ * per `b` Tensor. */
+int mmnb_pack_integer(mmnb_ctx *ctx, const void *b, int b_is_signed,
+                      int64_t b_batch, int64_t k, int64_t n,
+                      const int64_t *b_zero_point, int64_t b_zero_point_len,
+                      mmnb_pack **out);
+
+/* y[batch, m, n] = (A - a_zp) (B - b_zp), exact int32.  A is
+ * [a_batch, m, k] (int8 when a_is_signed, else uint8); a_zero_point NULL/0,
+ * scalar (len 1) or per row (len m, m != 1).  batch = max(a_batch, b_batch);
+ * each must equal batch or 1 (:44-47).  Host buffers, synchronous.  The
+ * Dart binding widens y to Int64List (the reference returns Tensor.int64,
+ * :75-78).
+ * Replaces: opMatMulInteger (lib/src/onnx_qlinear_ops.dart:30-79),
+ * _dispatch arm 'MatMulInteger' (lib/src/onnx_graph.dart:1563-1567). */
+int mmnb_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *pack, const void *a,
+                        int a_is_signed, int64_t a_batch, int64_t m,
+                        const int64_t *a_zero_point, int64_t a_zero_point_len,
+                        int32_t *y);
+
+/* Device-buffer form.  d_a_zero_point is a device int32 array of length
+ * a_zero_point_len (0, 1 or m), e.g. the output of
+ * mmnb_dynamic_quantize_linear_dev. */
+int mmnb_matmul_integer_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
+                            const void *d_a, int a_is_signed, int64_t a_batch,
+                            int64_t m, const int32_t *d_a_zero_point,
+                            int64_t a_zero_point_len, int32_t *d_y);
+
+/* The dynamic-quantisation chain of an ORT-exported MatMul, on the device:
+ *   (a_u8, a_scale, a_zp) = DynamicQuantizeLinear(x)     x fp32 [m, k]
+ *   acc = MatMulInteger(a_u8, B, a_zp, b_zp)             exact int32
+ *   y   = fl32(fl32(acc) * fl32(a_scale * b_scale[j]))  Cast -> Mul -> Mul
+ * b_scale is a device fp32 array of length 1 or n.  d_acc (int32 [m, n]) may
+ * be NULL; when given it receives the exact accumulator.  d_a_q (uint8
+ * [m, k]), d_a_scale (1 float) and d_a_zero_point (1 int32) are required
+ * outputs of the quantisation step.
+ * Replaces: the node sequence DynamicQuantizeLinear -> MatMulInteger ->
+ * Cast -> Mul (onnx_graph.dart:1561-1567 dispatching onnx_ops.dart:2556-2583,
+ * onnx_qlinear_ops.dart:30-79, onnx_ops.dart:579-606, :399-401). */
+int mmnb_dynamic_matmul_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
+                            const float *d_x, int64_t m,
+                            const float *d_b_scale, int64_t b_scale_len,
+                            uint8_t *d_a_q, float *d_a_scale,
+                            int32_t *d_a_zero_point, int32_t *d_acc,
+                            float *d_y);
+
+/* ---- packs ------------------------------------------------------------- */
+
+/* Free a pack's device memory.  Mirrors dropping the initializer Tensor
+ * (OnnxModel.dispose / a NativeFinalizer on the Dart side). */
+int mmnb_pack_free(mmnb_pack *pack);
+
+/* Device bytes held by a pack. */
+int64_t mmnb_pack_device_bytes(const mmnb_pack *pack);
+
+/* ---- device memory and timing (harness utilities; no reference
+ *      counterpart: the reference has no device) ------------------------- */
+int mmnb_device_alloc(mmnb_ctx *ctx, size_t bytes, void **d_ptr);
+int mmnb_device_free(mmnb_ctx *ctx, void *d_ptr);
+int mmnb_memcpy_h2d(mmnb_ctx *ctx, void *d_dst, const void *src, size_t bytes);
+int mmnb_memcpy_d2h(mmnb_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+int mmnb_memset_dev(mmnb_ctx *ctx, void *d_dst, int value, size_t bytes);
+int mmnb_synchronize(mmnb_ctx *ctx);
+
+/* Record timing event `slot` (0..15) on the context stream; read the
+ * elapsed milliseconds between two recorded slots after they complete. */
+int mmnb_event_record(mmnb_ctx *ctx, int slot);
+int mmnb_event_elapsed_ms(mmnb_ctx *ctx, int slot_start, int slot_end,
+                          float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MMNB_H */

@@ -1,0 +1,200 @@
+"""ctypes binding of libmmnb.so (the C ABI declared in include/mmnb.h).
+
+This is the Python counterpart of the dart:ffi binding a Dart host would
+use: plain pointers, sizes and int status codes.  Loading fails loudly when
+the library has not been built; there is no CPU fallback.
+"""
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libmmnb.so"
+
+MMNB_OK = 0
+MMNB_ERR_ARG = -1
+MMNB_ERR_UNSUPPORTED = -2
+MMNB_ERR_DEVICE = -3
+MMNB_ERR_OOM = -4
+
+# Every symbol include/mmnb.h declares, with (restype, argtypes).
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+_P = ctypes.POINTER
+SIGNATURES = {
+    "mmnb_abi_version": (_int, []),
+    "mmnb_last_error": (ctypes.c_char_p, []),
+    "mmnb_init": (_int, [_int, _P(_vp)]),
+    "mmnb_shutdown": (_int, [_vp]),
+    "mmnb_device_info": (_int, [_vp, ctypes.c_char_p, _sz, _P(_int), _P(_i64)]),
+    "mmnb_pack_nbits": (_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+                               _i64, _P(_vp)]),
+    "mmnb_matmul_nbits": (_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mmnb_matmul_nbits_dev": (_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mmnb_dynamic_quantize_linear": (_int, [_vp, _vp, _i64, _vp, _P(ctypes.c_float),
+                                            _P(_i64)]),
+    "mmnb_dynamic_quantize_linear_dev": (_int, [_vp, _vp, _i64, _vp, _vp, _vp]),
+    "mmnb_pack_integer": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _P(_vp)]),
+    "mmnb_matmul_integer": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, _vp]),
+    "mmnb_matmul_integer_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, _vp]),
+    "mmnb_dynamic_matmul_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+                                       _vp, _vp]),
+    "mmnb_pack_free": (_int, [_vp]),
+    "mmnb_pack_device_bytes": (_i64, [_vp]),
+    "mmnb_device_alloc": (_int, [_vp, _sz, _P(_vp)]),
+    "mmnb_device_free": (_int, [_vp, _vp]),
+    "mmnb_memcpy_h2d": (_int, [_vp, _vp, _vp, _sz]),
+    "mmnb_memcpy_d2h": (_int, [_vp, _vp, _vp, _sz]),
+    "mmnb_memset_dev": (_int, [_vp, _vp, _int, _sz]),
+    "mmnb_synchronize": (_int, [_vp]),
+    "mmnb_event_record": (_int, [_vp, _int]),
+    "mmnb_event_elapsed_ms": (_int, [_vp, _int, _int, _P(ctypes.c_float)]),
+}
+
+_lib = None
+_lock = threading.RLock()
+
+
+class MmnbError(RuntimeError):
+    """Device or allocation failure (no reference counterpart)."""
+
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+def load():
+    """Load libmmnb.so; raises if it is missing (build it first)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built: run `python -m onnx_runtime_dart_amd.build` "
+                    "(the HIP extension is required; there is no CPU fallback)")
+            L = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = L
+    return _lib
+
+
+def check(rc):
+    """Map a status code to the reference's exception types:
+    ArgumentError -> ValueError, UnsupportedError -> NotImplementedError."""
+    if rc == MMNB_OK:
+        return
+    msg = load().mmnb_last_error().decode(errors="replace")
+    if rc == MMNB_ERR_ARG:
+        raise ValueError(msg)
+    if rc == MMNB_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    if rc == MMNB_ERR_OOM:
+        raise MemoryError(msg)
+    raise MmnbError(rc, msg)
+
+
+def ptr(a):
+    """Raw data pointer of a C-contiguous numpy array (None for None)."""
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Context:
+    """One HIP device context (one stream) of libmmnb."""
+
+    def __init__(self, device=0):
+        self.lib = load()
+        h = ctypes.c_void_p()
+        check(self.lib.mmnb_init(int(device), ctypes.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            check(self.lib.mmnb_shutdown(self.handle))
+            self.handle = None
+
+    def info(self):
+        name = ctypes.create_string_buffer(256)
+        cus = ctypes.c_int()
+        hbm = ctypes.c_int64()
+        check(self.lib.mmnb_device_info(self.handle, name, 256, ctypes.byref(cus),
+                                        ctypes.byref(hbm)))
+        return {"name": name.value.decode(), "compute_units": cus.value,
+                "hbm_bytes": hbm.value}
+
+    def synchronize(self):
+        check(self.lib.mmnb_synchronize(self.handle))
+
+    def alloc(self, nbytes):
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = DeviceBuffer(self, arr.nbytes, dtype=arr.dtype, shape=arr.shape)
+        if arr.nbytes:
+            check(self.lib.mmnb_memcpy_h2d(self.handle, buf.ptr, ptr(arr), arr.nbytes))
+        return buf
+
+    def event_record(self, slot):
+        check(self.lib.mmnb_event_record(self.handle, int(slot)))
+
+    def event_elapsed_ms(self, s0, s1):
+        ms = ctypes.c_float()
+        check(self.lib.mmnb_event_elapsed_ms(self.handle, int(s0), int(s1), ctypes.byref(ms)))
+        return float(ms.value)
+
+
+class DeviceBuffer:
+    """A device allocation made through the C ABI."""
+
+    def __init__(self, ctx, nbytes, dtype=np.uint8, shape=None):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        p = ctypes.c_void_p()
+        check(ctx.lib.mmnb_device_alloc(ctx.handle, max(1, self.nbytes), ctypes.byref(p)))
+        self.ptr = p
+
+    def numpy(self, dtype=None, shape=None):
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        sh = shape if shape is not None else (self.shape if dtype is None else
+                                              (self.nbytes // dt.itemsize,))
+        out = np.empty(sh, dtype=dt)
+        if out.nbytes:
+            check(self.ctx.lib.mmnb_memcpy_d2h(self.ctx.handle, ptr(out), self.ptr,
+                                               out.nbytes))
+        return out
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        if arr.nbytes:
+            check(self.ctx.lib.mmnb_memcpy_h2d(self.ctx.handle, self.ptr, ptr(arr),
+                                               arr.nbytes))
+
+    def free(self):
+        if self.ptr:
+            check(self.ctx.lib.mmnb_device_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+
+_default_ctx = None
+
+
+def default_context():
+    """Process-wide context on device 0 (what the Dart binding opens once)."""
+    global _default_ctx
+    with _lock:
+        if _default_ctx is None:
+            _default_ctx = Context(0)
+    return _default_ctx

@@ -1,0 +1,378 @@
+// Int8 dynamic-quantisation path on gfx950: DynamicQuantizeLinear and
+// MatMulInteger (i8 MFMA, exact int32) with the optional fp32 rescale.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "mmnb_internal.h"
+
+namespace mmnb {
+
+// ---------------------------------------------------------------------------
+// DynamicQuantizeLinear (onnx_ops.dart:2556-2583), bit-exact:
+//   pass 1  per-block min/max partials, starting from 0 (:2558-2562); NaN is
+//           skipped because it never compares below/above (Dart `<`/`>`).
+//   pass 2  every block reduces the partials itself (deterministic, no
+//           atomics), derives scale/zero point in double exactly as the
+//           reference, then quantises its slice:
+//             scale = fl32((mx - mn) / 255.0)           (double ops)
+//             zp    = roundEven(clamp(fl32(-mn / scale), 0, 255))
+//             y     = clamp(rint(fl32(x / scale)) + zp, 0, 255)
+//           fl32(x / scale) of two binary32 operands equals the reference's
+//           double quotient rounded to binary32 (double rounding is
+//           innocuous for division at these precisions), so __fdiv_rn gives
+//           the same bits.  rint is round-half-even, as _roundEven
+//           (onnx_ops.dart:2490-2497) for finite input.
+// ---------------------------------------------------------------------------
+constexpr int kDqlThreads = 256;
+constexpr int kDqlMaxBlocks = 1024;
+
+__global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restrict__ x,
+                                                            int64_t n,
+                                                            float2 *__restrict__ part) {
+  float mn = 0.0f, mx = 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool vec = (((uintptr_t)x) & 15) == 0;
+  if (vec) {
+    const int64_t n4 = n >> 2;
+    const float4 *x4 = (const float4 *)x;
+    for (int64_t i = tid; i < n4; i += stride) {
+      const float4 v = x4[i];
+      mn = v.x < mn ? v.x : mn; mx = v.x > mx ? v.x : mx;
+      mn = v.y < mn ? v.y : mn; mx = v.y > mx ? v.y : mx;
+      mn = v.z < mn ? v.z : mn; mx = v.z > mx ? v.z : mx;
+      mn = v.w < mn ? v.w : mn; mx = v.w > mx ? v.w : mx;
+    }
+    for (int64_t i = (n4 << 2) + tid; i < n; i += stride) {
+      const float v = x[i];
+      mn = v < mn ? v : mn;
+      mx = v > mx ? v : mx;
+    }
+  } else {
+    for (int64_t i = tid; i < n; i += stride) {
+      const float v = x[i];
+      mn = v < mn ? v : mn;
+      mx = v > mx ? v : mx;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float a = __shfl_xor(mn, off, 64), b = __shfl_xor(mx, off, 64);
+    mn = a < mn ? a : mn;
+    mx = b > mx ? b : mx;
+  }
+  __shared__ float2 s[kDqlThreads / 64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) s[wave] = make_float2(mn, mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kDqlThreads / 64; w++) {
+      mn = s[w].x < mn ? s[w].x : mn;
+      mx = s[w].y > mx ? s[w].y : mx;
+    }
+    part[blockIdx.x] = make_float2(mn, mx);
+  }
+}
+
+__device__ __forceinline__ uint8_t dql_q(float v, float scale, int zp) {
+  if (scale == 0.0f) return (uint8_t)zp;
+  const float r = rintf(__fdiv_rn(v, scale));
+  // r is an integral float; clamp before converting (|r| <= ~2^8 for finite
+  // in-contract input, but saturate defensively).
+  float q = r + (float)zp;
+  q = q < 0.0f ? 0.0f : (q > 255.0f ? 255.0f : q);
+  return (uint8_t)(int)q;
+}
+
+__global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
+    const float *__restrict__ x, int64_t n, const float2 *__restrict__ part, int nparts,
+    uint8_t *__restrict__ y, float *__restrict__ out_scale, int32_t *__restrict__ out_zp) {
+  __shared__ float2 s[kDqlThreads / 64];
+  __shared__ float s_scale;
+  __shared__ int s_zp;
+  float mn = 0.0f, mx = 0.0f;
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+    const float2 p = part[i];
+    mn = p.x < mn ? p.x : mn;
+    mx = p.y > mx ? p.y : mx;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float a = __shfl_xor(mn, off, 64), b = __shfl_xor(mx, off, 64);
+    mn = a < mn ? a : mn;
+    mx = b > mx ? b : mx;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) s[wave] = make_float2(mn, mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kDqlThreads / 64; w++) {
+      mn = s[w].x < mn ? s[w].x : mn;
+      mx = s[w].y > mx ? s[w].y : mx;
+    }
+    const double dmn = (double)mn, dmx = (double)mx;
+    const float scale = (float)((dmx - dmn) / 255.0);
+    const double ds = (double)scale;
+    const float zpf = ds == 0.0 ? 0.0f : (float)(-dmn / ds);
+    double zc = (double)zpf;
+    zc = zc < 0.0 ? 0.0 : (zc > 255.0 ? 255.0 : zc);
+    const int zp = (int)rint(zc);
+    s_scale = scale;
+    s_zp = zp;
+    if (blockIdx.x == 0) {
+      *out_scale = scale;
+      *out_zp = zp;
+    }
+  }
+  __syncthreads();
+  const float scale = s_scale;
+  const int zp = s_zp;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)y) & 3) == 0);
+  int64_t done = 0;
+  if (vec) {
+    const int64_t n4 = n >> 2;
+    const float4 *x4 = (const float4 *)x;
+    uint32_t *y4 = (uint32_t *)y;
+    for (int64_t i = tid; i < n4; i += stride) {
+      const float4 v = x4[i];
+      const uint32_t b = (uint32_t)dql_q(v.x, scale, zp) | ((uint32_t)dql_q(v.y, scale, zp) << 8) |
+                         ((uint32_t)dql_q(v.z, scale, zp) << 16) |
+                         ((uint32_t)dql_q(v.w, scale, zp) << 24);
+      y4[i] = b;
+    }
+    done = n4 << 2;
+  }
+  for (int64_t i = done + tid; i < n; i += stride) y[i] = dql_q(x[i], scale, zp);
+}
+
+int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *d_scale,
+               int32_t *d_zp) {
+  void *d_part = nullptr;
+  int rc;
+  if ((rc = scratch_get(ctx, 3, sizeof(float2) * kDqlMaxBlocks, &d_part))) return rc;
+  // ~8 float4 per thread in pass 1
+  int64_t blocks = (n + (int64_t)kDqlThreads * 32 - 1) / ((int64_t)kDqlThreads * 32);
+  if (blocks < 1) blocks = 1;
+  if (blocks > kDqlMaxBlocks) blocks = kDqlMaxBlocks;
+  hipLaunchKernelGGL(k_dql_minmax, dim3((unsigned)blocks), dim3(kDqlThreads), 0, ctx->stream,
+                     d_x, n, (float2 *)d_part);
+  MMNB_HIP(hipGetLastError());
+  int64_t qblocks = (n + (int64_t)kDqlThreads * 16 - 1) / ((int64_t)kDqlThreads * 16);
+  if (qblocks < 1) qblocks = 1;
+  if (qblocks > 4096) qblocks = 4096;
+  hipLaunchKernelGGL(k_dql_quant, dim3((unsigned)qblocks), dim3(kDqlThreads), 0, ctx->stream,
+                     d_x, n, (const float2 *)d_part, (int)blocks, d_y, d_scale, d_zp);
+  MMNB_HIP(hipGetLastError());
+  return MMNB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MatMulInteger (onnx_qlinear_ops.dart:30-79) on v_mfma_i32_16x16x64_i8.
+//
+// The i8 MFMA multiplies signed bytes.  Operands are offset into int8:
+//   A' = A xor 0x80 = A - 128 (uint8 A) or A (int8 A);  A - azp = A' + c_m,
+//        c_m = (uint8 ? 128 : 0) - azp_m
+//   B' = B xor 0x80 (uint8 B) or B;                      B - bzp = B' + e_n,
+//        e_n = (uint8 ? 128 : 0) - bzp_n
+// so  Y = sum A'B' + e_n sum_k A'_m + c_m sum_k B'_n + K c_m e_n,
+// every term an exact integer; the sum is evaluated modulo 2^32, which is
+// exact whenever the true result fits int32 (|Y| <= 255*255*K, K <= 33025).
+// B' is prepared once per pack as [batch][n][kpad] (k contiguous, zero
+// padded) with its column sums; row sums of A' come from v_dot4 on the
+// operand registers.
+// ---------------------------------------------------------------------------
+__global__ void k_prep_int_b(const uint8_t *__restrict__ src, int b_signed, int64_t batch,
+                             int64_t k, int64_t n, int64_t kpad, int8_t *__restrict__ bt,
+                             int32_t *__restrict__ colsum) {
+  // one thread per (batch, column)
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= batch * n) return;
+  const int64_t b = idx / n, col = idx % n;
+  const uint8_t *s = src + b * k * n + col;
+  int8_t *d = bt + (b * n + col) * kpad;
+  int32_t sum = 0;
+  for (int64_t kk = 0; kk < kpad; kk++) {
+    int v = 0;
+    if (kk < k) {
+      const uint8_t raw = s[kk * n];
+      v = b_signed ? (int)(int8_t)raw : (int)raw - 128;
+    }
+    d[kk] = (int8_t)v;
+    sum += v;
+  }
+  colsum[idx] = sum;
+}
+
+__global__ void k_prep_int_e(int b_signed, int64_t n, const int32_t *__restrict__ bzp,
+                             int64_t bzp_len, int32_t *__restrict__ ecol) {
+  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= n) return;
+  int32_t z = 0;
+  if (bzp_len == 1) z = bzp[0];
+  else if (bzp_len == n && n != 1) z = bzp[col];
+  ecol[col] = (b_signed ? 0 : 128) - z;
+}
+
+int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int64_t batch,
+                      int64_t k, int64_t n, int64_t kpad, const int32_t *d_bzp,
+                      int64_t bzp_len, int8_t *d_bt, int32_t *d_colsum, int32_t *d_ecol) {
+  const int threads = 256;
+  const int64_t tot = batch * n;
+  hipLaunchKernelGGL(k_prep_int_b, dim3((unsigned)((tot + threads - 1) / threads)),
+                     dim3(threads), 0, ctx->stream, d_src, b_signed, batch, k, n, kpad, d_bt,
+                     d_colsum);
+  MMNB_HIP(hipGetLastError());
+  hipLaunchKernelGGL(k_prep_int_e, dim3((unsigned)((n + threads - 1) / threads)),
+                     dim3(threads), 0, ctx->stream, b_signed, n, d_bzp, bzp_len, d_ecol);
+  MMNB_HIP(hipGetLastError());
+  return MMNB_OK;
+}
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// WG tile 64 x 64 (4 waves, 2 x 2), wave tile 32 x 32 = 2 x 2 MFMA tiles of
+// 16 x 16; K steps of 64.  Operand lanes: l%16 = row (A) / column (B),
+// l/16 = which 16-byte quarter of the 64-k step.
+__global__ __launch_bounds__(256) void k_mmi_mfma(
+    const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
+    const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
+    const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
+    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, int32_t *__restrict__ Y,
+    const float *__restrict__ a_scale, const float *__restrict__ b_scale,
+    int64_t b_scale_len, float *__restrict__ Yf, int fast) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t bz = blockIdx.z;
+  const uint8_t *Ab = A + bz * a_bstride;
+  const int8_t *Bb = Bt + bz * b_bstride;
+  const int64_t m0 = (int64_t)blockIdx.y * 64 + wm * 32;
+  const int64_t n0 = (int64_t)blockIdx.x * 64 + wn * 32;
+  const int r16 = lane & 15, q = lane >> 4;
+  const uint32_t flip = a_signed ? 0u : 0x80808080u;
+
+  int64_t arow[2], bcol[2];
+  bool arok[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    arow[t] = m0 + t * 16 + r16;
+    arok[t] = arow[t] < M;
+    if (!arok[t]) arow[t] = M - 1;
+    bcol[t] = n0 + t * 16 + r16;
+    if (bcol[t] >= N) bcol[t] = N - 1;
+  }
+  int4v acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = (int4v){0, 0, 0, 0};
+  int rsum[2] = {0, 0};
+
+  for (int64_t k0 = 0; k0 < kpad; k0 += 64) {
+    const int64_t kq = k0 + q * 16;
+    int4v av[2], bv[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      uint32_t w[4];
+      if (fast) {
+        // K % 16 == 0 and 16-byte aligned rows: whole quarters are in range
+        // or entirely past K.
+        if (kq < K) {
+          const uint4 v = *(const uint4 *)(Ab + arow[t] * K + kq);
+          w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else {
+          w[0] = w[1] = w[2] = w[3] = flip;  // becomes 0 after the flip
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          uint32_t x = 0;
+#pragma unroll
+          for (int b = 0; b < 4; b++) {
+            const int64_t kk = kq + d * 4 + b;
+            const uint32_t byte = kk < K ? (uint32_t)Ab[arow[t] * K + kk] : (flip & 0xFFu);
+            x |= byte << (8 * b);
+          }
+          w[d] = x;
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        w[d] ^= flip;
+        rsum[t] = __builtin_amdgcn_sdot4((int)w[d], 0x01010101, rsum[t], false);
+      }
+      av[t] = (int4v){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      const uint4 bb = *(const uint4 *)(Bb + bcol[t] * kpad + kq);
+      bv[t] = (int4v){(int)bb.x, (int)bb.y, (int)bb.z, (int)bb.w};
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
+  }
+  // full row sums: add the four 16-byte quarters (lanes r16 + 16 q)
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    rsum[t] += __shfl_xor(rsum[t], 16, 64);
+    rsum[t] += __shfl_xor(rsum[t], 32, 64);
+  }
+  // Epilogue.  16x16 i32 accumulator layout: lane l holds column l%16 and
+  // rows 4*(l/16) + r, r = 0..3.
+  const float as = Yf ? *a_scale : 0.0f;
+  const int64_t Kk = K;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    int32_t rs[4], cm[4];
+    int64_t row[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int src = q * 4 + r;  // lane holding that row's sum (any quarter)
+      rs[r] = __shfl(rsum[i], src, 64);
+      row[r] = m0 + i * 16 + q * 4 + r;
+      int32_t z = 0;
+      if (azp_len == 1) z = azp[0];
+      else if (azp_len > 1 && row[r] < M) z = azp[row[r]];
+      cm[r] = (a_signed ? 0 : 128) - z;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int64_t col = n0 + j * 16 + r16;
+      if (col >= N) continue;
+      const uint32_t e = (uint32_t)ecol[col];
+      const uint32_t cs = (uint32_t)colsum[bz * cs_bstride + col];
+      float sj = 0.0f;
+      if (Yf) sj = as * b_scale[b_scale_len == 1 ? 0 : col];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        if (row[r] >= M) continue;
+        const uint32_t c = (uint32_t)cm[r];
+        const uint32_t v = (uint32_t)acc[i][j][r] + e * (uint32_t)rs[r] + c * cs +
+                           (uint32_t)Kk * c * e;
+        const int64_t o = (bz * M + row[r]) * N + col;
+        if (Y) Y[o] = (int32_t)v;
+        if (Yf) Yf[o] = (float)(int32_t)v * sj;
+      }
+    }
+  }
+}
+
+int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, int a_signed,
+                          int64_t a_batch, int64_t m, const int32_t *d_azp, int64_t azp_len,
+                          int32_t *d_y, const float *d_a_scale, const float *d_b_scale,
+                          int64_t b_scale_len, float *d_yf) {
+  const int64_t batch = a_batch > p->batch ? a_batch : p->batch;
+  const int64_t k = p->k, n = p->n;
+  if (!d_y && !d_yf) return fail(MMNB_ERR_ARG, "MatMulInteger: no output");
+  const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
+  const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
+  hipLaunchKernelGGL(k_mmi_mfma, grid, dim3(256), 0, ctx->stream, (const uint8_t *)d_a,
+                     a_signed, a_batch == 1 ? (int64_t)0 : m * k, m, k, p->d_bt,
+                     p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, p->d_colsum,
+                     p->batch == 1 ? (int64_t)0 : n, p->d_ecol, n, d_azp, azp_len, d_y,
+                     d_a_scale, d_b_scale, b_scale_len, d_yf, fast);
+  MMNB_HIP(hipGetLastError());
+  return MMNB_OK;
+}
+
+}  // namespace mmnb

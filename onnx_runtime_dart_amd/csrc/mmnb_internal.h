@@ -1,0 +1,124 @@
+// Internal declarations shared by the libmmnb translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "../../include/mmnb.h"
+
+namespace mmnb {
+
+// ---------------------------------------------------------------------------
+// Weight-pack layout for MatMulNBits (device).
+//
+// The reference hands over B as uint8 [N, n_blocks, block/2]: per output
+// column n a contiguous run of n_blocks*block/2 bytes, two k per byte, low
+// nibble = even k.  The pack keeps that column-major-by-n layout (one
+// contiguous run per column, so a column streams with 16-byte loads) but pads
+// every column to a multiple of 64 k (32 bytes) and permutes the eight dwords
+// inside each 32-byte segment:
+//
+//     original dword i (k = 8i .. 8i+7 of the segment), i = 0..7
+//     packed order:  d0 d2 d4 d6 | d1 d3 d5 d7
+//
+// so the first 16 bytes of a segment hold k = 16j + e and the second 16 bytes
+// k = 16j + 8 + e (j = 0..3, e = 0..7).  A lane that loads 16 bytes therefore
+// owns one 8-k half of each of four consecutive 16-k steps, which is the
+// operand shape of the 32x32x16 f16 MFMA (lane group g = lane/32 holds
+// k = 8g..8g+7 of each 16-k step).  Padding nibbles are zero.
+//
+// Scales stay fp32 [N, n_blocks]; zero points stay packed uint4 with the
+// reference's flat nibble index n*n_blocks + blk (or absent: 8).
+// ---------------------------------------------------------------------------
+constexpr int kSegK = 64;        // k per 32-byte segment
+constexpr int kSegBytes = 32;
+constexpr size_t kTailPad = 1024;  // bytes of slack after every device buffer
+
+enum PackKind { kPackNBits = 1, kPackInteger = 2 };
+
+struct Scratch {
+  void *ptr = nullptr;
+  size_t cap = 0;
+};
+
+}  // namespace mmnb
+
+struct mmnb_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  hipEvent_t events[16] = {};
+  int cu_count = 0;
+  // Device staging/scratch buffers, grown on demand and kept for reuse:
+  //  0: activations in (fp32 / uint8), 1: outputs, 2: prepared activations
+  //  (fp16 hi/lo), 3: small reductions, 4: misc.
+  mmnb::Scratch scratch[6];
+  int live_packs = 0;
+};
+
+struct mmnb_pack {
+  mmnb_ctx *ctx = nullptr;
+  int kind = 0;
+  int64_t bytes = 0;
+  // --- MatMulNBits
+  int64_t k = 0, n = 0, block = 0, n_blocks = 0;
+  int64_t k64 = 0;        // k padded to a multiple of 64 (and >= n_blocks*block)
+  int64_t col_bytes = 0;  // bytes per column in d_w (= k64 / 2)
+  uint8_t *d_w = nullptr;
+  float *d_scales = nullptr;
+  uint8_t *d_zp = nullptr;
+  // --- MatMulInteger
+  int64_t batch = 0;
+  int64_t kpad = 0;          // k padded to a multiple of 64
+  int b_signed = 0;
+  int8_t *d_bt = nullptr;    // [batch, n, kpad] signed bytes (uint8 B xor 0x80)
+  int32_t *d_colsum = nullptr;  // [batch, n] sum_k B'
+  int32_t *d_ecol = nullptr;    // [n]  (uint8 ? 128 : 0) - b_zp[n]
+};
+
+namespace mmnb {
+
+// Error state (thread-local message) ---------------------------------------
+int fail(int code, const std::string &msg);
+int check_hip(hipError_t e, const char *what);
+#define MMNB_HIP(call)                                        \
+  do {                                                        \
+    hipError_t _e = (call);                                   \
+    if (_e != hipSuccess) return ::mmnb::check_hip(_e, #call); \
+  } while (0)
+
+// Grow-only device scratch owned by the context.
+int scratch_get(mmnb_ctx *ctx, int slot, size_t bytes, void **out);
+
+// Kernel launchers (return MMNB_OK or an error code) -------------------------
+// MatMulNBits: y[m, n] = a[m, k] * W;  lda = row stride of a (elements).
+int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
+                        int64_t lda, int64_t m, float *d_y);
+
+// DynamicQuantizeLinear on device.
+int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y,
+               float *d_scale, int32_t *d_zp);
+
+// MatMulInteger (+ optional fused rescale).  d_azp: device int32 of length
+// azp_len (0, 1 or m).  When d_yf is non-null, y_f32 = fl32(fl32(acc) *
+// fl32(a_scale * b_scale[j])) with a_scale read from d_a_scale.
+int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a,
+                          int a_signed, int64_t a_batch, int64_t m,
+                          const int32_t *d_azp, int64_t azp_len,
+                          int32_t *d_y, const float *d_a_scale,
+                          const float *d_b_scale, int64_t b_scale_len,
+                          float *d_yf);
+
+// Pack construction helpers (device-side repack kernels).
+int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n,
+                         int64_t k, int64_t src_col_bytes,
+                         int64_t dst_col_bytes, uint8_t *d_dst);
+int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed,
+                      int64_t batch, int64_t k, int64_t n, int64_t kpad,
+                      const int32_t *d_bzp, int64_t bzp_len, int8_t *d_bt,
+                      int32_t *d_colsum, int32_t *d_ecol);
+
+}  // namespace mmnb

@@ -1,0 +1,241 @@
+"""Host-side mirror of the reference's quantized operator functions, running
+on the MI355X through libmmnb's C ABI.
+
+Same names (snake_case), argument meaning, output types and error behaviour
+as the Dart functions they replace:
+
+* ``op_matmul_nbits``    <- ``opMatMulNBits``  (lib/src/onnx_qlinear_ops.dart:114-156)
+* ``op_matmul_integer``  <- ``opMatMulInteger`` (lib/src/onnx_qlinear_ops.dart:30-79)
+* ``op_dynamic_quantize_linear`` <- ``opDynamicQuantizeLinear``
+  (lib/src/onnx_ops.dart:2556-2583)
+* ``dispatch``           <- the three ``_dispatch`` arms
+  (lib/src/onnx_graph.dart:1561-1567, :1584-1596)
+
+Tensors are numpy arrays (shape + dtype + row-major data, like the Dart
+``Tensor``).  Exceptions: ``NotImplementedError`` where the reference throws
+``UnsupportedError``, ``ValueError`` for ``ArgumentError``/``AssertionError``.
+
+Weight packs are uploaded once and cached per weight object, the way a Dart
+binding caches them in an ``Expando`` keyed on the initializer ``Tensor``
+(initializers keep their identity across runs, onnx_graph.dart:90-93, :553).
+"""
+import ctypes
+import threading
+import weakref
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, ptr
+
+
+class _PackCache:
+    """Device packs keyed by the identity of the host arrays they came from;
+    a pack is freed when any of its source arrays is garbage collected."""
+
+    def __init__(self):
+        self._packs = {}
+        self._lock = threading.Lock()
+
+    def get(self, key_objs, extra, make):
+        key = tuple(id(o) for o in key_objs) + tuple(extra)
+        with self._lock:
+            hit = self._packs.get(key)
+            if hit is not None:
+                refs, pack = hit
+                if all(r() is o for r, o in zip(refs, key_objs)):
+                    return pack
+                self._drop(key)
+        pack = make()
+        refs = []
+        for o in key_objs:
+            try:
+                refs.append(weakref.ref(o, lambda _r, k=key: self.evict(k)))
+            except TypeError:
+                refs.append(lambda o=o: o)  # not weak-referenceable: keep alive
+        with self._lock:
+            self._packs[key] = (refs, pack)
+        return pack
+
+    def evict(self, key):
+        with self._lock:
+            self._drop(key)
+
+    def _drop(self, key):
+        hit = self._packs.pop(key, None)
+        if hit is not None:
+            hit[1].free()
+
+    def clear(self):
+        with self._lock:
+            for key in list(self._packs):
+                self._drop(key)
+
+
+_CACHE = _PackCache()
+
+
+class Pack:
+    """An uploaded weight pack (device memory owned by libmmnb)."""
+
+    def __init__(self, ctx, handle, kind, **meta):
+        self.ctx = ctx
+        self.handle = handle
+        self.kind = kind
+        self.__dict__.update(meta)
+
+    @property
+    def device_bytes(self):
+        return int(self.ctx.lib.mmnb_pack_device_bytes(self.handle))
+
+    def free(self):
+        if self.handle:
+            check(self.ctx.lib.mmnb_pack_free(self.handle))
+            self.handle = None
+
+
+def _ctx(ctx):
+    return ctx if ctx is not None else _lib.default_context()
+
+
+# --------------------------------------------------------------- MatMulNBits
+
+def pack_nbits(b_q, scales, zero_points, *, k, n, bits, block_size, ctx=None):
+    """Upload a MatMulNBits weight (B, scales, optional packed zero points)."""
+    ctx = _ctx(ctx)
+    b = np.ascontiguousarray(b_q)
+    if b.dtype != np.uint8:
+        # the reference re-packs non-uint8 B through asIntList (:124)
+        b = np.ascontiguousarray(np.asarray(b, dtype=np.int64).astype(np.uint8))
+    s = np.ascontiguousarray(scales, dtype=np.float32)
+    z = None if zero_points is None else np.ascontiguousarray(zero_points)
+    if z is not None and z.dtype != np.uint8:
+        # float zero points are not byte data: the reference reads them as 8
+        # (zeroPoints?.u8 is null, :124, :132)
+        z = None
+    h = ctypes.c_void_p()
+    check(ctx.lib.mmnb_pack_nbits(ctx.handle, ptr(b), b.size, ptr(s), s.size, ptr(z),
+                                  0 if z is None else z.size, int(k), int(n), int(bits),
+                                  int(block_size), ctypes.byref(h)))
+    return Pack(ctx, h, "nbits", k=int(k), n=int(n), block=int(block_size))
+
+
+def op_matmul_nbits(a, b_q, scales, zero_points, *, k, n, bits, block_size, ctx=None):
+    """``y = A . dequant(B)^T``; A fp32 ``[..., K]``, returns fp32 ``[..., N]``.
+
+    Mirrors opMatMulNBits (onnx_qlinear_ops.dart:114-156): ``bits != 4`` is
+    unsupported, ``m = len(A) / K``."""
+    if bits != 4:
+        raise NotImplementedError(f"MatMulNBits: only bits=4 supported, got {bits}")
+    ctx = _ctx(ctx)
+    keys = [b_q, scales] + ([zero_points] if zero_points is not None else [])
+    pack = _CACHE.get(keys, (k, n, bits, block_size, ctx.device),
+                      lambda: pack_nbits(b_q, scales, zero_points, k=k, n=n, bits=bits,
+                                         block_size=block_size, ctx=ctx))
+    af = np.ascontiguousarray(a, dtype=np.float32)
+    if af.ndim == 0 or af.shape[-1] != k:
+        raise ValueError(f"MatMulNBits: A's last dimension must be K={k}, got {af.shape}")
+    m = af.size // k
+    y = np.empty(m * n, dtype=np.float32)
+    if m:
+        check(ctx.lib.mmnb_matmul_nbits(ctx.handle, pack.handle, ptr(af), m, ptr(y)))
+    return y.reshape(list(af.shape[:-1]) + [n])
+
+
+# ---------------------------------------------------- DynamicQuantizeLinear
+
+def op_dynamic_quantize_linear(x, ctx=None):
+    """Returns ``[y uint8 (x.shape), scale float32 (shape ()), zero_point int64
+    (shape ())]`` like opDynamicQuantizeLinear (onnx_ops.dart:2556-2583)."""
+    ctx = _ctx(ctx)
+    xf = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(xf.shape, dtype=np.uint8)
+    sc = ctypes.c_float()
+    zp = ctypes.c_int64()
+    check(ctx.lib.mmnb_dynamic_quantize_linear(ctx.handle, ptr(xf), xf.size, ptr(y),
+                                               ctypes.byref(sc), ctypes.byref(zp)))
+    return [y, np.array(sc.value, dtype=np.float32), np.array(zp.value, dtype=np.int64)]
+
+
+# ------------------------------------------------------------- MatMulInteger
+
+def _zp_array(zp):
+    if zp is None:
+        return None
+    return np.ascontiguousarray(np.asarray(zp).astype(np.int64).ravel())
+
+
+def pack_integer(b, b_zp, ctx=None):
+    """Upload a MatMulInteger right-hand operand ``[..., K, N]`` (uint8/int8)."""
+    ctx = _ctx(ctx)
+    b = np.ascontiguousarray(b)
+    if b.dtype not in (np.uint8, np.int8):
+        raise NotImplementedError(f"MatMulInteger: B must be uint8 or int8, got {b.dtype}")
+    if b.ndim < 2:
+        raise ValueError("MatMulInteger: B must have rank >= 2")
+    k, n = b.shape[-2], b.shape[-1]
+    batch = b.size // (k * n) if k * n else 1
+    z = _zp_array(b_zp)
+    h = ctypes.c_void_p()
+    check(ctx.lib.mmnb_pack_integer(ctx.handle, ptr(b.view(np.uint8)), int(b.dtype == np.int8),
+                                    batch, k, n, ptr(z), 0 if z is None else z.size,
+                                    ctypes.byref(h)))
+    return Pack(ctx, h, "integer", k=k, n=n, batch=batch, batch_shape=b.shape[:-2])
+
+
+def op_matmul_integer(a, b, a_zp, b_zp, ctx=None):
+    """``y = (A - aZp) . (B - bZp)`` exact, returned as int64 like the
+    reference (onnx_qlinear_ops.dart:30-79; int32 semantics)."""
+    ctx = _ctx(ctx)
+    a = np.ascontiguousarray(a)
+    if a.dtype not in (np.uint8, np.int8):
+        raise NotImplementedError(f"MatMulInteger: A must be uint8 or int8, got {a.dtype}")
+    b_arr = np.asarray(b)
+    if a.ndim < 2 or b_arr.ndim < 2:
+        raise ValueError("MatMulInteger: operands must have rank >= 2")
+    m, k = a.shape[-2], a.shape[-1]
+    if b_arr.shape[-2] != k:
+        raise ValueError("MatMulInteger inner dim mismatch")
+    n = b_arr.shape[-1]
+    keys = [b] + ([b_zp] if b_zp is not None and not np.isscalar(b_zp) else [])
+    extra = (ctx.device,) + ((int(b_zp),) if b_zp is not None and np.isscalar(b_zp) else ())
+    pack = _CACHE.get(keys, extra, lambda: pack_integer(b, b_zp, ctx))
+    a_batch = a.size // (m * k) if m * k else 1
+    batch = max(a_batch, pack.batch)
+    z = _zp_array(a_zp)
+    y = np.empty(batch * m * n, dtype=np.int32)
+    if m and n:
+        check(ctx.lib.mmnb_matmul_integer(ctx.handle, pack.handle, ptr(a.view(np.uint8)),
+                                          int(a.dtype == np.int8), a_batch, m, ptr(z),
+                                          0 if z is None else z.size, ptr(y)))
+    batch_shape = a.shape[:-2] if a_batch >= pack.batch else pack.batch_shape
+    return y.astype(np.int64).reshape(list(batch_shape) + [m, n])
+
+
+# --------------------------------------------------------- dispatch arms
+
+def dispatch(op_type, ins, attrs):
+    """The ``_dispatch`` arms for the three operators
+    (onnx_graph.dart:1561-1567, :1584-1596).  ``ins`` lists the node's
+    positional inputs (None for an empty name); returns the output list."""
+    def need(i):
+        if i >= len(ins) or ins[i] is None:
+            raise ValueError(f"{op_type}: missing input {i}")
+        return ins[i]
+
+    if op_type == "DynamicQuantizeLinear":
+        return op_dynamic_quantize_linear(need(0))
+    if op_type == "MatMulInteger":
+        return [op_matmul_integer(need(0), need(1), ins[2] if len(ins) > 2 else None,
+                                  ins[3] if len(ins) > 3 else None)]
+    if op_type == "MatMulNBits":
+        if len(ins) > 4:
+            raise NotImplementedError("MatMulNBits: g_idx/bias inputs not supported")
+        return [op_matmul_nbits(need(0), need(1), need(2), ins[3] if len(ins) > 3 else None,
+                                k=attrs["K"], n=attrs["N"], bits=attrs.get("bits", 4),
+                                block_size=attrs["block_size"])]
+    raise NotImplementedError(f"Unsupported op: {op_type}")
+
+
+def clear_pack_cache():
+    _CACHE.clear()

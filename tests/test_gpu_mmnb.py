@@ -1,0 +1,204 @@
+"""GPU parity of MatMulNBits (int4) against the CPU oracle, through the C ABI.
+
+Float bar: normwise relative error max|y_gpu - y_ref| / max|y_ref| <= 1e-5
+against the oracle (bit-faithful to the Dart native path), plus the
+accumulation bound |y_gpu - y_exact| <= gamma_{K+2} * sum|a||W| against an
+fp64 product (the GPU sums in a different order and applies each block's
+scale to a partial sum instead of rounding every weight, hence K+2).
+"""
+import numpy as np
+import pytest
+
+from oracle import refcpu
+from onnx_runtime_dart_amd import _lib, ops, synth
+from tests.helpers import fixture_float_ok, load_golden, node_arg, normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+U = 2.0 ** -24
+THREADS = min(16, refcpu.host_threads())
+
+
+def gamma(k):
+    return k * U / (1 - k * U)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return _lib.default_context()
+
+
+def run_gpu(ctx, p):
+    return ops.op_matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k=p.k, n=p.n, bits=4,
+                               block_size=p.block, ctx=ctx)
+
+
+def oracle(p, rows=None):
+    a = p.a if rows is None else p.a[rows]
+    return refcpu.matmul_nbits(a, p.b_q, p.scales, p.zero_points, p.k, p.n, 4, p.block,
+                               threads=THREADS)
+
+
+def check_bound(p, y, rows=None):
+    a = p.a if rows is None else p.a[rows]
+    y64, absdot = refcpu.matmul_nbits_f64(a, p.b_q, p.scales, p.zero_points, p.k, p.n,
+                                          p.block)
+    err = np.abs(y.astype(np.float64) - y64)
+    assert np.all(err <= gamma(p.k + 2) * absdot + 1e-30), float(np.max(err / (absdot + 1e-300)))
+
+
+@pytest.mark.parametrize("case", ["matmulnbits_basic", "matmulnbits_zeropoints",
+                                  "matmulnbits_partial_block"])
+def test_golden_fixtures_through_dispatch(ctx, case):
+    d, vals, exp = load_golden(case)
+    ins = [node_arg(d, vals, i) for i in range(len(d["node_inputs"]))]
+    y = ops.dispatch("MatMulNBits", ins, d["attrs"])[0]
+    assert y.shape == exp["out0"].shape and y.dtype == np.float32
+    ok, max_abs, cos = fixture_float_ok(y, exp["out0"])
+    assert ok, (max_abs, cos)
+    at = d["attrs"]
+    ref = refcpu.matmul_nbits(ins[0], ins[1], ins[2], ins[3] if len(ins) > 3 else None,
+                              at["K"], at["N"], 4, at["block_size"])
+    assert normwise_rel_err(y, ref) <= TOL
+
+
+def test_single_node_config(ctx):
+    # M=1, K=N=1024, block 32, packed zero points
+    p = synth.mmnb_problem(1, 1024, 1024, 32, True, seed=0)
+    y = run_gpu(ctx, p)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("kn", synth.DECODE_PROJECTIONS)
+def test_decode_sweep(ctx, m, kn):
+    k, n = kn
+    p = synth.mmnb_problem(m, k, n, 128, False, seed=1, scale_range=(0.002, 0.02))
+    y = run_gpu(ctx, p)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+
+
+@pytest.mark.parametrize("block,zp", [(128, False), (32, True)])
+def test_headline_gemv_4096(ctx, block, zp):
+    p = synth.mmnb_problem(1, 4096, 4096, block, zp, seed=7)
+    y = run_gpu(ctx, p)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+
+
+@pytest.mark.parametrize("m,n,block", [(128, 4096, 32), (128, 4096, 128)])
+def test_prefill_full_oracle(ctx, m, n, block):
+    p = synth.mmnb_problem(m, 4096, n, block, True, seed=2, outlier_frac=0.01)
+    y = run_gpu(ctx, p)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+
+
+@pytest.mark.parametrize("m,n,block", [(512, 4096, 32), (512, 14336, 128),
+                                       (2048, 4096, 128), (2048, 14336, 32)])
+def test_prefill_full_size_row_sample(ctx, m, n, block):
+    # Rows are independent: the oracle on a sample of rows is the exact
+    # reference for those rows of the full-size product.
+    p = synth.mmnb_problem(m, 4096, n, block, True, seed=2, outlier_frac=0.01)
+    y = run_gpu(ctx, p)
+    assert np.all(np.isfinite(y))
+    rows = np.array([0, 1, m // 3, m // 2 + 1, m - 2, m - 1])
+    ref = oracle(p, rows)
+    assert normwise_rel_err(y[rows], ref) <= TOL
+    check_bound(p, y[rows], rows)
+
+
+@pytest.mark.parametrize("m,k,n,block,zp", [
+    (1, 40, 5, 32, False),      # partial block, n % 4 != 0 (double tail in the oracle)
+    (2, 40, 5, 32, True),
+    (3, 200, 37, 64, True),
+    (1, 16, 3, 16, True),       # block 16
+    (5, 256, 70, 256, False),   # block 256, K == block
+    (9, 96, 33, 32, True),      # GEMM path, M not a multiple of the tile
+    (65, 1000, 130, 128, True),  # GEMM path, K not a multiple of 64
+    (8, 3000, 17, 64, False),
+    (1, 4096, 1, 128, True),    # single column
+])
+def test_edge_shapes(ctx, m, k, n, block, zp):
+    p = synth.mmnb_problem(m, k, n, block, zp, seed=11 + m + n)
+    y = run_gpu(ctx, p)
+    assert y.shape == (m, n)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+
+
+def test_batched_activation_shape(ctx):
+    p = synth.mmnb_problem(6, 256, 48, 32, True, seed=5)
+    a3 = p.a.reshape(2, 3, 256)
+    y = ops.op_matmul_nbits(a3, p.b_q, p.scales, p.zero_points, k=256, n=48, bits=4,
+                            block_size=32, ctx=ctx)
+    assert y.shape == (2, 3, 48)
+    assert normwise_rel_err(y.reshape(6, 48), oracle(p)) <= TOL
+
+
+def test_zero_rows_and_tiny_magnitudes(ctx):
+    p = synth.mmnb_problem(12, 512, 64, 32, True, seed=9)
+    p.a[3] = 0.0
+    p.a[5] *= np.float32(1e-30)
+    p.a[7] *= np.float32(1e20)
+    y = run_gpu(ctx, p)
+    ref = oracle(p)
+    assert np.all(y[3] == 0.0)
+    for r in range(12):
+        if r == 3:
+            continue
+        assert normwise_rel_err(y[r], ref[r]) <= TOL, r
+
+
+def test_all_zero_nibbles_closed_form(ctx):
+    # q = 0, zero point 8 -> W = -8 * scale: y = -8 * sum_k a_k scale[n, blk(k)]
+    k, n, bs = 256, 16, 64
+    nb = k // bs
+    b = np.zeros((n, nb, bs // 2), np.uint8)
+    s = np.random.default_rng(1).uniform(0.1, 1, (n, nb)).astype(np.float32)
+    a = np.random.default_rng(2).standard_normal((3, k)).astype(np.float32)
+    y = ops.op_matmul_nbits(a, b, s, None, k=k, n=n, bits=4, block_size=bs, ctx=ctx)
+    want = -8.0 * (a.astype(np.float64).reshape(3, nb, bs).sum(-1) @ s.T.astype(np.float64))
+    assert normwise_rel_err(y, want) <= TOL
+
+
+def test_device_entry_point_matches_host_entry_point(ctx):
+    # K a multiple of 64 (aligned path) and not (masked path)
+    for (m, k, n, bs) in [(1, 1024, 256, 32), (4, 1000, 96, 8 * 16), (24, 320, 200, 64)]:
+        p = synth.mmnb_problem(m, k, n, bs, True, seed=k)
+        pack = ops.pack_nbits(p.b_q, p.scales, p.zero_points, k=k, n=n, bits=4,
+                              block_size=bs, ctx=ctx)
+        da = ctx.to_device(p.a)
+        dy = ctx.alloc(m * n * 4)
+        _lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, pack.handle, da.ptr, m, dy.ptr))
+        ctx.synchronize()
+        y_dev = dy.numpy(np.float32, (m, n))
+        y_host = run_gpu(ctx, p)
+        np.testing.assert_array_equal(y_dev, y_host)
+        da.free()
+        dy.free()
+        pack.free()
+
+
+def test_pack_is_cached_and_resident(ctx):
+    p = synth.mmnb_problem(1, 512, 128, 32, True, seed=3)
+    ops.clear_pack_cache()
+    y1 = run_gpu(ctx, p)
+    y2 = run_gpu(ctx, p)
+    np.testing.assert_array_equal(y1, y2)  # deterministic, same resident pack
+    assert len(ops._CACHE._packs) == 1
+
+
+def test_argument_errors(ctx):
+    p = synth.mmnb_problem(1, 64, 8, 32, False, seed=3)
+    with pytest.raises(ValueError):  # B too short
+        ops.pack_nbits(p.b_q[:4], p.scales, None, k=64, n=8, bits=4, block_size=32, ctx=ctx)
+    with pytest.raises(ValueError):  # scales too short
+        ops.pack_nbits(p.b_q, p.scales[:2], None, k=64, n=8, bits=4, block_size=32, ctx=ctx)
+    with pytest.raises(NotImplementedError):  # block size not a power of two
+        ops.pack_nbits(p.b_q, p.scales, None, k=64, n=8, bits=4, block_size=48, ctx=ctx)
+    with pytest.raises(ValueError):  # A's last dim != K
+        ops.op_matmul_nbits(np.zeros((1, 63), np.float32), p.b_q, p.scales, None, k=64, n=8,
+                            bits=4, block_size=32, ctx=ctx)
