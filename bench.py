@@ -1,0 +1,319 @@
+#!/usr/bin/env python3
+"""Benchmark of the int4 MatMulNBits / int8 dynamic-quant path on one MI355X.
+
+Headline (the JSON line's "value"): the decode-shape MatMulNBits GEMV,
+M=1, K=N=4096, block 128, symmetric, in GB/s of algorithmic traffic
+(K*N/2 + N*ceil(K/bs)*4 + M*K*4 + M*N*4 bytes per call).  One step = one
+MatMulNBits call on one weight pack; the packs rotate over > 300 MB of
+distinct weights (more than the 256 MB Infinity Cache) so every call streams
+its weights from HBM.  The timed region replays a HIP graph of the rotation
+(so host launch overhead does not starve the GPU), bracketed by device
+synchronisation and HIP events on the library's stream.
+
+Also reported (extra keys on the same line):
+  roofline      the GEMV kernel: achieved GB/s from its own dispatch events
+                (kernel execution time, what rocprofv3 kernel-trace reports)
+  cpu_baseline  the oracle (a C restatement of the reference's Dart
+                algorithm) on the host, single thread, bounded sample
+  gemm          prefill GEMM M=512, K=N=4096, block 32 with zero points:
+                TFLOP/s and its MFMA roofline
+  int8          DynamicQuantizeLinear [512,1024] -> MatMulInteger
+                [1024,3072] -> fp32 rescale
+  decode_sweep  M in {1,4,8} x the four decode projections, block 128
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
+INT8_PEAK_TOPS = 5000.0
+ROTATE_BYTES = 320 * 1024 * 1024
+
+
+def mmnb_bytes(m, k, n, bs, zp):
+    nb = (k + bs - 1) // bs
+    b = k * n // 2 + n * nb * 4 + m * k * 4 + m * n * 4
+    if zp:
+        b += n * ((nb + 1) // 2)
+    return b
+
+
+def make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed):
+    packs = []
+    for i in range(count):
+        b_q, scales, zps = synth.mmnb_weights(k, n, bs, zp, seed * 100 + i,
+                                              (0.002, 0.02) if not zp else (0.005, 0.02))
+        packs.append(ops.pack_nbits(b_q, scales, zps, k=k, n=n, bits=4, block_size=bs,
+                                    ctx=ctx))
+    return packs
+
+
+def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup):
+    """Whole-job time per call (graph replay) and kernel durations per name."""
+    P = len(packs)
+
+    def issue_round():
+        for p in packs:
+            lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, p.handle, da.ptr, m, dy.ptr))
+
+    # warmup (also sizes any scratch before capture)
+    for _ in range(max(1, warmup // P)):
+        issue_round()
+    ctx.synchronize()
+    ctx.graph_begin()
+    issue_round()
+    g = ctx.graph_end()
+    reps = max(1, steps // P)
+    for _ in range(max(1, warmup // P)):
+        ctx.graph_launch(g)
+    ctx.synchronize()
+    ctx.event_record(0)
+    for _ in range(reps):
+        ctx.graph_launch(g)
+    ctx.event_record(1)
+    ctx.synchronize()
+    total_ms = ctx.event_elapsed_ms(0, 1)
+    ctx.graph_destroy(g)
+    n_steps = reps * P
+    # kernel durations from the dispatches themselves
+    nk = min(n_steps, 4096)
+    ctx.kernel_timing(True, max_launches=4 * nk)
+    done = 0
+    while done < nk:
+        issue_round()
+        done += P
+    kt = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    return n_steps, total_ms / n_steps, kt
+
+
+def kernel_avg_ms(kt, name):
+    c, tot, lo, hi = kt[name]
+    return tot / c
+
+
+def bench_gemv(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup, seed=1):
+    per_pack = mmnb_bytes(m, k, n, bs, zp)
+    count = max(2, int(np.ceil(ROTATE_BYTES / (k * n // 2 + n * ((k + bs - 1) // bs) * 4))))
+    packs = make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed)
+    a = synth.activations(m, k, seed)
+    da = ctx.to_device(a)
+    dy = ctx.alloc(m * n * 4)
+    n_steps, ms_step, kt = time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup)
+    kname = "k_gemv_valu" if "k_gemv_valu" in kt else sorted(kt)[0]
+    kms = kernel_avg_ms(kt, kname)
+    res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "packs": count,
+           "bytes_per_call": per_pack, "steps": n_steps, "ms_per_call": ms_step,
+           "gbs": per_pack / (ms_step * 1e-3) / 1e9, "kernel": kname,
+           "kernel_ms": kms, "kernel_gbs": per_pack / (kms * 1e-3) / 1e9,
+           "kernels": {k_: {"count": v[0], "avg_us": v[1] / v[0] * 1e3,
+                            "min_us": v[2] * 1e3, "max_us": v[3] * 1e3}
+                       for k_, v in kt.items()}}
+    da.free()
+    dy.free()
+    for p in packs:
+        p.free()
+    return res
+
+
+def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
+    p = synth.mmnb_problem(m, k, n, bs, zp, seed=2, outlier_frac=0.01)
+    pack = ops.pack_nbits(p.b_q, p.scales, p.zero_points, k=k, n=n, bits=4, block_size=bs,
+                          ctx=ctx)
+    da = ctx.to_device(p.a)
+    dy = ctx.alloc(m * n * 4)
+    n_steps, ms_step, kt = time_mmnb(ctx, lib, [pack], da, m, dy, steps, warmup)
+    flops = 2.0 * m * k * n
+    gk = kernel_avg_ms(kt, "k_gemm_mfma")
+    pk = kernel_avg_ms(kt, "k_prep_rowblock") if "k_prep_rowblock" in kt else 0.0
+    achieved = flops / (gk * 1e-3) / 1e12
+    res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "steps": n_steps,
+           "ms_per_call": ms_step, "tflops": flops / (ms_step * 1e-3) / 1e12,
+           "gemm_kernel_us": gk * 1e3, "prep_kernel_us": pk * 1e3,
+           "roofline": {"bound": "mfma", "achieved": achieved,
+                        "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
+                        "mfma_passes": 2,
+                        "mfma_utilisation": 2 * achieved / MFMA_FP16_PEAK_TFLOPS,
+                        "vs_fp32_mfma_peak": achieved / MFMA_FP32_PEAK_TFLOPS,
+                        "traffic": None}}
+    da.free()
+    dy.free()
+    pack.free()
+    return res
+
+
+def bench_int8(ctx, lib, ops, synth, steps, warmup):
+    m, k, n = 512, 1024, 3072
+    x, b = synth.int8_chain_problem(m, k, n)
+    pack = ops.pack_integer(b, np.array(0, np.int8), ctx=ctx)
+    bscale = np.array([0.01], np.float32)
+    dx, dbs = ctx.to_device(x), ctx.to_device(bscale)
+    daq, dsc, dzp = ctx.alloc(m * k), ctx.alloc(4), ctx.alloc(4)
+    dacc, dy = ctx.alloc(m * n * 4), ctx.alloc(m * n * 4)
+
+    def call():
+        lib.check(ctx.lib.mmnb_dynamic_matmul_dev(ctx.handle, pack.handle, dx.ptr, m, dbs.ptr,
+                                                  1, daq.ptr, dsc.ptr, dzp.ptr, dacc.ptr,
+                                                  dy.ptr))
+    for _ in range(warmup):
+        call()
+    ctx.synchronize()
+    ctx.graph_begin()
+    call()
+    g = ctx.graph_end()
+    ctx.synchronize()
+    ctx.event_record(0)
+    for _ in range(steps):
+        ctx.graph_launch(g)
+    ctx.event_record(1)
+    ctx.synchronize()
+    ms = ctx.event_elapsed_ms(0, 1) / steps
+    ctx.graph_destroy(g)
+    ctx.kernel_timing(True, max_launches=4 * min(steps, 1000))
+    for _ in range(min(steps, 1000)):
+        call()
+    kt = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    mmi_bytes = m * k + k * n + 4 * m * n * 2  # A u8, B i8, int32 acc + fp32 y
+    dql_bytes = 4 * m * k + m * k
+    mk = kernel_avg_ms(kt, "k_mmi_mfma")
+    res = {"m": m, "k": k, "n": n, "ms_per_chain": ms,
+           "kernels": {k_: {"count": v[0], "avg_us": v[1] / v[0] * 1e3}
+                       for k_, v in kt.items()},
+           "mmi_roofline": {"bound": "hbm", "achieved": mmi_bytes / (mk * 1e-3) / 1e9,
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": mmi_bytes / (mk * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                            "tops": 2.0 * m * k * n / (mk * 1e-3) / 1e12},
+           "dql_gbs": dql_bytes / ((kernel_avg_ms(kt, "k_dql_minmax") +
+                                    kernel_avg_ms(kt, "k_dql_quant")) * 1e-3) / 1e9}
+    for bf in (dx, dbs, daq, dsc, dzp, dacc, dy):
+        bf.free()
+    pack.free()
+    return res
+
+
+def cpu_baseline(synth, m, k, n, bs, zp, budget_s):
+    """The oracle (C restatement of the reference's Dart MatMulNBits:
+    dequantise to a fresh K x N fp32 buffer, then the sequential-k fp32
+    GEMV) timed on this host, single thread: the reference runs this op on
+    one isolate (its pool never takes MatMulNBits)."""
+    from oracle import refcpu
+
+    p = synth.mmnb_problem(m, k, n, bs, zp, seed=1, scale_range=(0.002, 0.02))
+    refcpu.matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k, n, 4, bs)  # warm
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        refcpu.matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k, n, 4, bs)
+        times.append(time.perf_counter() - t0)
+    per = mmnb_bytes(m, k, n, bs, zp)
+    mean = float(np.mean(times))
+    threads = refcpu.host_threads()
+    # column-sliced multi-thread variant (the pool's partition), for context
+    tmt = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        refcpu.matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k, n, 4, bs,
+                            threads=threads)
+        tmt.append(time.perf_counter() - t0)
+    return {"value": per / mean / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"MatMulNBits M={m} K={k} N={n} block {bs} "
+                      f"{'with' if zp else 'no'} zero points, {len(times)} calls "
+                      f"({sum(times):.1f} s), mean {mean * 1e3:.1f} ms/call, "
+                      f"min {min(times) * 1e3:.1f} ms",
+            "multi_thread": {"value": per / float(np.min(tmt)) / 1e9, "cores": threads,
+                             "ms_per_call": float(np.min(tmt)) * 1e3}}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2160)
+    ap.add_argument("--warmup", type=int, default=216)
+    ap.add_argument("--quick", action="store_true", help="headline only, no extras")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build runs the kernel on a single "
+              "GPU and has no multi-GPU path; run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from onnx_runtime_dart_amd import _lib as lib, ops, synth
+
+    ctx = lib.default_context()
+    info = ctx.info()
+    print(f"# device {info}", file=sys.stderr, flush=True)
+
+    head = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 128, False, args.steps,
+                      args.warmup)
+    print(f"# headline GEMV: {head['gbs']:.0f} GB/s whole-job, kernel "
+          f"{head['kernel_gbs']:.0f} GB/s ({head['kernel_ms'] * 1e3:.2f} us)",
+          file=sys.stderr, flush=True)
+    out = {
+        "metric": "int4 MatMulNBits GB/s (M=1) & TFLOPS (M=512), % of HBM/MFMA roofline",
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_call"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights (u4 packed), fp32 activations/accumulate",
+        "data": "synthetic (seeded), weights rotated over >300 MB",
+        "config": {"workload": "MatMulNBits decode GEMV M=1 K=4096 N=4096 block 128 "
+                               "symmetric (one call per step)",
+                   "m": 1, "k": 4096, "n": 4096, "block_size": 128, "zero_points": False,
+                   "packs_rotated": head["packs"], "bytes_per_step": head["bytes_per_call"],
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": head["kernel"],
+                     "kernel_avg_us": round(head["kernel_ms"] * 1e3, 3)},
+    }
+    if not args.quick:
+        try:
+            out["gemv_bs32_zp"] = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 32, True,
+                                             args.steps, args.warmup, seed=3)
+            print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['kernel_gbs']:.0f} GB/s kernel",
+                  file=sys.stderr, flush=True)
+            out["gemm"] = bench_gemm(ctx, lib, ops, synth, 512, 4096, 4096, 32, True,
+                                     200, 20)
+            print(f"# GEMM M=512: {out['gemm']['tflops']:.1f} TFLOP/s op, kernel "
+                  f"{out['gemm']['roofline']['achieved']:.1f}", file=sys.stderr, flush=True)
+            out["int8"] = bench_int8(ctx, lib, ops, synth, 500, 50)
+            print(f"# int8 chain: {out['int8']['ms_per_chain'] * 1e3:.1f} us",
+                  file=sys.stderr, flush=True)
+            sweep = []
+            for m in (1, 4, 8):
+                for (k, n) in synth.DECODE_PROJECTIONS:
+                    r = bench_gemv(ctx, lib, ops, synth, m, k, n, 128, False, 1000, 100)
+                    sweep.append({kk: r[kk] for kk in ("m", "k", "n", "gbs", "kernel_gbs",
+                                                       "kernel_ms", "bytes_per_call")})
+            out["decode_sweep"] = sweep
+            print("# decode sweep done", file=sys.stderr, flush=True)
+        except Exception as e:  # extras must not hide the headline
+            out["extras_error"] = repr(e)
+    out["cpu_baseline"] = cpu_baseline(synth, 1, 4096, 4096, 128, False,
+                                       args.cpu_budget if not args.quick else 3.0)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

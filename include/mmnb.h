@@ -203,6 +203,31 @@ int mmnb_event_record(mmnb_ctx *ctx, int slot);
 int mmnb_event_elapsed_ms(mmnb_ctx *ctx, int slot_start, int slot_end,
                           float *ms);
 
+/* Kernel timing mode.  While enabled, every kernel libmmnb launches records
+ * start/stop events taken from its own dispatch (hipExtLaunchKernelGGL), so
+ * the durations are the kernels' execution times, the quantity a
+ * kernel-trace profiler reports.  Enabling (again) resets the record; at
+ * most max_launches launches are recorded. */
+int mmnb_kernel_timing(mmnb_ctx *ctx, int enable, int max_launches);
+
+/* Sum, count, min and max of the recorded durations of kernel `kernel_id`
+ * (see mmnb_kernel_name); waits for the recorded launches to finish. */
+int mmnb_kernel_timing_read(mmnb_ctx *ctx, int kernel_id, int64_t *count,
+                            double *total_ms, double *min_ms, double *max_ms);
+
+/* Name of kernel id 0.. (NULL past the last id). */
+const char *mmnb_kernel_name(int kernel_id);
+
+/* HIP graph capture of the context stream: between begin and end, the
+ * "_dev" entry points are recorded instead of run (host entry points are
+ * rejected).  Device scratch must already be large enough, i.e. each
+ * captured call must have run once before.  The returned executable graph
+ * replays the recorded work with one launch. */
+int mmnb_graph_begin(mmnb_ctx *ctx);
+int mmnb_graph_end(mmnb_ctx *ctx, void **graph_exec);
+int mmnb_graph_launch(mmnb_ctx *ctx, void *graph_exec);
+int mmnb_graph_destroy(mmnb_ctx *ctx, void *graph_exec);
+
 #ifdef __cplusplus
 }
 #endif

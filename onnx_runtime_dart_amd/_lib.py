@@ -52,6 +52,14 @@ SIGNATURES = {
     "mmnb_synchronize": (_int, [_vp]),
     "mmnb_event_record": (_int, [_vp, _int]),
     "mmnb_event_elapsed_ms": (_int, [_vp, _int, _int, _P(ctypes.c_float)]),
+    "mmnb_kernel_timing": (_int, [_vp, _int, _int]),
+    "mmnb_kernel_timing_read": (_int, [_vp, _int, _P(_i64), _P(ctypes.c_double),
+                                       _P(ctypes.c_double), _P(ctypes.c_double)]),
+    "mmnb_kernel_name": (ctypes.c_char_p, [_int]),
+    "mmnb_graph_begin": (_int, [_vp]),
+    "mmnb_graph_end": (_int, [_vp, _P(_vp)]),
+    "mmnb_graph_launch": (_int, [_vp, _vp]),
+    "mmnb_graph_destroy": (_int, [_vp, _vp]),
 }
 
 _lib = None
@@ -146,6 +154,41 @@ class Context:
 
     def event_record(self, slot):
         check(self.lib.mmnb_event_record(self.handle, int(slot)))
+
+    def kernel_timing(self, enable, max_launches=4096):
+        check(self.lib.mmnb_kernel_timing(self.handle, int(bool(enable)), int(max_launches)))
+
+    def kernel_timing_read(self):
+        """{kernel name: (count, total_ms, min_ms, max_ms)} of recorded launches."""
+        out = {}
+        kid = 0
+        while True:
+            name = self.lib.mmnb_kernel_name(kid)
+            if name is None:
+                break
+            c = ctypes.c_int64()
+            t, lo, hi = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+            check(self.lib.mmnb_kernel_timing_read(self.handle, kid, ctypes.byref(c),
+                                                   ctypes.byref(t), ctypes.byref(lo),
+                                                   ctypes.byref(hi)))
+            if c.value:
+                out[name.decode()] = (c.value, t.value, lo.value, hi.value)
+            kid += 1
+        return out
+
+    def graph_begin(self):
+        check(self.lib.mmnb_graph_begin(self.handle))
+
+    def graph_end(self):
+        g = ctypes.c_void_p()
+        check(self.lib.mmnb_graph_end(self.handle, ctypes.byref(g)))
+        return g
+
+    def graph_launch(self, g):
+        check(self.lib.mmnb_graph_launch(self.handle, g))
+
+    def graph_destroy(self, g):
+        check(self.lib.mmnb_graph_destroy(self.handle, g))
 
     def event_elapsed_ms(self, s0, s1):
         ms = ctypes.c_float()

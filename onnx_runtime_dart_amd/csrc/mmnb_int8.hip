@@ -155,16 +155,14 @@ int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *
   int64_t blocks = (n + (int64_t)kDqlThreads * 32 - 1) / ((int64_t)kDqlThreads * 32);
   if (blocks < 1) blocks = 1;
   if (blocks > kDqlMaxBlocks) blocks = kDqlMaxBlocks;
-  hipLaunchKernelGGL(k_dql_minmax, dim3((unsigned)blocks), dim3(kDqlThreads), 0, ctx->stream,
-                     d_x, n, (float2 *)d_part);
-  MMNB_HIP(hipGetLastError());
+  if ((rc = launch(ctx, kKernDqlMinmax, k_dql_minmax, dim3((unsigned)blocks), dim3(kDqlThreads),
+                    0, d_x, n, (float2 *)d_part)))
+    return rc;
   int64_t qblocks = (n + (int64_t)kDqlThreads * 16 - 1) / ((int64_t)kDqlThreads * 16);
   if (qblocks < 1) qblocks = 1;
   if (qblocks > 4096) qblocks = 4096;
-  hipLaunchKernelGGL(k_dql_quant, dim3((unsigned)qblocks), dim3(kDqlThreads), 0, ctx->stream,
-                     d_x, n, (const float2 *)d_part, (int)blocks, d_y, d_scale, d_zp);
-  MMNB_HIP(hipGetLastError());
-  return MMNB_OK;
+  return launch(ctx, kKernDqlQuant, k_dql_quant, dim3((unsigned)qblocks), dim3(kDqlThreads), 0,
+                d_x, n, (const float2 *)d_part, (int)blocks, d_y, d_scale, d_zp);
 }
 
 // ---------------------------------------------------------------------------
@@ -219,14 +217,11 @@ int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int64_t
                       int64_t bzp_len, int8_t *d_bt, int32_t *d_colsum, int32_t *d_ecol) {
   const int threads = 256;
   const int64_t tot = batch * n;
-  hipLaunchKernelGGL(k_prep_int_b, dim3((unsigned)((tot + threads - 1) / threads)),
-                     dim3(threads), 0, ctx->stream, d_src, b_signed, batch, k, n, kpad, d_bt,
-                     d_colsum);
-  MMNB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(k_prep_int_e, dim3((unsigned)((n + threads - 1) / threads)),
-                     dim3(threads), 0, ctx->stream, b_signed, n, d_bzp, bzp_len, d_ecol);
-  MMNB_HIP(hipGetLastError());
-  return MMNB_OK;
+  int rc = launch(ctx, kKernPrepIntB, k_prep_int_b, dim3((unsigned)((tot + threads - 1) / threads)),
+                  dim3(threads), 0, d_src, b_signed, batch, k, n, kpad, d_bt, d_colsum);
+  if (rc) return rc;
+  return launch(ctx, kKernPrepIntB, k_prep_int_e, dim3((unsigned)((n + threads - 1) / threads)),
+                dim3(threads), 0, b_signed, n, d_bzp, bzp_len, d_ecol);
 }
 
 typedef int int4v __attribute__((ext_vector_type(4)));
@@ -366,13 +361,11 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
   if (!d_y && !d_yf) return fail(MMNB_ERR_ARG, "MatMulInteger: no output");
   const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
-  hipLaunchKernelGGL(k_mmi_mfma, grid, dim3(256), 0, ctx->stream, (const uint8_t *)d_a,
-                     a_signed, a_batch == 1 ? (int64_t)0 : m * k, m, k, p->d_bt,
-                     p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, p->d_colsum,
-                     p->batch == 1 ? (int64_t)0 : n, p->d_ecol, n, d_azp, azp_len, d_y,
-                     d_a_scale, d_b_scale, b_scale_len, d_yf, fast);
-  MMNB_HIP(hipGetLastError());
-  return MMNB_OK;
+  return launch(ctx, kKernMmi, k_mmi_mfma, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
+                a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
+                p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, (const int32_t *)p->d_colsum,
+                p->batch == 1 ? (int64_t)0 : n, (const int32_t *)p->d_ecol, n, d_azp, azp_len,
+                d_y, d_a_scale, d_b_scale, b_scale_len, d_yf, fast);
 }
 
 }  // namespace mmnb

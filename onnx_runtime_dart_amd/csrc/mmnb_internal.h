@@ -1,9 +1,11 @@
 // Internal declarations shared by the libmmnb translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <vector>
 #include <mutex>
 #include <string>
 
@@ -57,6 +59,14 @@ struct mmnb_ctx {
   //  (fp16 hi/lo), 3: small reductions, 4: misc.
   mmnb::Scratch scratch[6];
   int live_packs = 0;
+  // Kernel timing mode: launches go through hipExtLaunchKernelGGL with a
+  // start/stop event pair taken from the dispatch itself.
+  bool timing = false;
+  std::vector<hipEvent_t> tev;   // 2 per slot
+  std::vector<int> tkid;         // kernel id per used slot
+  size_t tused = 0;
+  // Stream capture in progress (no synchronisation or allocation allowed).
+  bool capturing = false;
 };
 
 struct mmnb_pack {
@@ -89,6 +99,37 @@ int check_hip(hipError_t e, const char *what);
     hipError_t _e = (call);                                   \
     if (_e != hipSuccess) return ::mmnb::check_hip(_e, #call); \
   } while (0)
+
+// Kernel ids reported by the timing mode (see mmnb_kernel_name).
+enum KernelId {
+  kKernGemv = 0,
+  kKernPrep = 1,
+  kKernGemm = 2,
+  kKernDqlMinmax = 3,
+  kKernDqlQuant = 4,
+  kKernMmi = 5,
+  kKernRepack = 6,
+  kKernPrepIntB = 7,
+  kKernCount = 8
+};
+
+// Launch `kern` on the context stream; in timing mode the dispatch records
+// its own start/stop events.
+template <typename... KArgs, typename... Args>
+int launch(mmnb_ctx *ctx, int kid, void (*kern)(KArgs...), dim3 grid, dim3 block,
+           size_t shmem, Args... args) {
+  if (ctx->timing && ctx->tused < ctx->tkid.size()) {
+    const size_t i = ctx->tused++;
+    ctx->tkid[i] = kid;
+    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)shmem, ctx->stream, ctx->tev[2 * i],
+                          ctx->tev[2 * i + 1], 0, static_cast<KArgs>(args)...);
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, shmem, ctx->stream, static_cast<KArgs>(args)...);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return check_hip(e, "kernel launch");
+  return 0;
+}
 
 // Grow-only device scratch owned by the context.
 int scratch_get(mmnb_ctx *ctx, int slot, size_t bytes, void **out);

@@ -64,10 +64,8 @@ int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n, int64_t
   const int64_t total = n * segs;
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(k_repack_nbits, dim3((unsigned)blocks), dim3(threads), 0, ctx->stream,
-                     d_src, n, src_col, dst_col, k, d_dst);
-  MMNB_HIP(hipGetLastError());
-  return MMNB_OK;
+  return launch(ctx, kKernRepack, k_repack_nbits, dim3((unsigned)blocks), dim3(threads), 0,
+                d_src, n, src_col, dst_col, k, d_dst);
 }
 
 // ---------------------------------------------------------------------------
@@ -193,22 +191,21 @@ __global__ __launch_bounds__(256) void k_gemv_valu(
 }
 
 template <int M>
-static void launch_gemv_m(int u, dim3 grid, hipStream_t st, const float *A, int64_t lda,
-                          const mmnb_pack *p, float *Y, int chunks, int lpc_log2,
-                          int fast, int bs_log2) {
+static int launch_gemv_m(mmnb_ctx *ctx, int u, dim3 grid, const float *A, int64_t lda,
+                         const mmnb_pack *p, float *Y, int chunks, int lpc_log2, int fast,
+                         int bs_log2) {
   const int nb = (int)p->n_blocks, K = (int)p->k, N = (int)p->n;
   if (u == 4)
-    hipLaunchKernelGGL((k_gemv_valu<M, 4>), grid, dim3(256), 0, st, A, lda, p->d_w,
-                       p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks,
-                       lpc_log2, fast);
-  else if (u == 2)
-    hipLaunchKernelGGL((k_gemv_valu<M, 2>), grid, dim3(256), 0, st, A, lda, p->d_w,
-                       p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks,
-                       lpc_log2, fast);
-  else
-    hipLaunchKernelGGL((k_gemv_valu<M, 1>), grid, dim3(256), 0, st, A, lda, p->d_w,
-                       p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks,
-                       lpc_log2, fast);
+    return launch(ctx, kKernGemv, k_gemv_valu<M, 4>, grid, dim3(256), 0, A, lda, p->d_w,
+                  p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks, lpc_log2,
+                  fast);
+  if (u == 2)
+    return launch(ctx, kKernGemv, k_gemv_valu<M, 2>, grid, dim3(256), 0, A, lda, p->d_w,
+                  p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks, lpc_log2,
+                  fast);
+  return launch(ctx, kKernGemv, k_gemv_valu<M, 1>, grid, dim3(256), 0, A, lda, p->d_w,
+                p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks, lpc_log2,
+                fast);
 }
 
 static int ilog2(int64_t v) {
@@ -237,17 +234,15 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   const int bs_log2 = ilog2(p->block);
   const int lpc_log2 = ilog2(lpc);
   switch (m) {
-    case 1: launch_gemv_m<1>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    case 2: launch_gemv_m<2>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    case 3: launch_gemv_m<3>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    case 4: launch_gemv_m<4>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    case 5: launch_gemv_m<5>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    case 6: launch_gemv_m<6>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    case 7: launch_gemv_m<7>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
-    default: launch_gemv_m<8>(u, grid, ctx->stream, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2); break;
+    case 1: return launch_gemv_m<1>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 2: return launch_gemv_m<2>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 3: return launch_gemv_m<3>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 4: return launch_gemv_m<4>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 5: return launch_gemv_m<5>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 6: return launch_gemv_m<6>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 7: return launch_gemv_m<7>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    default: return launch_gemv_m<8>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
   }
-  MMNB_HIP(hipGetLastError());
-  return MMNB_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -452,15 +447,13 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   int rc;
   if ((rc = scratch_get(ctx, 2, ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)mpad * 4, &d_exp))) return rc;
-  hipLaunchKernelGGL(k_prep_rowblock, dim3((unsigned)rblocks), dim3(256), 0, ctx->stream,
-                     d_a, lda, m, p->k, segs, (uint4 *)d_ap, (int *)d_exp);
-  MMNB_HIP(hipGetLastError());
+  if ((rc = launch(ctx, kKernPrep, k_prep_rowblock, dim3((unsigned)rblocks), dim3(256), 0, d_a,
+                    lda, m, p->k, segs, (uint4 *)d_ap, (int *)d_exp)))
+    return rc;
   const dim3 grid((unsigned)((p->n + kGemmBN - 1) / kGemmBN), (unsigned)(mpad / kGemmBM));
-  hipLaunchKernelGGL(k_gemm_mfma, grid, dim3(256), 0, ctx->stream, (const uint4 *)d_ap,
-                     (const int *)d_exp, segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,
-                     p->n_blocks, p->block, m, p->n, d_y);
-  MMNB_HIP(hipGetLastError());
-  return MMNB_OK;
+  return launch(ctx, kKernGemm, k_gemm_mfma, grid, dim3(256), 0, (const uint4 *)d_ap,
+                (const int *)d_exp, segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,
+                p->n_blocks, p->block, m, p->n, d_y);
 }
 
 int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,

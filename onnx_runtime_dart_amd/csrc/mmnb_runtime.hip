@@ -31,6 +31,10 @@ int scratch_get(mmnb_ctx *ctx, int slot, size_t bytes, void **out) {
   Scratch &s = ctx->scratch[slot];
   if (bytes == 0) bytes = 1;
   if (s.cap < bytes) {
+    if (ctx->capturing)
+      return fail(MMNB_ERR_ARG,
+                  "device scratch must grow during graph capture: run the call once "
+                  "before capturing it");
     if (s.ptr) {
       // The stream may still read the old buffer: drain it first.
       MMNB_HIP(hipStreamSynchronize(ctx->stream));
@@ -133,6 +137,7 @@ int mmnb_shutdown(mmnb_ctx *ctx) {
       if (s.ptr) (void)hipFree(s.ptr);
     for (auto &ev : ctx->events)
       if (ev) (void)hipEventDestroy(ev);
+    for (auto &ev : ctx->tev) (void)hipEventDestroy(ev);
     (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
@@ -259,6 +264,7 @@ int mmnb_matmul_nbits_dev(mmnb_ctx *ctx, const mmnb_pack *pack, const float *d_a
 int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
                       int64_t m, float *y) {
   MMNB_GUARD_CTX(ctx);
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "host entry point during graph capture");
   int rc = check_nbits_pack(ctx, pack);
   if (rc) return rc;
   if (m < 0) return fail(MMNB_ERR_ARG, "MatMulNBits: negative M");
@@ -307,6 +313,7 @@ int mmnb_dynamic_quantize_linear_dev(mmnb_ctx *ctx, const float *d_x, int64_t n,
 int mmnb_dynamic_quantize_linear(mmnb_ctx *ctx, const float *x, int64_t n,
                                  uint8_t *y, float *scale, int64_t *zero_point) {
   MMNB_GUARD_CTX(ctx);
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "host entry point during graph capture");
   if (n < 0) return fail(MMNB_ERR_ARG, "DynamicQuantizeLinear: negative length");
   if ((n > 0 && (!x || !y)) || !scale || !zero_point)
     return fail(MMNB_ERR_ARG, "DynamicQuantizeLinear: null buffer");
@@ -446,6 +453,7 @@ int mmnb_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *pack, const void *a,
                         const int64_t *a_zero_point, int64_t a_zero_point_len,
                         int32_t *y) {
   MMNB_GUARD_CTX(ctx);
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "host entry point during graph capture");
   const int64_t azl = a_zero_point ? a_zero_point_len : 0;
   int rc = check_int_args(ctx, pack, a_batch, m, azl);
   if (rc) return rc;
@@ -611,6 +619,116 @@ int mmnb_event_elapsed_ms(mmnb_ctx *ctx, int slot_start, int slot_end, float *ms
   if (rc) return rc;
   MMNB_HIP(hipEventSynchronize(ctx->events[slot_end]));
   MMNB_HIP(hipEventElapsedTime(ms, ctx->events[slot_start], ctx->events[slot_end]));
+  return MMNB_OK;
+}
+
+static const char *kKernelNames[kKernCount] = {
+    "k_gemv_valu", "k_prep_rowblock", "k_gemm_mfma", "k_dql_minmax",
+    "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b"};
+
+const char *mmnb_kernel_name(int kernel_id) {
+  if (kernel_id < 0 || kernel_id >= kKernCount) return nullptr;
+  return kKernelNames[kernel_id];
+}
+
+int mmnb_kernel_timing(mmnb_ctx *ctx, int enable, int max_launches) {
+  MMNB_GUARD_CTX(ctx);
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  if (!enable) {
+    ctx->timing = false;
+    return MMNB_OK;
+  }
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "kernel timing during graph capture");
+  if (max_launches < 1 || max_launches > (1 << 20))
+    return fail(MMNB_ERR_ARG, "max_launches out of range");
+  MMNB_HIP(hipStreamSynchronize(ctx->stream));
+  while (ctx->tev.size() < (size_t)max_launches * 2) {
+    hipEvent_t ev;
+    MMNB_HIP(hipEventCreate(&ev));
+    ctx->tev.push_back(ev);
+  }
+  ctx->tkid.assign((size_t)max_launches, -1);
+  ctx->tused = 0;
+  ctx->timing = true;
+  return MMNB_OK;
+}
+
+int mmnb_kernel_timing_read(mmnb_ctx *ctx, int kernel_id, int64_t *count, double *total_ms,
+                            double *min_ms, double *max_ms) {
+  MMNB_GUARD_CTX(ctx);
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  MMNB_HIP(hipStreamSynchronize(ctx->stream));
+  int64_t c = 0;
+  double tot = 0.0, mn = 0.0, mx = 0.0;
+  for (size_t i = 0; i < ctx->tused; i++) {
+    if (ctx->tkid[i] != kernel_id) continue;
+    float ms = 0.0f;
+    MMNB_HIP(hipEventElapsedTime(&ms, ctx->tev[2 * i], ctx->tev[2 * i + 1]));
+    if (c == 0 || ms < mn) mn = ms;
+    if (c == 0 || ms > mx) mx = ms;
+    tot += ms;
+    c++;
+  }
+  if (count) *count = c;
+  if (total_ms) *total_ms = tot;
+  if (min_ms) *min_ms = mn;
+  if (max_ms) *max_ms = mx;
+  return MMNB_OK;
+}
+
+int mmnb_graph_begin(mmnb_ctx *ctx) {
+  MMNB_GUARD_CTX(ctx);
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "graph capture already active");
+  if (ctx->timing) return fail(MMNB_ERR_ARG, "graph capture while kernel timing is on");
+  MMNB_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  ctx->capturing = true;
+  return MMNB_OK;
+}
+
+int mmnb_graph_end(mmnb_ctx *ctx, void **graph_exec) {
+  MMNB_GUARD_CTX(ctx);
+  if (!graph_exec) return fail(MMNB_ERR_ARG, "null out pointer");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  if (!ctx->capturing) return fail(MMNB_ERR_ARG, "no graph capture active");
+  ctx->capturing = false;
+  hipGraph_t g = nullptr;
+  MMNB_HIP(hipStreamEndCapture(ctx->stream, &g));
+  hipGraphExec_t ex = nullptr;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return check_hip(e, "hipGraphInstantiate");
+  *graph_exec = (void *)ex;
+  return MMNB_OK;
+}
+
+int mmnb_graph_launch(mmnb_ctx *ctx, void *graph_exec) {
+  MMNB_GUARD_CTX(ctx);
+  if (!graph_exec) return fail(MMNB_ERR_ARG, "null graph");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  MMNB_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream));
+  return MMNB_OK;
+}
+
+int mmnb_graph_destroy(mmnb_ctx *ctx, void *graph_exec) {
+  MMNB_GUARD_CTX(ctx);
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  if (graph_exec) {
+    MMNB_HIP(hipStreamSynchronize(ctx->stream));
+    MMNB_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  }
   return MMNB_OK;
 }
 
