@@ -137,7 +137,8 @@ def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
     n_steps, ms_step, kt = time_mmnb(ctx, lib, [pack], da, m, dy, steps, warmup)
     flops = 2.0 * m * k * n
     gk = kernel_avg_ms(kt, "k_gemm_mfma")
-    pk = kernel_avg_ms(kt, "k_prep_rowblock") if "k_prep_rowblock" in kt else 0.0
+    # k_prep_a counts both prep launches (row exponents, hi/lo split)
+    pk = kt["k_prep_a"][1] / kt["k_gemm_mfma"][0] if "k_prep_a" in kt else 0.0
     achieved = flops / (gk * 1e-3) / 1e12
     res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "steps": n_steps,
            "ms_per_call": ms_step, "tflops": flops / (ms_step * 1e-3) / 1e12,
@@ -292,6 +293,10 @@ def main():
             out["gemv_bs32_zp"] = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 32, True,
                                              args.steps, args.warmup, seed=3)
             print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['kernel_gbs']:.0f} GB/s kernel",
+                  file=sys.stderr, flush=True)
+            out["gemv_large"] = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128,
+                                           False, 60, 6, seed=4)
+            print(f"# GEMV K=N=16384: {out['gemv_large']['kernel_gbs']:.0f} GB/s kernel",
                   file=sys.stderr, flush=True)
             out["gemm"] = bench_gemm(ctx, lib, ops, synth, 512, 4096, 4096, 32, True,
                                      200, 20)

@@ -71,141 +71,204 @@ int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n, int64_t
 // ---------------------------------------------------------------------------
 // Decode-shape GEMV on the vector ALUs (fp32 FMA), M <= 8.
 //
-// The K extent of a column is cut into 16-byte chunks (32 nibbles); chunk c
-// = (segment s = c/2, half g = c%2) holds k = 64s + 16j + 8g + e for
-// j = 0..3, e = 0..7 (dword j, nibble e).  LPC lanes share one column and
-// walk its chunks with stride LPC; a wave serves G = 64/LPC columns at a time
-// and U such groups, so every lane keeps U independent 16-byte weight loads
-// in flight.  Per dword the lane forms sum_e a*q, then folds the block's
-// zero point through sum_e a and its scale:
+// A column's K extent is cut into 16-byte chunks (32 nibbles); chunk c =
+// (segment s = c/2, half g = c%2) holds k = 64s + 16j + 8g + e for dword
+// j = 0..3, nibble e = 0..7.  A workgroup owns 2R columns and all of K:
+//   wave w, lane l: half h = l/32 picks one column of each pair, t = l%32;
+//   the lane owns chunk c = 32w + t (+ 32W per extra iteration) of the R
+//   columns 2r + h, r = 0..R-1.
+// Every lane issues all of its R weight loads (16 B each), their scales and
+// zero points, and its 32 activations before doing any arithmetic, so a
+// workgroup has its whole share of the weight stream in flight at once.  The
+// activations of a chunk are loaded once and reused for R columns.  Per dword
+// the lane forms sum_e a*q and folds the block's zero point through sum a:
 //     acc += scale * (sum a*q) - (scale*zp) * (sum a).
+// The 32 lanes of a column half-wave reduce with DPP/swizzle, the waves
+// through LDS.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_seg_sum(float v, int lpc) {
-  for (int off = 1; off < lpc; off <<= 1) v += __shfl_xor(v, off, 64);
-  return v;
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                false);
+  return v + __builtin_bit_cast(float, moved);
 }
 
-template <int M, int U>
-__global__ __launch_bounds__(256) void k_gemv_valu(
-    const float *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W,
-    int64_t col_bytes, const float *__restrict__ S, const uint8_t *__restrict__ Z,
-    int nb, int bs_log2, int K, int N, float *__restrict__ Y, int chunks,
-    int lpc_log2, int fast) {
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int lpc = 1 << lpc_log2;
-  const int G = 64 >> lpc_log2;
-  const int gi = lane >> lpc_log2;
-  const int t = lane & (lpc - 1);
-  const int col0 = wave * (U * G);
+// Sum over each group of 32 lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  // xor 16 inside each 32-lane group (ds_swizzle bit mode, xor_mask = 16)
+  const int o = __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F);
+  return v + __builtin_bit_cast(float, o);
+}
 
-  float acc[M][U];
+constexpr int kGemvMaxWaves = 4;
+
+template <int M, int R, int NBPC>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
+    const float *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W,
+    int64_t col_bytes, const float *__restrict__ S, const uint8_t *__restrict__ Z, int nb,
+    int bs_log2, int K, int N, float *__restrict__ Y, int C, int iters, int fast) {
+  __shared__ float red[kGemvMaxWaves][M][2 * R];
+  const int nw = blockDim.x >> 6;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int h = l >> 5, t = l & 31;
+  const int col0 = blockIdx.x * (2 * R);
+
+  int colr[R];
+  bool colok[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int c = col0 + 2 * r + h;
+    colok[r] = c < N;
+    colr[r] = colok[r] ? c : N - 1;
+  }
+  float acc[M][R];
 #pragma unroll
   for (int m = 0; m < M; m++)
 #pragma unroll
-    for (int u = 0; u < U; u++) acc[m][u] = 0.0f;
+    for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
 
-  for (int c = t; c < chunks; c += lpc) {
-    const int s = c >> 1, g = c & 1;
-    const int kb = s * kSegK + g * 8;
-    // weights, scales, zero points for the U columns
-    uint4 wv[U];
-    float sc[U][4], sz[U][4];
+  for (int it = 0; it < iters; it++) {
+    const int c = 32 * w + t + it * 32 * nw;
+    const bool cv = c < C;
+    const int cc = cv ? c : 0;
+    const int s = cc >> 1, g = cc & 1;
+    // ---- issue every load of this chunk
+    uint4 wv[R];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      int col = col0 + u * G + gi;
-      const bool ok = col < N;
-      col = ok ? col : N - 1;
-      wv[u] = *(const uint4 *)(W + (int64_t)col * col_bytes + (int64_t)c * 16);
+    for (int r = 0; r < R; r++)
+      wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+    float sc[R][NBPC], sz[R][NBPC];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        int blk = (kb + 16 * j) >> bs_log2;
-        const bool inb = blk < nb;
-        blk = inb ? blk : nb - 1;
-        const int zi = col * nb + blk;
-        float s_ = S[zi];
+    for (int q = 0; q < NBPC; q++) {
+      // block of dwords j in [q*4/NBPC, (q+1)*4/NBPC)
+      const int kq = s * kSegK + 16 * (q * (4 / NBPC)) + (NBPC == 4 ? 8 * g : 0);
+      int blk = kq >> bs_log2;
+      const bool inb = cv && blk < nb;
+      blk = blk < nb ? blk : nb - 1;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int zi = colr[r] * nb + blk;
+        const float sv = S[zi];
         int zpv = 8;
         if (Z) {
           const uint8_t zb = Z[zi >> 1];
           zpv = (zi & 1) ? (zb >> 4) : (zb & 0xF);
         }
-        s_ = (inb && ok) ? s_ : 0.0f;
-        sc[u][j] = s_;
-        sz[u][j] = s_ * (float)zpv;
+        sc[r][q] = inb ? sv : 0.0f;
+        sz[r][q] = inb ? sv * (float)zpv : 0.0f;
       }
     }
+    float av[M][32];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int k0 = kb + 16 * j;
-      float av[M][8];
-      float sa[M];
+    for (int m = 0; m < M; m++) {
+      const float *ar = A + (int64_t)m * lda + s * kSegK + 8 * g;
 #pragma unroll
-      for (int m = 0; m < M; m++) {
-        const float *ar = A + (int64_t)m * lda + k0;
+      for (int j = 0; j < 4; j++) {
         if (fast) {
-          const float4 x0 = *(const float4 *)(ar);
-          const float4 x1 = *(const float4 *)(ar + 4);
-          av[m][0] = x0.x; av[m][1] = x0.y; av[m][2] = x0.z; av[m][3] = x0.w;
-          av[m][4] = x1.x; av[m][5] = x1.y; av[m][6] = x1.z; av[m][7] = x1.w;
+          const float4 x0 = cv ? *(const float4 *)(ar + 16 * j) : make_float4(0, 0, 0, 0);
+          const float4 x1 = cv ? *(const float4 *)(ar + 16 * j + 4) : make_float4(0, 0, 0, 0);
+          av[m][8 * j + 0] = x0.x; av[m][8 * j + 1] = x0.y;
+          av[m][8 * j + 2] = x0.z; av[m][8 * j + 3] = x0.w;
+          av[m][8 * j + 4] = x1.x; av[m][8 * j + 5] = x1.y;
+          av[m][8 * j + 6] = x1.z; av[m][8 * j + 7] = x1.w;
         } else {
+          const int k0 = s * kSegK + 8 * g + 16 * j;
 #pragma unroll
-          for (int e = 0; e < 8; e++) av[m][e] = (k0 + e < K) ? ar[e] : 0.0f;
+          for (int e = 0; e < 8; e++) av[m][8 * j + e] = (cv && k0 + e < K) ? ar[16 * j + e] : 0.0f;
         }
-        float s_ = 0.0f;
+      }
+    }
+    // ---- arithmetic
+    float sa[M][NBPC];
 #pragma unroll
-        for (int e = 0; e < 8; e++) s_ += av[m][e];
-        sa[m] = s_;
+    for (int m = 0; m < M; m++)
+#pragma unroll
+      for (int q = 0; q < NBPC; q++) {
+        float v = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32 / NBPC; e++) v += av[m][q * (32 / NBPC) + e];
+        sa[m][q] = v;
       }
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const uint32_t w = j == 0 ? wv[u].x : j == 1 ? wv[u].y : j == 2 ? wv[u].z : wv[u].w;
-        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        float q[8];
-        q[0] = (float)(lo & 0xFF);
-        q[1] = (float)(hi & 0xFF);
-        q[2] = (float)((lo >> 8) & 0xFF);
-        q[3] = (float)((hi >> 8) & 0xFF);
-        q[4] = (float)((lo >> 16) & 0xFF);
-        q[5] = (float)((hi >> 16) & 0xFF);
-        q[6] = (float)(lo >> 24);
-        q[7] = (float)(hi >> 24);
+    for (int r = 0; r < R; r++) {
+      const uint32_t wd[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+#pragma unroll
+      for (int q = 0; q < NBPC; q++) {
+        float d[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) d[m] = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 4 / NBPC; jj++) {
+          const int j = q * (4 / NBPC) + jj;
+          const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
+          float qv[8];
+          qv[0] = (float)(lo & 0xFF);
+          qv[1] = (float)(hi & 0xFF);
+          qv[2] = (float)((lo >> 8) & 0xFF);
+          qv[3] = (float)((hi >> 8) & 0xFF);
+          qv[4] = (float)((lo >> 16) & 0xFF);
+          qv[5] = (float)((hi >> 16) & 0xFF);
+          qv[6] = (float)(lo >> 24);
+          qv[7] = (float)(hi >> 24);
+#pragma unroll
+          for (int m = 0; m < M; m++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) d[m] = fmaf(av[m][8 * j + e], qv[e], d[m]);
+        }
 #pragma unroll
         for (int m = 0; m < M; m++) {
-          float d = 0.0f;
-#pragma unroll
-          for (int e = 0; e < 8; e++) d = fmaf(av[m][e], q[e], d);
-          acc[m][u] = fmaf(sc[u][j], d, acc[m][u]);
-          acc[m][u] = fmaf(-sz[u][j], sa[m], acc[m][u]);
+          acc[m][r] = fmaf(sc[r][q], d[m], acc[m][r]);
+          acc[m][r] = fmaf(-sz[r][q], sa[m][q], acc[m][r]);
         }
       }
     }
   }
+  // ---- reductions: 32 lanes of a half-wave, then the waves
 #pragma unroll
   for (int m = 0; m < M; m++)
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const float v = wave_seg_sum(acc[m][u], lpc);
-      const int col = col0 + u * G + gi;
-      if (t == 0 && col < N) Y[(int64_t)m * N + col] = v;
+    for (int r = 0; r < R; r++) {
+      const float v = half_wave_sum(acc[m][r]);
+      if (t == 0) red[w][m][2 * r + h] = v;
     }
+  __syncthreads();
+  for (int i = threadIdx.x; i < M * 2 * R; i += blockDim.x) {
+    const int m = i / (2 * R), cl = i % (2 * R);
+    float v = 0.0f;
+    for (int ww = 0; ww < nw; ww++) v += red[ww][m][cl];
+    const int col = col0 + cl;
+    if (col < N) Y[(int64_t)m * N + col] = v;
+  }
+}
+
+template <int M, int R>
+static int launch_gemv_mr(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const float *A,
+                          int64_t lda, const mmnb_pack *p, float *Y, int C, int iters,
+                          int fast, int bs_log2) {
+  const int nb = (int)p->n_blocks, K = (int)p->k, N = (int)p->n;
+#define MMNB_GEMV_LAUNCH(Q)                                                                  \
+  return launch(ctx, kKernGemv, k_gemv_valu<M, R, Q>, grid, block, 0, A, lda, p->d_w,      \
+                p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C, iters, fast)
+  if (nbpc == 4) MMNB_GEMV_LAUNCH(4);
+  if (nbpc == 2) MMNB_GEMV_LAUNCH(2);
+  MMNB_GEMV_LAUNCH(1);
+#undef MMNB_GEMV_LAUNCH
 }
 
 template <int M>
-static int launch_gemv_m(mmnb_ctx *ctx, int u, dim3 grid, const float *A, int64_t lda,
-                         const mmnb_pack *p, float *Y, int chunks, int lpc_log2, int fast,
-                         int bs_log2) {
-  const int nb = (int)p->n_blocks, K = (int)p->k, N = (int)p->n;
-  if (u == 4)
-    return launch(ctx, kKernGemv, k_gemv_valu<M, 4>, grid, dim3(256), 0, A, lda, p->d_w,
-                  p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks, lpc_log2,
-                  fast);
-  if (u == 2)
-    return launch(ctx, kKernGemv, k_gemv_valu<M, 2>, grid, dim3(256), 0, A, lda, p->d_w,
-                  p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks, lpc_log2,
-                  fast);
-  return launch(ctx, kKernGemv, k_gemv_valu<M, 1>, grid, dim3(256), 0, A, lda, p->d_w,
-                p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, chunks, lpc_log2,
-                fast);
+static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
+                         const float *A, int64_t lda, const mmnb_pack *p, float *Y, int C,
+                         int iters, int fast, int bs_log2) {
+  if (M <= 2 && R == 8)
+    return launch_gemv_mr<M, (M <= 2 ? 8 : 1)>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
+  if (M <= 4 && R == 4)
+    return launch_gemv_mr<M, (M <= 4 ? 4 : 1)>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
+  if (R == 2) return launch_gemv_mr<M, 2>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
+  return launch_gemv_mr<M, 1>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
 }
 
 static int ilog2(int64_t v) {
@@ -216,32 +279,35 @@ static int ilog2(int64_t v) {
 
 static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y) {
-  const int chunks = (int)(p->col_bytes / 16);
-  int lpc = 1;
-  while (lpc < chunks && lpc < 64) lpc <<= 1;
-  const int G = 64 / lpc;
+  const int C = (int)(p->col_bytes / 16);  // chunks per column
+  // waves splitting K: one chunk per lane up to 16 waves, then iterate
+  int nw = (C + 31) / 32;
+  int iters = 1;
+  if (nw > kGemvMaxWaves) {
+    iters = (nw + kGemvMaxWaves - 1) / kGemvMaxWaves;
+    nw = (C + 32 * iters - 1) / (32 * iters);
+  }
+  // columns per workgroup 2R: as many as keep >= 2 workgroups per CU
   const int64_t n = p->n;
-  // columns per wave: keep >= ~4 waves per CU where N allows
-  const int64_t want_waves = (int64_t)ctx->cu_count * 4;
-  int u = 4;
-  while (u > 1 && (n + (int64_t)u * G - 1) / ((int64_t)u * G) < want_waves) u >>= 1;
-  const int64_t waves = (n + (int64_t)u * G - 1) / ((int64_t)u * G);
-  const dim3 grid((unsigned)((waves + 3) / 4));
+  int R = m <= 2 ? 8 : (m <= 4 ? 4 : 2);
+  while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
+  const dim3 block((unsigned)(64 * nw));
   // Aligned float4 path: every 8-float run of a chunk lies inside the row,
   // i.e. rows hold k64 values (zero padded past K by the host entry point, or
   // K itself is a multiple of 64).
   const int f = ((lda % 4 == 0) && (((uintptr_t)d_a & 15) == 0) && (lda >= p->k64)) ? 1 : 0;
   const int bs_log2 = ilog2(p->block);
-  const int lpc_log2 = ilog2(lpc);
+  const int nbpc = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
   switch (m) {
-    case 1: return launch_gemv_m<1>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    case 2: return launch_gemv_m<2>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    case 3: return launch_gemv_m<3>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    case 4: return launch_gemv_m<4>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    case 5: return launch_gemv_m<5>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    case 6: return launch_gemv_m<6>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    case 7: return launch_gemv_m<7>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
-    default: return launch_gemv_m<8>(ctx, u, grid, d_a, lda, p, d_y, chunks, lpc_log2, f, bs_log2);
+    case 1: return launch_gemv_m<1>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    case 2: return launch_gemv_m<2>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    case 3: return launch_gemv_m<3>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    case 4: return launch_gemv_m<4>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    case 5: return launch_gemv_m<5>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    case 6: return launch_gemv_m<6>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    case 7: return launch_gemv_m<7>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+    default: return launch_gemv_m<8>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
   }
 }
 
@@ -260,60 +326,70 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
 // perm = {0,4,1,5,2,6,3,7} (the order the weight dequantisation produces).
 // Rows >= M and k >= K are zero.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_prep_rowblock(
+// Row exponents: one wave per row, e_m = 13 - floor(log2(max|a_m|)).
+__global__ __launch_bounds__(256) void k_prep_rowexp(const float *__restrict__ A, int64_t lda,
+                                                     int64_t M, int64_t K,
+                                                     int *__restrict__ row_exp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const float *ar = A + row * lda;
+  float mx = 0.0f;
+  const bool vec = ((((uintptr_t)ar) & 15) == 0);
+  int64_t k0 = 0;
+  if (vec) {
+    const int64_t k4 = K >> 2;
+    for (int64_t i = lane; i < k4; i += 64) {
+      const float4 v = ((const float4 *)ar)[i];
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    k0 = k4 << 2;
+  }
+  for (int64_t k = k0 + lane; k < K; k += 64) mx = fmaxf(mx, fabsf(ar[k]));
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) {
+    int e = 0;
+    if (mx > 0.0f && mx < INFINITY) e = 13 - ilogbf(mx);
+    row_exp[row] = e;
+  }
+}
+
+// Split into fp16 hi/lo in the MFMA operand layout.  One workgroup per
+// (32-row block, 64-k segment); thread (j, l) writes unit (j, lane l) of the
+// hi and the lo piece.
+__global__ __launch_bounds__(256) void k_prep_convert(
     const float *__restrict__ A, int64_t lda, int64_t M, int64_t K, int64_t segs,
-    uint4 *__restrict__ out, int *__restrict__ row_exp) {
-  __shared__ int s_exp[32];
-  const int rb = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // Phase 1: per-row max|a| -> exponent.  4 waves x 8 rows.
-  for (int r = wave; r < 32; r += 4) {
-    const int64_t row = (int64_t)rb * 32 + r;
-    float mx = 0.0f;
-    if (row < M) {
-      const float *ar = A + row * lda;
-      for (int64_t k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(ar[k]));
-    }
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (lane == 0) {
-      int e = 0;
-      if (mx > 0.0f && mx < INFINITY) e = 13 - ilogbf(mx);
-      s_exp[r] = e;
-      if (row < M) row_exp[row] = e;
-    }
-  }
-  __syncthreads();
-  // Phase 2: units (s, j, lane l) -> hi and lo 16-byte pieces.
-  const int64_t units = segs * 4 * 64;
-  for (int64_t u = threadIdx.x; u < units; u += blockDim.x) {
-    const int l = (int)(u & 63);
-    const int j = (int)((u >> 6) & 3);
-    const int64_t s = u >> 8;
-    const int r = l & 31, g = l >> 5;
-    const int64_t row = (int64_t)rb * 32 + r;
-    const int64_t k0 = s * kSegK + 16 * j + 8 * g;
-    float v[8];
+    const int *__restrict__ row_exp, uint4 *__restrict__ out) {
+  const int64_t s = blockIdx.x, rb = blockIdx.y;
+  const int l = threadIdx.x & 63, j = threadIdx.x >> 6;
+  const int r = l & 31, g = l >> 5;
+  const int64_t row = rb * 32 + r;
+  const int64_t k0 = s * kSegK + 16 * j + 8 * g;
+  float v[8];
+  if (row < M && k0 + 8 <= K && (((uintptr_t)(A + row * lda + k0)) & 15) == 0) {
+    const float4 x0 = *(const float4 *)(A + row * lda + k0);
+    const float4 x1 = *(const float4 *)(A + row * lda + k0 + 4);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+  } else {
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const int64_t kk = k0 + e;
-      v[e] = (row < M && kk < K) ? A[row * lda + kk] : 0.0f;
-    }
-    const int ex = s_exp[r];
-    _Float16 hi[8], lo[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float x = ldexpf(v[e], ex);
-      const _Float16 h = (_Float16)x;
-      hi[e] = h;
-      lo[e] = (_Float16)(x - (float)h);
-    }
-    // permute to the dequantised-weight order {0,4,1,5,2,6,3,7}
-    half8_t H = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
-    half8_t L = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
-    const int64_t base = (((int64_t)rb * segs + s) * 4 + j) * 2;
-    out[(base + 0) * 64 + l] = __builtin_bit_cast(uint4, H);
-    out[(base + 1) * 64 + l] = __builtin_bit_cast(uint4, L);
+    for (int e = 0; e < 8; e++) v[e] = (row < M && k0 + e < K) ? A[row * lda + k0 + e] : 0.0f;
   }
+  const int ex = row < M ? row_exp[row] : 0;
+  _Float16 hi[8], lo[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = ldexpf(v[e], ex);
+    const _Float16 h = (_Float16)x;
+    hi[e] = h;
+    lo[e] = (_Float16)(x - (float)h);
+  }
+  // permute to the dequantised-weight order {0,4,1,5,2,6,3,7}
+  half8_t H = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
+  half8_t L = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
+  const int64_t base = ((rb * segs + s) * 4 + j) * 2;
+  out[(base + 0) * 64 + l] = __builtin_bit_cast(uint4, H);
+  out[(base + 1) * 64 + l] = __builtin_bit_cast(uint4, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -447,8 +523,11 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   int rc;
   if ((rc = scratch_get(ctx, 2, ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)mpad * 4, &d_exp))) return rc;
-  if ((rc = launch(ctx, kKernPrep, k_prep_rowblock, dim3((unsigned)rblocks), dim3(256), 0, d_a,
-                    lda, m, p->k, segs, (uint4 *)d_ap, (int *)d_exp)))
+  if ((rc = launch(ctx, kKernPrep, k_prep_rowexp, dim3((unsigned)((m + 3) / 4)), dim3(256), 0,
+                    d_a, lda, m, p->k, (int *)d_exp)))
+    return rc;
+  if ((rc = launch(ctx, kKernPrep, k_prep_convert, dim3((unsigned)segs, (unsigned)rblocks),
+                    dim3(256), 0, d_a, lda, m, p->k, segs, (const int *)d_exp, (uint4 *)d_ap)))
     return rc;
   const dim3 grid((unsigned)((p->n + kGemmBN - 1) / kGemmBN), (unsigned)(mpad / kGemmBM));
   return launch(ctx, kKernGemm, k_gemm_mfma, grid, dim3(256), 0, (const uint4 *)d_ap,

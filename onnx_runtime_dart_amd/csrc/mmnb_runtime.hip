@@ -623,7 +623,7 @@ int mmnb_event_elapsed_ms(mmnb_ctx *ctx, int slot_start, int slot_end, float *ms
 }
 
 static const char *kKernelNames[kKernCount] = {
-    "k_gemv_valu", "k_prep_rowblock", "k_gemm_mfma", "k_dql_minmax",
+    "k_gemv_valu", "k_prep_a", "k_gemm_mfma", "k_dql_minmax",
     "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b"};
 
 const char *mmnb_kernel_name(int kernel_id) {
