@@ -65,6 +65,8 @@ struct mmnb_ctx {
   std::vector<hipEvent_t> tev;   // 2 per slot
   std::vector<int> tkid;         // kernel id per used slot
   size_t tused = 0;
+  // Tuning override of the GEMV columns-per-lane R (MMNB_GEMV_R; 0 = auto).
+  int gemv_r = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
 };

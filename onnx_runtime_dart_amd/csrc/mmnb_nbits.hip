@@ -291,6 +291,7 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   const int64_t n = p->n;
   int R = m <= 2 ? 8 : (m <= 4 ? 4 : 2);
   while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  if (ctx->gemv_r > 0) R = ctx->gemv_r;  // tuning override
   const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
   const dim3 block((unsigned)(64 * nw));
   // Aligned float4 path: every 8-float run of a chunk lies inside the row,
@@ -424,28 +425,83 @@ __device__ __forceinline__ int zp_of(const uint8_t *__restrict__ Z, int64_t zi) 
   return (zi & 1) ? (zb >> 4) : (zb & 0xF);
 }
 
-constexpr int kGemmBM = 64;
-constexpr int kGemmBN = 128;
+constexpr int kGemmBM = 64;   // two 32-row blocks
+constexpr int kGemmBN = 128;  // four 32-column blocks
+constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 
+// Prefill GEMM.  Workgroup tile 64 (M) x 128 (N), 4 waves in 2 x 2, wave
+// tile 32 x 64 (one 32-row A block, two 32-column weight blocks).  Per 64-k
+// segment the workgroup stages the prepared activations (16 x 1 KB units:
+// 2 row blocks x 4 steps x hi/lo) and the packed weights (128 columns x 32 B)
+// in LDS, double-buffered: the global loads of segment s+1 are in flight
+// while segment s runs on the MFMAs.  Each 16-k step issues 2 (weight
+// blocks) x 2 (hi, lo) v_mfma_f32_32x32x16_f16 into per-block partials D; at
+// each quantisation-block boundary acc += scale[n, blk] * D.
+template <int NBPS>  // quantisation blocks per 64-k segment: 1 (block >= 64), 2, 4
 __global__ __launch_bounds__(256) void k_gemm_mfma(
     const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int64_t segs,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S,
-    const uint8_t *__restrict__ Z, int64_t nb, int64_t bs, int64_t M, int64_t N,
-    float *__restrict__ Y) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint8_t *__restrict__ Z, int64_t nb, int bs_log2, int64_t M, int64_t N,
+    int grid_x, int grid_y, float *__restrict__ Y) {
+  __shared__ uint4 sA[2][16 * 64];
+  __shared__ uint4 sW[2][kGemmBN * 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t rb = (int64_t)blockIdx.y * (kGemmBM / 32) + wm;  // 32-row block
-  const int64_t n0 = (int64_t)blockIdx.x * kGemmBN + wn * 64;
   const int cl = lane & 31, g = lane >> 5;
 
+  // XCD-aware tile order: consecutive workgroup ids go to different XCDs
+  // (round robin), so regroup them into contiguous chunks per XCD, then walk
+  // the chunk kGemmGroup row bands at a time.
+  const int G = grid_x * grid_y;
+  int L = blockIdx.x;
+  if ((G & 7) == 0) L = (L & 7) * (G >> 3) + (L >> 3);
+  const int per_group = kGemmGroup * grid_x;
+  const int first_y = (L / per_group) * kGemmGroup;
+  const int rows_in_group = min(grid_y - first_y, kGemmGroup);
+  const int ty = first_y + (L % per_group) % rows_in_group;
+  const int tx = (L % per_group) / rows_in_group;
+
+  const int64_t rb0 = (int64_t)ty * 2;
+  const int64_t n0 = (int64_t)tx * kGemmBN;
+
+  // global -> LDS assignment
+  int64_t a_src[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int idx = tid + 256 * i;
+    const int u = idx >> 6, l = idx & 63;
+    a_src[i] = ((rb0 + (u >> 3)) * segs * 8 + (u & 7)) * 64 + l;  // + s * 8 * 64
+  }
+  int64_t wcol = n0 + (tid >> 1);
+  if (wcol >= N) wcol = N - 1;
+  const uint8_t *w_src = W + wcol * col_bytes + (tid & 1) * 16;
+
+  // this wave's columns / rows
   int64_t col[2];
   bool colok[2];
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    col[t] = n0 + t * 32 + cl;
+    col[t] = n0 + wn * 64 + t * 32 + cl;
     colok[t] = col[t] < N;
     if (!colok[t]) col[t] = N - 1;
   }
+
+  auto load_scales = [&](int64_t s, float (&sc)[2][NBPS], int (&zq)[2][NBPS]) {
+#pragma unroll
+    for (int q = 0; q < NBPS; q++) {
+      const int64_t blk = (s * kSegK + q * (kSegK / NBPS)) >> bs_log2;
+      const bool inb = blk < nb;
+      const int64_t b2 = inb ? blk : nb - 1;
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        const int64_t zi = col[t] * nb + b2;
+        const float sv = S[zi];
+        sc[t][q] = inb ? sv : 0.0f;
+        zq[t][q] = zp_of(Z, zi);
+      }
+    }
+  };
+
   float16_t acc[2], D[2];
 #pragma unroll
   for (int t = 0; t < 2; t++)
@@ -454,54 +510,76 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
       acc[t][r] = 0.0f;
       D[t][r] = 0.0f;
     }
-  int zpv[2] = {8, 8};
-  float scl[2] = {0.0f, 0.0f};
-  int64_t cur_blk = -1;
+
+  // prologue: segment 0 -> buffer 0
+  uint4 ra[4], rw;
+#pragma unroll
+  for (int i = 0; i < 4; i++) ra[i] = Ap[a_src[i]];
+  rw = *(const uint4 *)w_src;
+  float sc_cur[2][NBPS], sc_nxt[2][NBPS];
+  int zp_cur[2][NBPS], zp_nxt[2][NBPS];
+  load_scales(0, sc_cur, zp_cur);
+#pragma unroll
+  for (int i = 0; i < 4; i++) sA[0][tid + 256 * i] = ra[i];
+  sW[0][tid] = rw;
+  __syncthreads();
 
   for (int64_t s = 0; s < segs; s++) {
+    const int buf = (int)(s & 1);
+    const bool more = s + 1 < segs;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) ra[i] = Ap[a_src[i] + (s + 1) * 8 * 64];
+      rw = *(const uint4 *)(w_src + (s + 1) * kSegBytes);
+      load_scales(s + 1, sc_nxt, zp_nxt);
+    }
     uint4 wv[2];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
-      wv[t] = *(const uint4 *)(W + col[t] * col_bytes + s * kSegBytes + g * 16);
+    for (int t = 0; t < 2; t++) wv[t] = sW[buf][(wn * 64 + t * 32 + cl) * 2 + g];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int64_t kstep = s * kSegK + 16 * j;
-      const int64_t blk = kstep / bs;
-      if (blk != cur_blk) {
-        cur_blk = blk;
-        const bool inb = blk < nb;
-        const int64_t b2 = inb ? blk : nb - 1;
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-          const int64_t zi = col[t] * nb + b2;
-          zpv[t] = zp_of(Z, zi);
-          scl[t] = inb ? S[zi] : 0.0f;
-        }
-      }
-      const int64_t ubase = ((rb * segs + s) * 4 + j) * 2;
-      const half8_t ah = __builtin_bit_cast(half8_t, Ap[(ubase + 0) * 64 + lane]);
-      const half8_t al = __builtin_bit_cast(half8_t, Ap[(ubase + 1) * 64 + lane]);
+      const int q = j / (4 / NBPS);
+      const half8_t ah = __builtin_bit_cast(half8_t, sA[buf][(wm * 8 + j * 2 + 0) * 64 + lane]);
+      const half8_t al = __builtin_bit_cast(half8_t, sA[buf][(wm * 8 + j * 2 + 1) * 64 + lane]);
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const uint32_t w = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z : wv[t].w;
-        const half8_t b = dequant8(w, zpv[t]);
+        const half8_t b = dequant8(w, zp_cur[t][q]);
         D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[t], 0, 0, 0);
         D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[t], 0, 0, 0);
       }
-      // block boundary after this 16-k step?
-      if (((kstep + 16) % bs) == 0) {
+      // end of a quantisation block?
+      const bool boundary = (NBPS > 1) ? (((j + 1) % (4 / NBPS)) == 0)
+                                       : (j == 3 && (((s + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0);
+      if (boundary) {
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
           for (int r = 0; r < 16; r++) {
-            acc[t][r] = fmaf(scl[t], D[t][r], acc[t][r]);
+            acc[t][r] = fmaf(sc_cur[t][q], D[t][r], acc[t][r]);
             D[t][r] = 0.0f;
           }
       }
     }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) sA[buf ^ 1][tid + 256 * i] = ra[i];
+      sW[buf ^ 1][tid] = rw;
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int q = 0; q < NBPS; q++) {
+          sc_cur[t][q] = sc_nxt[t][q];
+          zp_cur[t][q] = zp_nxt[t][q];
+        }
+    }
+    __syncthreads();
   }
+  // A block still open at the end (only when K64 ends mid-block, i.e. the
+  // padding past n_blocks*block): its scale is zero, nothing to add.
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
+  const int64_t rb = rb0 + wm;
 #pragma unroll
   for (int t = 0; t < 2; t++) {
     if (!colok[t]) continue;
@@ -529,10 +607,17 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   if ((rc = launch(ctx, kKernPrep, k_prep_convert, dim3((unsigned)segs, (unsigned)rblocks),
                     dim3(256), 0, d_a, lda, m, p->k, segs, (const int *)d_exp, (uint4 *)d_ap)))
     return rc;
-  const dim3 grid((unsigned)((p->n + kGemmBN - 1) / kGemmBN), (unsigned)(mpad / kGemmBM));
-  return launch(ctx, kKernGemm, k_gemm_mfma, grid, dim3(256), 0, (const uint4 *)d_ap,
-                (const int *)d_exp, segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,
-                p->n_blocks, p->block, m, p->n, d_y);
+  const int gx = (int)((p->n + kGemmBN - 1) / kGemmBN), gy = (int)(mpad / kGemmBM);
+  const int bs_log2 = ilog2(p->block);
+  const dim3 grid((unsigned)(gx * gy));
+#define MMNB_GEMM_LAUNCH(Q)                                                                   \
+  return launch(ctx, kKernGemm, k_gemm_mfma<Q>, grid, dim3(256), 0, (const uint4 *)d_ap,     \
+                (const int *)d_exp, segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,        \
+                p->n_blocks, bs_log2, m, p->n, gx, gy, d_y)
+  if (p->block >= 64) MMNB_GEMM_LAUNCH(1);
+  if (p->block == 32) MMNB_GEMM_LAUNCH(2);
+  MMNB_GEMM_LAUNCH(4);
+#undef MMNB_GEMM_LAUNCH
 }
 
 int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -108,6 +109,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
   if (!ctx) return fail(MMNB_ERR_OOM, "mmnb_init: out of host memory");
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
+  if (const char *r = std::getenv("MMNB_GEMV_R")) {
+    const int v = std::atoi(r);
+    if (v == 1 || v == 2 || v == 4 || v == 8) ctx->gemv_r = v;
+  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;
