@@ -226,6 +226,58 @@ int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int64_t
 
 typedef int int4v __attribute__((ext_vector_type(4)));
 
+// Epilogue shared by both MatMulInteger kernels: completes the row sums,
+// applies the exact integer zero-point corrections and stores int32 and/or
+// the fused fp32 rescale.  16x16 i32 accumulator layout: lane l holds column
+// l%16 and rows 4*(l/16) + r, r = 0..3.
+__device__ __forceinline__ void mmi_epilogue(
+    const int4v (&acc)[2][2], int (&rsum)[2], int a_signed, int64_t bz, int64_t M, int64_t K,
+    int64_t N, int64_t m0, int64_t n0, int lane, const int32_t *__restrict__ colsum,
+    int64_t cs_bstride, const int32_t *__restrict__ ecol, const int32_t *__restrict__ azp,
+    int64_t azp_len, int32_t *__restrict__ Y, const float *__restrict__ a_scale,
+    const float *__restrict__ b_scale, int64_t b_scale_len, float *__restrict__ Yf) {
+  const int r16 = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    rsum[t] += __shfl_xor(rsum[t], 16, 64);
+    rsum[t] += __shfl_xor(rsum[t], 32, 64);
+  }
+  const float as = Yf ? *a_scale : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    int32_t rs[4], cm[4];
+    int64_t row[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      rs[r] = __shfl(rsum[i], q * 4 + r, 64);  // lane holding that row's sum
+      row[r] = m0 + i * 16 + q * 4 + r;
+      int32_t z = 0;
+      if (azp_len == 1) z = azp[0];
+      else if (azp_len > 1 && row[r] < M) z = azp[row[r]];
+      cm[r] = (a_signed ? 0 : 128) - z;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int64_t col = n0 + j * 16 + r16;
+      if (col >= N) continue;
+      const uint32_t e = (uint32_t)ecol[col];
+      const uint32_t cs = (uint32_t)colsum[bz * cs_bstride + col];
+      float sj = 0.0f;
+      if (Yf) sj = as * b_scale[b_scale_len == 1 ? 0 : col];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        if (row[r] >= M) continue;
+        const uint32_t c = (uint32_t)cm[r];
+        const uint32_t v = (uint32_t)acc[i][j][r] + e * (uint32_t)rs[r] + c * cs +
+                           (uint32_t)K * c * e;
+        const int64_t o = (bz * M + row[r]) * N + col;
+        if (Y) Y[o] = (int32_t)v;
+        if (Yf) Yf[o] = (float)(int32_t)v * sj;
+      }
+    }
+  }
+}
+
 // WG tile 64 x 64 (4 waves, 2 x 2), wave tile 32 x 32 = 2 x 2 MFMA tiles of
 // 16 x 16; K steps of 64.  Operand lanes: l%16 = row (A) / column (B),
 // l/16 = which 16-byte quarter of the 64-k step.
@@ -306,50 +358,97 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
       for (int j = 0; j < 2; j++)
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
   }
-  // full row sums: add the four 16-byte quarters (lanes r16 + 16 q)
+  mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
+               azp_len, Y, a_scale, b_scale, b_scale_len, Yf);
+}
+
+
+// MatMulInteger with LDS staging by direct global->LDS DMA
+// (global_load_lds_dwordx4, 16 B per lane, no VGPR round trip).  Same tile
+// and arithmetic as k_mmi_mfma; the K range is staged in chunks of kMmiKc
+// bytes: the workgroup issues the whole chunk of A (64 rows) and B (64
+// columns) at once, waits, then runs the MFMAs from LDS.  LDS rows hold
+// kMmiKc/16 16-byte pieces; piece c of row r is stored at slot c ^ (r & 15)
+// so the 16 rows an MFMA operand read touches land in 16 different bank
+// groups.  Pieces past K (or rows past M) are read from a constant page whose
+// bytes become zero after the int8 offset.  Requires K % 16 == 0 and a
+// 16-byte aligned A.
+constexpr int kMmiKc = 512;
+constexpr int kMmiPieces = kMmiKc / 16;  // per row
+
+__global__ __launch_bounds__(256) void k_mmi_lds(
+    const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
+    const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
+    const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
+    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, int32_t *__restrict__ Y,
+    const float *__restrict__ a_scale, const float *__restrict__ b_scale,
+    int64_t b_scale_len, float *__restrict__ Yf, const uint8_t *__restrict__ pad) {
+  __shared__ uint4 sA[64 * kMmiPieces];
+  __shared__ uint4 sB[64 * kMmiPieces];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t bz = blockIdx.z;
+  const uint8_t *Ab = A + bz * a_bstride;
+  const int8_t *Bb = Bt + bz * b_bstride;
+  const int64_t m0 = (int64_t)blockIdx.y * 64 + wm * 32;
+  const int64_t n0 = (int64_t)blockIdx.x * 64 + wn * 32;
+  const int64_t mt0 = (int64_t)blockIdx.y * 64, nt0 = (int64_t)blockIdx.x * 64;
+  const int r16 = lane & 15, q = lane >> 4;
+  const uint32_t flip = a_signed ? 0u : 0x80808080u;
+  const uint8_t *apad = pad + (a_signed ? 0 : 1024);
+
+  int4v acc[2][2];
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
-    rsum[t] += __shfl_xor(rsum[t], 16, 64);
-    rsum[t] += __shfl_xor(rsum[t], 32, 64);
-  }
-  // Epilogue.  16x16 i32 accumulator layout: lane l holds column l%16 and
-  // rows 4*(l/16) + r, r = 0..3.
-  const float as = Yf ? *a_scale : 0.0f;
-  const int64_t Kk = K;
+  for (int i = 0; i < 2; i++)
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    int32_t rs[4], cm[4];
-    int64_t row[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int src = q * 4 + r;  // lane holding that row's sum (any quarter)
-      rs[r] = __shfl(rsum[i], src, 64);
-      row[r] = m0 + i * 16 + q * 4 + r;
-      int32_t z = 0;
-      if (azp_len == 1) z = azp[0];
-      else if (azp_len > 1 && row[r] < M) z = azp[row[r]];
-      cm[r] = (a_signed ? 0 : 128) - z;
+    for (int j = 0; j < 2; j++) acc[i][j] = (int4v){0, 0, 0, 0};
+  int rsum[2] = {0, 0};
+
+  for (int64_t k0 = 0; k0 < kpad; k0 += kMmiKc) {
+    const int64_t kc = kpad - k0 < kMmiKc ? kpad - k0 : kMmiKc;  // multiple of 64
+    // ---- DMA: 64 rows x kMmiPieces pieces each for A and B; instruction i of
+    // a wave fills LDS slots [64 i, 64 i + 64).
+    constexpr int kInstr = 64 * kMmiPieces / 64;  // per operand
+    for (int i = wave; i < kInstr; i += 4) {
+      const int slot = i * 64 + lane;
+      const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
+      const int c = cs_ ^ (r & 15);
+      const int64_t kk = k0 + (int64_t)c * 16;
+      const int64_t arow = mt0 + r;
+      const uint8_t *ga = (arow < M && kk < K) ? Ab + arow * K + kk : apad;
+      int64_t bcol = nt0 + r;
+      if (bcol >= N) bcol = N - 1;
+      const int8_t *gb = kk < kpad ? Bb + bcol * kpad + kk : (const int8_t *)pad;
+      __builtin_amdgcn_global_load_lds(ga, sA + i * 64, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gb, sB + i * 64, 16, 0, 0);
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int st = 0; st < kc / 64; st++) {
+      int4v av[2], bv[2];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int64_t col = n0 + j * 16 + r16;
-      if (col >= N) continue;
-      const uint32_t e = (uint32_t)ecol[col];
-      const uint32_t cs = (uint32_t)colsum[bz * cs_bstride + col];
-      float sj = 0.0f;
-      if (Yf) sj = as * b_scale[b_scale_len == 1 ? 0 : col];
+      for (int t = 0; t < 2; t++) {
+        const int ra = wm * 32 + t * 16 + r16;
+        const uint4 x = sA[ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
+        uint32_t w[4] = {x.x ^ flip, x.y ^ flip, x.z ^ flip, x.w ^ flip};
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        if (row[r] >= M) continue;
-        const uint32_t c = (uint32_t)cm[r];
-        const uint32_t v = (uint32_t)acc[i][j][r] + e * (uint32_t)rs[r] + c * cs +
-                           (uint32_t)Kk * c * e;
-        const int64_t o = (bz * M + row[r]) * N + col;
-        if (Y) Y[o] = (int32_t)v;
-        if (Yf) Yf[o] = (float)(int32_t)v * sj;
+        for (int d = 0; d < 4; d++)
+          rsum[t] = __builtin_amdgcn_sdot4((int)w[d], 0x01010101, rsum[t], false);
+        av[t] = (int4v){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        const int rb = wn * 32 + t * 16 + r16;
+        const uint4 y = sB[rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
+        bv[t] = (int4v){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
       }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
+    __syncthreads();
   }
+  mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
+               azp_len, Y, a_scale, b_scale, b_scale_len, Yf);
 }
 
 int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, int a_signed,
@@ -361,6 +460,13 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
   if (!d_y && !d_yf) return fail(MMNB_ERR_ARG, "MatMulInteger: no output");
   const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
+  if (fast && ctx->d_pad)
+    return launch(ctx, kKernMmi, k_mmi_lds, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
+                  a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
+                  p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad,
+                  (const int32_t *)p->d_colsum, p->batch == 1 ? (int64_t)0 : n,
+                  (const int32_t *)p->d_ecol, n, d_azp, azp_len, d_y, d_a_scale, d_b_scale,
+                  b_scale_len, d_yf, (const uint8_t *)ctx->d_pad);
   return launch(ctx, kKernMmi, k_mmi_mfma, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
                 a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                 p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, (const int32_t *)p->d_colsum,

@@ -65,6 +65,8 @@ struct mmnb_ctx {
   std::vector<hipEvent_t> tev;   // 2 per slot
   std::vector<int> tkid;         // kernel id per used slot
   size_t tused = 0;
+  // 2 KB constant page: 1 KB of 0x00 then 1 KB of 0x80 (int8 padding).
+  void *d_pad = nullptr;
   // Tuning override of the GEMV columns-per-lane R (MMNB_GEMV_R; 0 = auto).
   int gemv_r = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).

@@ -16,6 +16,9 @@ namespace mmnb {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef float f4vec __attribute__((ext_vector_type(4)));
+typedef int i4vec __attribute__((ext_vector_type(4)));
+typedef unsigned u4vec __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Repack: [N][src_col] bytes (reference layout) -> [N][dst_col] bytes with
@@ -433,16 +436,21 @@ constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 // tile 32 x 64 (one 32-row A block, two 32-column weight blocks).  Per 64-k
 // segment the workgroup stages the prepared activations (16 x 1 KB units:
 // 2 row blocks x 4 steps x hi/lo) and the packed weights (128 columns x 32 B)
-// in LDS, double-buffered: the global loads of segment s+1 are in flight
-// while segment s runs on the MFMAs.  Each 16-k step issues 2 (weight
-// blocks) x 2 (hi, lo) v_mfma_f32_32x32x16_f16 into per-block partials D; at
-// each quantisation-block boundary acc += scale[n, blk] * D.
+// in LDS (double-buffered).  The global loads run kGemmDepth-1 segments
+// ahead of the MFMAs through a ring of registers (the segment loop is
+// unrolled by the ring depth so every ring slot is a fixed register set),
+// so each segment's data has had several segments of compute time to
+// arrive.  Each 16-k step issues 2 (weight blocks) x 2 (hi, lo)
+// v_mfma_f32_32x32x16_f16 into per-block partials D; at each quantisation
+// block boundary acc += scale[n, blk] * D.
+constexpr int kGemmDepth = 4;
+
 template <int NBPS>  // quantisation blocks per 64-k segment: 1 (block >= 64), 2, 4
 __global__ __launch_bounds__(256) void k_gemm_mfma(
-    const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int64_t segs,
+    const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S,
-    const uint8_t *__restrict__ Z, int64_t nb, int bs_log2, int64_t M, int64_t N,
-    int grid_x, int grid_y, float *__restrict__ Y) {
+    const uint8_t *__restrict__ Z, int nb, int bs_log2, int M, int N, int grid_x, int grid_y,
+    float *__restrict__ Y) {
   __shared__ uint4 sA[2][16 * 64];
   __shared__ uint4 sW[2][kGemmBN * 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -460,47 +468,32 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   const int rows_in_group = min(grid_y - first_y, kGemmGroup);
   const int ty = first_y + (L % per_group) % rows_in_group;
   const int tx = (L % per_group) / rows_in_group;
+  const int rb0 = ty * 2;
+  const int n0 = tx * kGemmBN;
 
-  const int64_t rb0 = (int64_t)ty * 2;
-  const int64_t n0 = (int64_t)tx * kGemmBN;
-
-  // global -> LDS assignment
-  int64_t a_src[4];
+  // global -> register -> LDS assignment (per segment: 4 A units + 1 weight
+  // piece per thread)
+  const uint4 *a_base = Ap + (size_t)rb0 * segs * 8 * 64;
+  int a_off[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int idx = tid + 256 * i;
-    const int u = idx >> 6, l = idx & 63;
-    a_src[i] = ((rb0 + (u >> 3)) * segs * 8 + (u & 7)) * 64 + l;  // + s * 8 * 64
+    const int u = idx >> 6;
+    a_off[i] = ((u >> 3) * segs * 8 + (u & 7)) * 64 + (idx & 63);
   }
-  int64_t wcol = n0 + (tid >> 1);
-  if (wcol >= N) wcol = N - 1;
-  const uint8_t *w_src = W + wcol * col_bytes + (tid & 1) * 16;
+  const int wcol = min(n0 + (tid >> 1), N - 1);
+  const uint8_t *w_base = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
 
-  // this wave's columns / rows
-  int64_t col[2];
+  int col[2];
   bool colok[2];
+  const float *s_base[2];
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    col[t] = n0 + wn * 64 + t * 32 + cl;
-    colok[t] = col[t] < N;
-    if (!colok[t]) col[t] = N - 1;
+    const int c = n0 + wn * 64 + t * 32 + cl;
+    colok[t] = c < N;
+    col[t] = colok[t] ? c : N - 1;
+    s_base[t] = S + (size_t)col[t] * nb;
   }
-
-  auto load_scales = [&](int64_t s, float (&sc)[2][NBPS], int (&zq)[2][NBPS]) {
-#pragma unroll
-    for (int q = 0; q < NBPS; q++) {
-      const int64_t blk = (s * kSegK + q * (kSegK / NBPS)) >> bs_log2;
-      const bool inb = blk < nb;
-      const int64_t b2 = inb ? blk : nb - 1;
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
-        const int64_t zi = col[t] * nb + b2;
-        const float sv = S[zi];
-        sc[t][q] = inb ? sv : 0.0f;
-        zq[t][q] = zp_of(Z, zi);
-      }
-    }
-  };
 
   float16_t acc[2], D[2];
 #pragma unroll
@@ -511,82 +504,114 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
       D[t][r] = 0.0f;
     }
 
-  // prologue: segment 0 -> buffer 0
-  uint4 ra[4], rw;
-#pragma unroll
-  for (int i = 0; i < 4; i++) ra[i] = Ap[a_src[i]];
-  rw = *(const uint4 *)w_src;
-  float sc_cur[2][NBPS], sc_nxt[2][NBPS];
-  int zp_cur[2][NBPS], zp_nxt[2][NBPS];
-  load_scales(0, sc_cur, zp_cur);
-#pragma unroll
-  for (int i = 0; i < 4; i++) sA[0][tid + 256 * i] = ra[i];
-  sW[0][tid] = rw;
-  __syncthreads();
+  // Ring slot: ext-vector members (not arrays) so every field stays in
+  // registers even before the loops over blocks are unrolled.
+  struct Stage {
+    u4vec a0, a1, a2, a3, w;
+    f4vec sc0, sc1;
+    i4vec zp0, zp1;
+  };
+  Stage st0, st1, st2, st3;
+  const u4vec *a_vbase = (const u4vec *)a_base;
+  u4vec *sAv = (u4vec *)&sA[0][0];
+  u4vec *sWv = (u4vec *)&sW[0][0];
 
-  for (int64_t s = 0; s < segs; s++) {
-    const int buf = (int)(s & 1);
-    const bool more = s + 1 < segs;
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) ra[i] = Ap[a_src[i] + (s + 1) * 8 * 64];
-      rw = *(const uint4 *)(w_src + (s + 1) * kSegBytes);
-      load_scales(s + 1, sc_nxt, zp_nxt);
-    }
-    uint4 wv[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++) wv[t] = sW[buf][(wn * 64 + t * 32 + cl) * 2 + g];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int q = j / (4 / NBPS);
-      const half8_t ah = __builtin_bit_cast(half8_t, sA[buf][(wm * 8 + j * 2 + 0) * 64 + lane]);
-      const half8_t al = __builtin_bit_cast(half8_t, sA[buf][(wm * 8 + j * 2 + 1) * 64 + lane]);
-#pragma unroll
-      for (int t = 0; t < 2; t++) {
-        const uint32_t w = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z : wv[t].w;
-        const half8_t b = dequant8(w, zp_cur[t][q]);
-        D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[t], 0, 0, 0);
-        D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[t], 0, 0, 0);
-      }
-      // end of a quantisation block?
-      const bool boundary = (NBPS > 1) ? (((j + 1) % (4 / NBPS)) == 0)
-                                       : (j == 3 && (((s + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0);
-      if (boundary) {
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            acc[t][r] = fmaf(sc_cur[t][q], D[t][r], acc[t][r]);
-            D[t][r] = 0.0f;
-          }
-      }
-    }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) sA[buf ^ 1][tid + 256 * i] = ra[i];
-      sW[buf ^ 1][tid] = rw;
-#pragma unroll
-      for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int q = 0; q < NBPS; q++) {
-          sc_cur[t][q] = sc_nxt[t][q];
-          zp_cur[t][q] = zp_nxt[t][q];
-        }
-    }
-    __syncthreads();
+#define MMNB_ISSUE(SLOT, SEG)                                                        \
+  {                                                                                  \
+    const int sg = min((SEG), segs - 1);                                             \
+    st##SLOT.a0 = a_vbase[a_off[0] + sg * 512];                                      \
+    st##SLOT.a1 = a_vbase[a_off[1] + sg * 512];                                      \
+    st##SLOT.a2 = a_vbase[a_off[2] + sg * 512];                                      \
+    st##SLOT.a3 = a_vbase[a_off[3] + sg * 512];                                      \
+    st##SLOT.w = *(const u4vec *)(w_base + sg * kSegBytes);                          \
+    _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
+      const int blk = (sg * kSegK + q * (kSegK / NBPS)) >> bs_log2;                  \
+      const bool inb = blk < nb;                                                     \
+      const int b2 = inb ? blk : nb - 1;                                             \
+      const float sv0 = s_base[0][b2], sv1 = s_base[1][b2];                          \
+      st##SLOT.sc0[q] = inb ? sv0 : 0.0f;                                            \
+      st##SLOT.sc1[q] = inb ? sv1 : 0.0f;                                            \
+      st##SLOT.zp0[q] = zp_of(Z, (int64_t)col[0] * nb + b2);                         \
+      st##SLOT.zp1[q] = zp_of(Z, (int64_t)col[1] * nb + b2);                         \
+    }                                                                                \
   }
-  // A block still open at the end (only when K64 ends mid-block, i.e. the
-  // padding past n_blocks*block): its scale is zero, nothing to add.
+#define MMNB_STORE(SLOT, BUF)                                                        \
+  {                                                                                  \
+    sAv[(BUF) * 1024 + tid] = st##SLOT.a0;                                           \
+    sAv[(BUF) * 1024 + tid + 256] = st##SLOT.a1;                                     \
+    sAv[(BUF) * 1024 + tid + 512] = st##SLOT.a2;                                     \
+    sAv[(BUF) * 1024 + tid + 768] = st##SLOT.a3;                                     \
+    sWv[(BUF) * 256 + tid] = st##SLOT.w;                                             \
+  }
+#define MMNB_COMPUTE(SEG, BUF, SLOT)                                                 \
+  {                                                                                  \
+    uint4 wv[2];                                                                     \
+    _Pragma("unroll") for (int t = 0; t < 2; t++) wv[t] =                            \
+        sW[BUF][(wn * 64 + t * 32 + cl) * 2 + g];                                    \
+    _Pragma("unroll") for (int j = 0; j < 4; j++) {                                  \
+      const int q = j / (4 / NBPS);                                                  \
+      const half8_t ah =                                                             \
+          __builtin_bit_cast(half8_t, sA[BUF][(wm * 8 + j * 2 + 0) * 64 + lane]);    \
+      const half8_t al =                                                             \
+          __builtin_bit_cast(half8_t, sA[BUF][(wm * 8 + j * 2 + 1) * 64 + lane]);    \
+      _Pragma("unroll") for (int t = 0; t < 2; t++) {                                \
+        const uint32_t w = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z    \
+                                                                    : wv[t].w;       \
+        const half8_t b = dequant8(w, t == 0 ? st##SLOT.zp0[q] : st##SLOT.zp1[q]);  \
+        D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[t], 0, 0, 0);         \
+        D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[t], 0, 0, 0);         \
+      }                                                                              \
+      const bool boundary =                                                          \
+          (NBPS > 1) ? (((j + 1) % (4 / NBPS)) == 0)                                 \
+                     : (j == 3 && ((((SEG) + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0); \
+      if (boundary) {                                                                \
+        _Pragma("unroll") for (int t = 0; t < 2; t++)                                \
+            _Pragma("unroll") for (int r = 0; r < 16; r++) {                         \
+          acc[t][r] = fmaf(t == 0 ? st##SLOT.sc0[q] : st##SLOT.sc1[q], D[t][r],      \
+                           acc[t][r]);                                               \
+          D[t][r] = 0.0f;                                                            \
+        }                                                                            \
+      }                                                                              \
+    }                                                                                \
+  }
+// SUB(D0, ISSUE_SLOT, NEXT_SLOT): ring slots are literal tokens
+#define MMNB_SUB(D0, ISLOT, NSLOT)                                                   \
+  {                                                                                  \
+    const int s = s0 + (D0);                                                         \
+    if (s < segs) {                                                                  \
+      MMNB_ISSUE(ISLOT, s + kGemmDepth - 1);                                         \
+      MMNB_COMPUTE(s, (D0) & 1, D0);                                                 \
+      if (s + 1 < segs) MMNB_STORE(NSLOT, ((D0) + 1) & 1);                           \
+      __syncthreads();                                                               \
+    }                                                                                \
+  }
+
+  // prologue: segments 0..depth-2 in flight, segment 0 staged
+  MMNB_ISSUE(0, 0);
+  MMNB_ISSUE(1, 1);
+  MMNB_ISSUE(2, 2);
+  MMNB_STORE(0, 0);
+  __syncthreads();
+  for (int s0 = 0; s0 < segs; s0 += kGemmDepth) {
+    MMNB_SUB(0, 3, 1);
+    MMNB_SUB(1, 0, 2);
+    MMNB_SUB(2, 1, 3);
+    MMNB_SUB(3, 2, 0);
+  }
+#undef MMNB_SUB
+#undef MMNB_COMPUTE
+#undef MMNB_STORE
+#undef MMNB_ISSUE
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
-  const int64_t rb = rb0 + wm;
+  const int rb = rb0 + wm;
 #pragma unroll
   for (int t = 0; t < 2; t++) {
     if (!colok[t]) continue;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int64_t row = rb * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-      if (row < M) Y[row * N + col[t]] = ldexpf(acc[t][r], -row_exp[row]);
+      const int row = rb * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+      if (row < M) Y[(size_t)row * N + col[t]] = ldexpf(acc[t][r], -row_exp[row]);
     }
   }
 }
@@ -612,8 +637,8 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   const dim3 grid((unsigned)(gx * gy));
 #define MMNB_GEMM_LAUNCH(Q)                                                                   \
   return launch(ctx, kKernGemm, k_gemm_mfma<Q>, grid, dim3(256), 0, (const uint4 *)d_ap,     \
-                (const int *)d_exp, segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,        \
-                p->n_blocks, bs_log2, m, p->n, gx, gy, d_y)
+                (const int *)d_exp, (int)segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,  \
+                (int)p->n_blocks, bs_log2, (int)m, (int)p->n, gx, gy, d_y)
   if (p->block >= 64) MMNB_GEMM_LAUNCH(1);
   if (p->block == 32) MMNB_GEMM_LAUNCH(2);
   MMNB_GEMM_LAUNCH(4);

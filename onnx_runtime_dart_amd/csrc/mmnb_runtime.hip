@@ -125,6 +125,13 @@ int mmnb_init(int device, mmnb_ctx **out) {
       return check_hip(e, "hipEventCreate");
     }
   }
+  e = hipMalloc(&ctx->d_pad, 2048);
+  if (e == hipSuccess) e = hipMemset(ctx->d_pad, 0, 1024);
+  if (e == hipSuccess) e = hipMemset((char *)ctx->d_pad + 1024, 0x80, 1024);
+  if (e != hipSuccess) {
+    delete ctx;
+    return check_hip(e, "hipMalloc(pad page)");
+  }
   *out = ctx;
   return MMNB_OK;
 }
@@ -140,6 +147,7 @@ int mmnb_shutdown(mmnb_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (auto &s : ctx->scratch)
       if (s.ptr) (void)hipFree(s.ptr);
+    if (ctx->d_pad) (void)hipFree(ctx->d_pad);
     for (auto &ev : ctx->events)
       if (ev) (void)hipEventDestroy(ev);
     for (auto &ev : ctx->tev) (void)hipEventDestroy(ev);
