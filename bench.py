@@ -240,6 +240,27 @@ def cpu_baseline(synth, m, k, n, bs, zp, budget_s):
                              "ms_per_call": float(np.min(tmt)) * 1e3}}
 
 
+def profile_pass(ctx, lib, ops, synth):
+    """Kernels for a rocprofv3 counter run: the headline GEMV and a copy of
+    known size (the calibration reference for FETCH_SIZE / WRITE_SIZE)."""
+    m, k, n, bs = 1, 4096, 4096, 128
+    count = int(np.ceil(ROTATE_BYTES / (k * n // 2 + n * (k // bs) * 4)))
+    packs = make_packs(ctx, ops, synth, m, k, n, bs, False, count, 1)
+    da = ctx.to_device(synth.activations(m, k, 1))
+    dy = ctx.alloc(m * n * 4)
+    for i in range(100):
+        lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, packs[i % count].handle, da.ptr, m,
+                                                dy.ptr))
+    ctx.synchronize()
+    nbytes = 64 << 20
+    src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    for _ in range(10):
+        lib.check(ctx.lib.mmnb_memcpy_d2d(ctx.handle, dst.ptr, src.ptr, nbytes))
+    ctx.synchronize()
+    print(f"# profile pass: {100} GEMV calls ({mmnb_bytes(m, k, n, bs, False)} algorithmic "
+          f"bytes each), 10 copies of {nbytes} bytes", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,6 +268,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=216)
     ap.add_argument("--quick", action="store_true", help="headline only, no extras")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--profile", action="store_true",
+                    help="counter pass for rocprofv3: the headline GEMV (100 calls over the "
+                         "rotated packs) and a 64 MiB device-to-device copy (10 calls) as the "
+                         "counter calibration; prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs the kernel on a single "
@@ -256,6 +281,9 @@ def main():
     from onnx_runtime_dart_amd import _lib as lib, ops, synth
 
     ctx = lib.default_context()
+    if args.profile:
+        profile_pass(ctx, lib, ops, synth)
+        return
     info = ctx.info()
     print(f"# device {info}", file=sys.stderr, flush=True)
 

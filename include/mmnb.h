@@ -195,6 +195,7 @@ int mmnb_device_free(mmnb_ctx *ctx, void *d_ptr);
 int mmnb_memcpy_h2d(mmnb_ctx *ctx, void *d_dst, const void *src, size_t bytes);
 int mmnb_memcpy_d2h(mmnb_ctx *ctx, void *dst, const void *d_src, size_t bytes);
 int mmnb_memset_dev(mmnb_ctx *ctx, void *d_dst, int value, size_t bytes);
+int mmnb_memcpy_d2d(mmnb_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
 int mmnb_synchronize(mmnb_ctx *ctx);
 
 /* Record timing event `slot` (0..15) on the context stream; read the

@@ -49,6 +49,7 @@ SIGNATURES = {
     "mmnb_memcpy_h2d": (_int, [_vp, _vp, _vp, _sz]),
     "mmnb_memcpy_d2h": (_int, [_vp, _vp, _vp, _sz]),
     "mmnb_memset_dev": (_int, [_vp, _vp, _int, _sz]),
+    "mmnb_memcpy_d2d": (_int, [_vp, _vp, _vp, _sz]),
     "mmnb_synchronize": (_int, [_vp]),
     "mmnb_event_record": (_int, [_vp, _int]),
     "mmnb_event_elapsed_ms": (_int, [_vp, _int, _int, _P(ctypes.c_float)]),

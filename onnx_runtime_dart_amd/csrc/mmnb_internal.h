@@ -83,7 +83,8 @@ struct mmnb_pack {
   int64_t col_bytes = 0;  // bytes per column in d_w (= k64 / 2)
   uint8_t *d_w = nullptr;
   float *d_scales = nullptr;
-  uint8_t *d_zp = nullptr;
+  uint8_t *d_zp = nullptr;  // packed uint4; 0x88 filler when the op has none
+  bool has_zp = false;
   // --- MatMulInteger
   int64_t batch = 0;
   int64_t kpad = 0;          // k padded to a multiple of 64

@@ -20,6 +20,14 @@ typedef float f4vec __attribute__((ext_vector_type(4)));
 typedef int i4vec __attribute__((ext_vector_type(4)));
 typedef unsigned u4vec __attribute__((ext_vector_type(4)));
 
+// Zero point of flat (column, block) index zi.  Z is never null: packs
+// without zero points carry a buffer of 0x88 (8 in both nibbles), so the
+// load is unconditional (a conditional load ends in a full vmcnt wait).
+__device__ __forceinline__ int zp_of(const uint8_t *__restrict__ Z, int64_t zi) {
+  const uint32_t zb = Z[zi >> 1];
+  return (int)((zb >> ((zi & 1) * 4)) & 0xF);
+}
+
 // ---------------------------------------------------------------------------
 // Repack: [N][src_col] bytes (reference layout) -> [N][dst_col] bytes with
 // the per-32-byte dword permutation d0 d2 d4 d6 | d1 d3 d5 d7.  Nibbles with
@@ -109,7 +117,7 @@ __device__ __forceinline__ float half_wave_sum(float v) {
 
 constexpr int kGemvMaxWaves = 4;
 
-template <int M, int R, int NBPC>
+template <int M, int R, int NBPC, bool HAS_ZP>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     const float *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W,
     int64_t col_bytes, const float *__restrict__ S, const uint8_t *__restrict__ Z, int nb,
@@ -144,25 +152,25 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
 #pragma unroll
     for (int r = 0; r < R; r++)
       wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
-    float sc[R][NBPC], sz[R][NBPC];
+    // raw scale / zero-point loads (no arithmetic on loaded values here, so
+    // the loads stay in flight together)
+    float sraw[R][NBPC];
+    uint32_t zraw[R][NBPC];
+    bool inbq[NBPC];
+    int zsh[R][NBPC];
 #pragma unroll
     for (int q = 0; q < NBPC; q++) {
       // block of dwords j in [q*4/NBPC, (q+1)*4/NBPC)
       const int kq = s * kSegK + 16 * (q * (4 / NBPC)) + (NBPC == 4 ? 8 * g : 0);
       int blk = kq >> bs_log2;
-      const bool inb = cv && blk < nb;
+      inbq[q] = cv && blk < nb;
       blk = blk < nb ? blk : nb - 1;
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const int zi = colr[r] * nb + blk;
-        const float sv = S[zi];
-        int zpv = 8;
-        if (Z) {
-          const uint8_t zb = Z[zi >> 1];
-          zpv = (zi & 1) ? (zb >> 4) : (zb & 0xF);
-        }
-        sc[r][q] = inb ? sv : 0.0f;
-        sz[r][q] = inb ? sv * (float)zpv : 0.0f;
+        sraw[r][q] = S[zi];
+        if (HAS_ZP) zraw[r][q] = Z[zi >> 1];
+        zsh[r][q] = (zi & 1) * 4;
       }
     }
     float av[M][32];
@@ -186,6 +194,15 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
       }
     }
     // ---- arithmetic
+    float sc[R][NBPC], sz[R][NBPC];
+#pragma unroll
+    for (int q = 0; q < NBPC; q++)
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int zpv = HAS_ZP ? (int)((zraw[r][q] >> zsh[r][q]) & 0xF) : 8;
+        sc[r][q] = inbq[q] ? sraw[r][q] : 0.0f;
+        sz[r][q] = inbq[q] ? sraw[r][q] * (float)zpv : 0.0f;
+      }
     float sa[M][NBPC];
 #pragma unroll
     for (int m = 0; m < M; m++)
@@ -254,8 +271,13 @@ static int launch_gemv_mr(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const 
                           int fast, int bs_log2) {
   const int nb = (int)p->n_blocks, K = (int)p->k, N = (int)p->n;
 #define MMNB_GEMV_LAUNCH(Q)                                                                  \
-  return launch(ctx, kKernGemv, k_gemv_valu<M, R, Q>, grid, block, 0, A, lda, p->d_w,      \
-                p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C, iters, fast)
+  return p->has_zp                                                                         \
+             ? launch(ctx, kKernGemv, k_gemv_valu<M, R, Q, true>, grid, block, 0, A, lda,    \
+                      p->d_w, p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C,  \
+                      iters, fast)                                                          \
+             : launch(ctx, kKernGemv, k_gemv_valu<M, R, Q, false>, grid, block, 0, A, lda,   \
+                      p->d_w, p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C,  \
+                      iters, fast)
   if (nbpc == 4) MMNB_GEMV_LAUNCH(4);
   if (nbpc == 2) MMNB_GEMV_LAUNCH(2);
   MMNB_GEMV_LAUNCH(1);
@@ -422,11 +444,6 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp) {
   return r;
 }
 
-__device__ __forceinline__ int zp_of(const uint8_t *__restrict__ Z, int64_t zi) {
-  if (!Z) return 8;
-  const uint8_t zb = Z[zi >> 1];
-  return (zi & 1) ? (zb >> 4) : (zb & 0xF);
-}
 
 constexpr int kGemmBM = 64;   // two 32-row blocks
 constexpr int kGemmBN = 128;  // four 32-column blocks
@@ -447,7 +464,7 @@ constexpr int kGemmDepth = 4;
 
 template <int NBPS>  // quantisation blocks per 64-k segment: 1 (block >= 64), 2, 4
 __global__ __launch_bounds__(256) void k_gemm_mfma(
-    const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs,
+    const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs, int segs4,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S,
     const uint8_t *__restrict__ Z, int nb, int bs_log2, int M, int N, int grid_x, int grid_y,
     float *__restrict__ Y) {
@@ -473,13 +490,15 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
 
   // global -> register -> LDS assignment (per segment: 4 A units + 1 weight
   // piece per thread)
-  const uint4 *a_base = Ap + (size_t)rb0 * segs * 8 * 64;
+  // The prepared activations hold segs4 (a multiple of kGemmDepth) segments,
+  // zero past K, so the pipelined loop below runs without guards.
+  const uint4 *a_base = Ap + (size_t)rb0 * segs4 * 8 * 64;
   int a_off[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int idx = tid + 256 * i;
     const int u = idx >> 6;
-    a_off[i] = ((u >> 3) * segs * 8 + (u & 7)) * 64 + (idx & 63);
+    a_off[i] = ((u >> 3) * segs4 * 8 + (u & 7)) * 64 + (idx & 63);
   }
   const int wcol = min(n0 + (tid >> 1), N - 1);
   const uint8_t *w_base = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
@@ -508,8 +527,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   // registers even before the loops over blocks are unrolled.
   struct Stage {
     u4vec a0, a1, a2, a3, w;
-    f4vec sc0, sc1;
-    i4vec zp0, zp1;
+    f4vec sc0, sc1;   // raw scale loads
+    u4vec zb0, zb1;   // raw zero-point bytes
   };
   Stage st0, st1, st2, st3;
   const u4vec *a_vbase = (const u4vec *)a_base;
@@ -518,21 +537,21 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
 
 #define MMNB_ISSUE(SLOT, SEG)                                                        \
   {                                                                                  \
+    const int sa_ = min((SEG), segs4 - 1);                                           \
     const int sg = min((SEG), segs - 1);                                             \
-    st##SLOT.a0 = a_vbase[a_off[0] + sg * 512];                                      \
-    st##SLOT.a1 = a_vbase[a_off[1] + sg * 512];                                      \
-    st##SLOT.a2 = a_vbase[a_off[2] + sg * 512];                                      \
-    st##SLOT.a3 = a_vbase[a_off[3] + sg * 512];                                      \
+    st##SLOT.a0 = a_vbase[a_off[0] + sa_ * 512];                                     \
+    st##SLOT.a1 = a_vbase[a_off[1] + sa_ * 512];                                     \
+    st##SLOT.a2 = a_vbase[a_off[2] + sa_ * 512];                                     \
+    st##SLOT.a3 = a_vbase[a_off[3] + sa_ * 512];                                     \
     st##SLOT.w = *(const u4vec *)(w_base + sg * kSegBytes);                          \
+    /* loads only: arithmetic on loaded values waits for them */                   \
     _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
-      const int blk = (sg * kSegK + q * (kSegK / NBPS)) >> bs_log2;                  \
-      const bool inb = blk < nb;                                                     \
-      const int b2 = inb ? blk : nb - 1;                                             \
-      const float sv0 = s_base[0][b2], sv1 = s_base[1][b2];                          \
-      st##SLOT.sc0[q] = inb ? sv0 : 0.0f;                                            \
-      st##SLOT.sc1[q] = inb ? sv1 : 0.0f;                                            \
-      st##SLOT.zp0[q] = zp_of(Z, (int64_t)col[0] * nb + b2);                         \
-      st##SLOT.zp1[q] = zp_of(Z, (int64_t)col[1] * nb + b2);                         \
+      const int blk = (sa_ * kSegK + q * (kSegK / NBPS)) >> bs_log2;                 \
+      const int b2 = blk < nb ? blk : nb - 1;                                        \
+      st##SLOT.sc0[q] = s_base[0][b2];                                               \
+      st##SLOT.sc1[q] = s_base[1][b2];                                               \
+      st##SLOT.zb0[q] = Z[(col[0] * nb + b2) >> 1];                                  \
+      st##SLOT.zb1[q] = Z[(col[1] * nb + b2) >> 1];                                  \
     }                                                                                \
   }
 #define MMNB_STORE(SLOT, BUF)                                                        \
@@ -545,6 +564,18 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   }
 #define MMNB_COMPUTE(SEG, BUF, SLOT)                                                 \
   {                                                                                  \
+    int zpv0[NBPS], zpv1[NBPS];                                                      \
+    float scv0[NBPS], scv1[NBPS];                                                    \
+    _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
+      const int blk = ((SEG) * kSegK + q * (kSegK / NBPS)) >> bs_log2;               \
+      const bool inb = blk < nb;                                                     \
+      const int b2 = inb ? blk : nb - 1;                                             \
+      const int sh0 = ((col[0] * nb + b2) & 1) * 4, sh1 = ((col[1] * nb + b2) & 1) * 4; \
+      zpv0[q] = (int)((st##SLOT.zb0[q] >> sh0) & 0xF);                               \
+      zpv1[q] = (int)((st##SLOT.zb1[q] >> sh1) & 0xF);                               \
+      scv0[q] = inb ? st##SLOT.sc0[q] : 0.0f;                                        \
+      scv1[q] = inb ? st##SLOT.sc1[q] : 0.0f;                                        \
+    }                                                                                \
     uint4 wv[2];                                                                     \
     _Pragma("unroll") for (int t = 0; t < 2; t++) wv[t] =                            \
         sW[BUF][(wn * 64 + t * 32 + cl) * 2 + g];                                    \
@@ -557,7 +588,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
       _Pragma("unroll") for (int t = 0; t < 2; t++) {                                \
         const uint32_t w = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z    \
                                                                     : wv[t].w;       \
-        const half8_t b = dequant8(w, t == 0 ? st##SLOT.zp0[q] : st##SLOT.zp1[q]);  \
+        const half8_t b = dequant8(w, t == 0 ? zpv0[q] : zpv1[q]);                   \
         D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[t], 0, 0, 0);         \
         D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[t], 0, 0, 0);         \
       }                                                                              \
@@ -567,8 +598,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
       if (boundary) {                                                                \
         _Pragma("unroll") for (int t = 0; t < 2; t++)                                \
             _Pragma("unroll") for (int r = 0; r < 16; r++) {                         \
-          acc[t][r] = fmaf(t == 0 ? st##SLOT.sc0[q] : st##SLOT.sc1[q], D[t][r],      \
-                           acc[t][r]);                                               \
+          acc[t][r] = fmaf(t == 0 ? scv0[q] : scv1[q], D[t][r], acc[t][r]);          \
           D[t][r] = 0.0f;                                                            \
         }                                                                            \
       }                                                                              \
@@ -578,12 +608,10 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
 #define MMNB_SUB(D0, ISLOT, NSLOT)                                                   \
   {                                                                                  \
     const int s = s0 + (D0);                                                         \
-    if (s < segs) {                                                                  \
-      MMNB_ISSUE(ISLOT, s + kGemmDepth - 1);                                         \
-      MMNB_COMPUTE(s, (D0) & 1, D0);                                                 \
-      if (s + 1 < segs) MMNB_STORE(NSLOT, ((D0) + 1) & 1);                           \
-      __syncthreads();                                                               \
-    }                                                                                \
+    MMNB_ISSUE(ISLOT, s + kGemmDepth - 1);                                           \
+    MMNB_COMPUTE(s, (D0) & 1, D0);                                                   \
+    MMNB_STORE(NSLOT, ((D0) + 1) & 1);                                               \
+    __syncthreads();                                                                 \
   }
 
   // prologue: segments 0..depth-2 in flight, segment 0 staged
@@ -592,7 +620,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   MMNB_ISSUE(2, 2);
   MMNB_STORE(0, 0);
   __syncthreads();
-  for (int s0 = 0; s0 < segs; s0 += kGemmDepth) {
+  for (int s0 = 0; s0 < segs4; s0 += kGemmDepth) {
     MMNB_SUB(0, 3, 1);
     MMNB_SUB(1, 0, 2);
     MMNB_SUB(2, 1, 3);
@@ -619,9 +647,10 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
 static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y) {
   const int64_t segs = p->k64 / kSegK;
+  const int64_t segs4 = (segs + kGemmDepth - 1) / kGemmDepth * kGemmDepth;
   const int64_t mpad = (m + kGemmBM - 1) / kGemmBM * kGemmBM;
   const int64_t rblocks = mpad / 32;
-  const size_t ap_bytes = (size_t)(rblocks * segs * 4 * 2 * 64) * 16;
+  const size_t ap_bytes = (size_t)(rblocks * segs4 * 4 * 2 * 64) * 16;
   void *d_ap = nullptr, *d_exp = nullptr;
   int rc;
   if ((rc = scratch_get(ctx, 2, ap_bytes, &d_ap))) return rc;
@@ -629,15 +658,16 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   if ((rc = launch(ctx, kKernPrep, k_prep_rowexp, dim3((unsigned)((m + 3) / 4)), dim3(256), 0,
                     d_a, lda, m, p->k, (int *)d_exp)))
     return rc;
-  if ((rc = launch(ctx, kKernPrep, k_prep_convert, dim3((unsigned)segs, (unsigned)rblocks),
-                    dim3(256), 0, d_a, lda, m, p->k, segs, (const int *)d_exp, (uint4 *)d_ap)))
+  if ((rc = launch(ctx, kKernPrep, k_prep_convert, dim3((unsigned)segs4, (unsigned)rblocks),
+                    dim3(256), 0, d_a, lda, m, p->k, segs4, (const int *)d_exp, (uint4 *)d_ap)))
     return rc;
   const int gx = (int)((p->n + kGemmBN - 1) / kGemmBN), gy = (int)(mpad / kGemmBM);
   const int bs_log2 = ilog2(p->block);
   const dim3 grid((unsigned)(gx * gy));
 #define MMNB_GEMM_LAUNCH(Q)                                                                   \
   return launch(ctx, kKernGemm, k_gemm_mfma<Q>, grid, dim3(256), 0, (const uint4 *)d_ap,     \
-                (const int *)d_exp, (int)segs, p->d_w, p->col_bytes, p->d_scales, p->d_zp,  \
+                (const int *)d_exp, (int)segs, (int)segs4, p->d_w, p->col_bytes,            \
+                p->d_scales, p->d_zp,                                                         \
                 (int)p->n_blocks, bs_log2, (int)m, (int)p->n, gx, gy, d_y)
   if (p->block >= 64) MMNB_GEMM_LAUNCH(1);
   if (p->block == 32) MMNB_GEMM_LAUNCH(2);

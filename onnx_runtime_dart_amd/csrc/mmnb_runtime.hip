@@ -227,7 +227,8 @@ int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
   const size_t wbytes = (size_t)(n * p->col_bytes);
   if ((rc = device_alloc(wbytes, (void **)&p->d_w))) return cleanup(rc);
   if ((rc = device_alloc((size_t)(n * nb) * 4, (void **)&p->d_scales))) return cleanup(rc);
-  if (zero_points && (rc = device_alloc((size_t)zp_need, (void **)&p->d_zp))) return cleanup(rc);
+  p->has_zp = zero_points != nullptr;
+  if ((rc = device_alloc((size_t)zp_need, (void **)&p->d_zp))) return cleanup(rc);
   // Upload the raw B into scratch, repack on the device.
   void *d_raw = nullptr;
   if ((rc = scratch_get(ctx, 4, (size_t)(n * src_col), &d_raw))) return cleanup(rc);
@@ -245,10 +246,12 @@ int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
     if ((e = hipMemcpyAsync(p->d_zp, zero_points, (size_t)zp_need, hipMemcpyHostToDevice,
                             ctx->stream)) != hipSuccess)
       return cleanup(check_hip(e, "hipMemcpyAsync(zero_points)"));
+  } else if ((e = hipMemsetAsync(p->d_zp, 0x88, (size_t)zp_need, ctx->stream)) != hipSuccess) {
+    return cleanup(check_hip(e, "hipMemsetAsync(zero_points)"));
   }
   if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
     return cleanup(check_hip(e, "hipStreamSynchronize(pack)"));
-  p->bytes = (int64_t)wbytes + n * nb * 4 + (zero_points ? zp_need : 0);
+  p->bytes = (int64_t)wbytes + n * nb * 4 + zp_need;
   ctx->live_packs++;
   *out = p;
   return MMNB_OK;
@@ -592,6 +595,15 @@ int mmnb_memcpy_d2h(mmnb_ctx *ctx, void *dst, const void *d_src, size_t bytes) {
     MMNB_HIP(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
     MMNB_HIP(hipStreamSynchronize(ctx->stream));
   }
+  return MMNB_OK;
+}
+
+int mmnb_memcpy_d2d(mmnb_ctx *ctx, void *d_dst, const void *d_src, size_t bytes) {
+  MMNB_GUARD_CTX(ctx);
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  if (bytes) MMNB_HIP(hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
   return MMNB_OK;
 }
 
