@@ -31,6 +31,8 @@ def build(verbose=False):
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
            "-Wall", "-Wno-unused-function",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           # MFMA results in VGPRs, so epilogue FMAs need no v_accvgpr_read
+           "-mllvm", "-amdgpu-mfma-vgpr-form",
            "-o", str(out_tmp)] + [str(CSRC / s) for s in SOURCES]
     if verbose:
         print(" ".join(cmd), flush=True)

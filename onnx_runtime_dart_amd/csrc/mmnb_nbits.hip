@@ -425,12 +425,27 @@ __global__ __launch_bounds__(256) void k_prep_convert(
 // at each quantisation-block boundary acc += scale[n, blk] * D.  The 16-byte
 // weight load of a lane covers four 16-k steps (one 64-k segment).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ half8_t dequant8(uint32_t w, int zp) {
-  const uint32_t t0 = (w & 0x000F000Fu) | 0x64006400u;
-  const uint32_t t1 = (w & 0x00F000F0u) | 0x64006400u;
+// (a & mask) | orv in one VALU op.  gfx9 VOP3 takes no literal, so the
+// compiler splits this into v_and + v_or; with the mask in an SGPR and the
+// magic in a VGPR it is one v_and_or_b32.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(orv));
+  return r;
+}
+
+// 8 nibbles of one dword -> 8 fp16 values (q - zp), exact.  (q | 0x6400)
+// as fp16 is 1024 + q; (16q | 0x6400) is 1024 + 16q, so
+//   lo nibble pairs: (1024 + q) - (1024 + zp)
+//   hi nibble pairs: (1024 + 16q) / 16 - (64 + zp)
+// Output order {n0, n4, n1, n5, n2, n6, n3, n7}; the prepared activations
+// use the same k permutation.
+__device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) {
+  const uint32_t t0 = and_or(w, 0x000F000Fu, magic);
+  const uint32_t t1 = and_or(w, 0x00F000F0u, magic);
   const uint32_t w8 = w >> 8;
-  const uint32_t t2 = (w8 & 0x000F000Fu) | 0x64006400u;
-  const uint32_t t3 = (w8 & 0x00F000F0u) | 0x64006400u;
+  const uint32_t t2 = and_or(w8, 0x000F000Fu, magic);
+  const uint32_t t3 = and_or(w8, 0x00F000F0u, magic);
   const _Float16 z1024 = (_Float16)(1024 + zp);
   const _Float16 z64 = (_Float16)(64 + zp);
   const half2_t zz = {z1024, z1024};
@@ -444,13 +459,13 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp) {
   return r;
 }
 
-
 constexpr int kGemmBM = 64;   // two 32-row blocks
 constexpr int kGemmBN = 128;  // four 32-column blocks
 constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 
-// Prefill GEMM.  Workgroup tile 64 (M) x 128 (N), 4 waves in 2 x 2, wave
-// tile 32 x 64 (one 32-row A block, two 32-column weight blocks).  Per 64-k
+// Prefill GEMM.  Workgroup tile 64 (M) x 128 (N), 4 waves in 1 x 4, wave
+// tile 64 x 32 (both 32-row A blocks, one 32-column weight block, so every
+// weight is dequantised once per workgroup).  Per 64-k
 // segment the workgroup stages the prepared activations (16 x 1 KB units:
 // 2 row blocks x 4 steps x hi/lo) and the packed weights (128 columns x 32 B)
 // in LDS (double-buffered).  The global loads run kGemmDepth-1 segments
@@ -471,8 +486,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   __shared__ uint4 sA[2][16 * 64];
   __shared__ uint4 sW[2][kGemmBN * 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
   const int cl = lane & 31, g = lane >> 5;
+  const uint32_t magic = 0x64006400u;
 
   // XCD-aware tile order: consecutive workgroup ids go to different XCDs
   // (round robin), so regroup them into contiguous chunks per XCD, then walk
@@ -503,16 +518,11 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   const int wcol = min(n0 + (tid >> 1), N - 1);
   const uint8_t *w_base = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
 
-  int col[2];
-  bool colok[2];
-  const float *s_base[2];
-#pragma unroll
-  for (int t = 0; t < 2; t++) {
-    const int c = n0 + wn * 64 + t * 32 + cl;
-    colok[t] = c < N;
-    col[t] = colok[t] ? c : N - 1;
-    s_base[t] = S + (size_t)col[t] * nb;
-  }
+  // this lane's output column
+  const int ccol = n0 + wave * 32 + cl;
+  const bool colok = ccol < N;
+  const int col = colok ? ccol : N - 1;
+  const float *s_base = S + (size_t)col * nb;
 
   float16_t acc[2], D[2];
 #pragma unroll
@@ -527,8 +537,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   // registers even before the loops over blocks are unrolled.
   struct Stage {
     u4vec a0, a1, a2, a3, w;
-    f4vec sc0, sc1;   // raw scale loads
-    u4vec zb0, zb1;   // raw zero-point bytes
+    f4vec sc;  // raw scale loads
+    u4vec zb;  // raw zero-point bytes
   };
   Stage st0, st1, st2, st3;
   const u4vec *a_vbase = (const u4vec *)a_base;
@@ -548,10 +558,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
     _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
       const int blk = (sa_ * kSegK + q * (kSegK / NBPS)) >> bs_log2;                 \
       const int b2 = blk < nb ? blk : nb - 1;                                        \
-      st##SLOT.sc0[q] = s_base[0][b2];                                               \
-      st##SLOT.sc1[q] = s_base[1][b2];                                               \
-      st##SLOT.zb0[q] = Z[(col[0] * nb + b2) >> 1];                                  \
-      st##SLOT.zb1[q] = Z[(col[1] * nb + b2) >> 1];                                  \
+      st##SLOT.sc[q] = s_base[b2];                                                   \
+      st##SLOT.zb[q] = Z[(col * nb + b2) >> 1];                                      \
     }                                                                                \
   }
 #define MMNB_STORE(SLOT, BUF)                                                        \
@@ -564,42 +572,35 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   }
 #define MMNB_COMPUTE(SEG, BUF, SLOT)                                                 \
   {                                                                                  \
-    int zpv0[NBPS], zpv1[NBPS];                                                      \
-    float scv0[NBPS], scv1[NBPS];                                                    \
+    int zpv[NBPS];                                                                   \
+    float scv[NBPS];                                                                 \
     _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
       const int blk = ((SEG) * kSegK + q * (kSegK / NBPS)) >> bs_log2;               \
       const bool inb = blk < nb;                                                     \
       const int b2 = inb ? blk : nb - 1;                                             \
-      const int sh0 = ((col[0] * nb + b2) & 1) * 4, sh1 = ((col[1] * nb + b2) & 1) * 4; \
-      zpv0[q] = (int)((st##SLOT.zb0[q] >> sh0) & 0xF);                               \
-      zpv1[q] = (int)((st##SLOT.zb1[q] >> sh1) & 0xF);                               \
-      scv0[q] = inb ? st##SLOT.sc0[q] : 0.0f;                                        \
-      scv1[q] = inb ? st##SLOT.sc1[q] : 0.0f;                                        \
+      zpv[q] = (int)((st##SLOT.zb[q] >> (((col * nb + b2) & 1) * 4)) & 0xF);         \
+      scv[q] = inb ? st##SLOT.sc[q] : 0.0f;                                          \
     }                                                                                \
-    uint4 wv[2];                                                                     \
-    _Pragma("unroll") for (int t = 0; t < 2; t++) wv[t] =                            \
-        sW[BUF][(wn * 64 + t * 32 + cl) * 2 + g];                                    \
+    const u4vec wv = sWv[(BUF) * 256 + (wave * 32 + cl) * 2 + g];                    \
     _Pragma("unroll") for (int j = 0; j < 4; j++) {                                  \
       const int q = j / (4 / NBPS);                                                  \
-      const half8_t ah =                                                             \
-          __builtin_bit_cast(half8_t, sA[BUF][(wm * 8 + j * 2 + 0) * 64 + lane]);    \
-      const half8_t al =                                                             \
-          __builtin_bit_cast(half8_t, sA[BUF][(wm * 8 + j * 2 + 1) * 64 + lane]);    \
-      _Pragma("unroll") for (int t = 0; t < 2; t++) {                                \
-        const uint32_t w = j == 0 ? wv[t].x : j == 1 ? wv[t].y : j == 2 ? wv[t].z    \
-                                                                    : wv[t].w;       \
-        const half8_t b = dequant8(w, t == 0 ? zpv0[q] : zpv1[q]);                   \
-        D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[t], 0, 0, 0);         \
-        D[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[t], 0, 0, 0);         \
+      const half8_t b = dequant8(wv[j], zpv[q], magic);                              \
+      _Pragma("unroll") for (int rb = 0; rb < 2; rb++) {                             \
+        const half8_t ah = __builtin_bit_cast(                                       \
+            half8_t, sAv[(BUF) * 1024 + (rb * 8 + j * 2 + 0) * 64 + lane]);          \
+        const half8_t al = __builtin_bit_cast(                                       \
+            half8_t, sAv[(BUF) * 1024 + (rb * 8 + j * 2 + 1) * 64 + lane]);          \
+        D[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[rb], 0, 0, 0);       \
+        D[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[rb], 0, 0, 0);       \
       }                                                                              \
       const bool boundary =                                                          \
           (NBPS > 1) ? (((j + 1) % (4 / NBPS)) == 0)                                 \
                      : (j == 3 && ((((SEG) + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0); \
       if (boundary) {                                                                \
-        _Pragma("unroll") for (int t = 0; t < 2; t++)                                \
+        _Pragma("unroll") for (int rb = 0; rb < 2; rb++)                             \
             _Pragma("unroll") for (int r = 0; r < 16; r++) {                         \
-          acc[t][r] = fmaf(t == 0 ? scv0[q] : scv1[q], D[t][r], acc[t][r]);          \
-          D[t][r] = 0.0f;                                                            \
+          acc[rb][r] = fmaf(scv[q], D[rb][r], acc[rb][r]);                           \
+          D[rb][r] = 0.0f;                                                           \
         }                                                                            \
       }                                                                              \
     }                                                                                \
@@ -632,14 +633,14 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
 #undef MMNB_ISSUE
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
-  const int rb = rb0 + wm;
+  if (colok) {
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
-    if (!colok[t]) continue;
+    for (int rb = 0; rb < 2; rb++) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = rb * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-      if (row < M) Y[(size_t)row * N + col[t]] = ldexpf(acc[t][r], -row_exp[row]);
+      for (int r = 0; r < 16; r++) {
+        const int row = (rb0 + rb) * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+        if (row < M) Y[(size_t)row * N + col] = ldexpf(acc[rb][r], -row_exp[row]);
+      }
     }
   }
 }
