@@ -206,6 +206,62 @@ def bench_int8(ctx, lib, ops, synth, steps, warmup):
     return res
 
 
+def bench_platform(ctx, lib):
+    """Per-dispatch floor and streaming-read ceiling of this GPU, measured
+    with the library's calibration kernels and the same dispatch events."""
+    out = {}
+    ctx.kernel_timing(True, max_launches=400)
+    for _ in range(200):
+        lib.check(ctx.lib.mmnb_probe_empty(ctx.handle, 1024))
+    kt = ctx.kernel_timing_read()
+    ctx.kernel_timing(False)
+    out["empty_kernel_us"] = kt["k_probe_empty"][1] / kt["k_probe_empty"][0] * 1e3
+    for label, size, nbuf, reps in (("read_8.95MB", 8945664, 37, 370),
+                                    ("read_134MB", 134217728, 3, 30)):
+        bufs = [ctx.alloc(size) for _ in range(nbuf)]
+        for b in bufs:
+            lib.check(ctx.lib.mmnb_memset_dev(ctx.handle, b.ptr, 1, size))
+        for b in bufs:  # warm
+            lib.check(ctx.lib.mmnb_probe_stream_read(ctx.handle, b.ptr, size))
+        ctx.kernel_timing(True, max_launches=2 * reps)
+        for i in range(reps):
+            lib.check(ctx.lib.mmnb_probe_stream_read(ctx.handle, bufs[i % nbuf].ptr, size))
+        kt = ctx.kernel_timing_read()
+        ctx.kernel_timing(False)
+        us = kt["k_probe_read"][1] / kt["k_probe_read"][0] * 1e3
+        # back-to-back rate: graph of one rotation, events around the replays
+        ctx.synchronize()
+        ctx.graph_begin()
+        for b in bufs:
+            lib.check(ctx.lib.mmnb_probe_stream_read(ctx.handle, b.ptr, size))
+        g = ctx.graph_end()
+        ctx.graph_launch(g)
+        ctx.synchronize()
+        ctx.event_record(0)
+        for _ in range(max(1, reps // nbuf)):
+            ctx.graph_launch(g)
+        ctx.event_record(1)
+        ctx.synchronize()
+        b2b = ctx.event_elapsed_ms(0, 1) * 1e3 / (max(1, reps // nbuf) * nbuf)
+        ctx.graph_destroy(g)
+        out[label] = {"kernel_us": us, "kernel_gbs": size / (us * 1e-6) / 1e9,
+                      "back_to_back_us": b2b, "back_to_back_gbs": size / (b2b * 1e-6) / 1e9}
+        for b in bufs:
+            b.free()
+    return out
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the counter
+    reads for a copy of known size), or None if not measured."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(path.read_text()).get(workload, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(synth, m, k, n, bs, zp, budget_s):
     """The oracle (C restatement of the reference's Dart MatMulNBits:
     dequantise to a fresh K x N fp32 buffer, then the sequential-k fp32
@@ -313,7 +369,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": head["kernel"],
+                     "traffic": measured_traffic("gemv_m1_k4096_n4096_bs128"),
+                     "kernel": head["kernel"],
                      "kernel_avg_us": round(head["kernel_ms"] * 1e3, 3)},
     }
     if not args.quick:
@@ -341,6 +398,8 @@ def main():
                                                        "kernel_ms", "bytes_per_call")})
             out["decode_sweep"] = sweep
             print("# decode sweep done", file=sys.stderr, flush=True)
+            out["platform"] = bench_platform(ctx, lib)
+            print(f"# platform: {out['platform']}", file=sys.stderr, flush=True)
         except Exception as e:  # extras must not hide the headline
             out["extras_error"] = repr(e)
     out["cpu_baseline"] = cpu_baseline(synth, 1, 4096, 4096, 128, False,

@@ -219,6 +219,14 @@ int mmnb_kernel_timing_read(mmnb_ctx *ctx, int kernel_id, int64_t *count,
 /* Name of kernel id 0.. (NULL past the last id). */
 const char *mmnb_kernel_name(int kernel_id);
 
+/* Platform calibration kernels (timed through the kernel timing mode):
+ * an empty kernel (grid of `blocks` x 256 threads) and a streaming read of
+ * `bytes` (multiple of 16) from d_buf with 16-byte loads, four per thread.
+ * They measure the per-dispatch floor and the achievable HBM read rate that
+ * the operator kernels are judged against. */
+int mmnb_probe_empty(mmnb_ctx *ctx, int blocks);
+int mmnb_probe_stream_read(mmnb_ctx *ctx, const void *d_buf, size_t bytes);
+
 /* HIP graph capture of the context stream: between begin and end, the
  * "_dev" entry points are recorded instead of run (host entry points are
  * rejected).  Device scratch must already be large enough, i.e. each

@@ -57,6 +57,8 @@ SIGNATURES = {
     "mmnb_kernel_timing_read": (_int, [_vp, _int, _P(_i64), _P(ctypes.c_double),
                                        _P(ctypes.c_double), _P(ctypes.c_double)]),
     "mmnb_kernel_name": (ctypes.c_char_p, [_int]),
+    "mmnb_probe_empty": (_int, [_vp, _int]),
+    "mmnb_probe_stream_read": (_int, [_vp, _vp, _sz]),
     "mmnb_graph_begin": (_int, [_vp]),
     "mmnb_graph_end": (_int, [_vp, _P(_vp)]),
     "mmnb_graph_launch": (_int, [_vp, _vp]),

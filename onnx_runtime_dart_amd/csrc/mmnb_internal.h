@@ -65,7 +65,8 @@ struct mmnb_ctx {
   std::vector<hipEvent_t> tev;   // 2 per slot
   std::vector<int> tkid;         // kernel id per used slot
   size_t tused = 0;
-  // 2 KB constant page: 1 KB of 0x00 then 1 KB of 0x80 (int8 padding).
+  // 4 KB device page: 1 KB of 0x00 and 1 KB of 0x80 (int8 padding), then a
+  // 2 KB sink for the calibration kernels.
   void *d_pad = nullptr;
   // Tuning override of the GEMV columns-per-lane R (MMNB_GEMV_R; 0 = auto).
   int gemv_r = 0;
@@ -115,7 +116,9 @@ enum KernelId {
   kKernMmi = 5,
   kKernRepack = 6,
   kKernPrepIntB = 7,
-  kKernCount = 8
+  kKernProbeEmpty = 8,
+  kKernProbeRead = 9,
+  kKernCount = 10
 };
 
 // Launch `kern` on the context stream; in timing mode the dispatch records
@@ -157,6 +160,10 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a,
                           int32_t *d_y, const float *d_a_scale,
                           const float *d_b_scale, int64_t b_scale_len,
                           float *d_yf);
+
+// Platform calibration kernels.
+int launch_probe_empty(mmnb_ctx *ctx, int blocks);
+int launch_probe_read(mmnb_ctx *ctx, const void *d_buf, size_t bytes);
 
 // Pack construction helpers (device-side repack kernels).
 int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n,

@@ -147,11 +147,32 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     const bool cv = c < C;
     const int cc = cv ? c : 0;
     const int s = cc >> 1, g = cc & 1;
-    // ---- issue every load of this chunk
-    uint4 wv[R];
+    // ---- issue every load of this chunk: activations first (L2 hits, used
+    // by every column), then scales / zero points, then the weights in
+    // column order, so the arithmetic of column 0 can start while the later
+    // columns' weights are still arriving.
+    float av[M][32];
 #pragma unroll
-    for (int r = 0; r < R; r++)
-      wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+    for (int m = 0; m < M; m++) {
+      const float *ar = A + (int64_t)m * lda + s * kSegK + 8 * g;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if (fast) {
+          // unconditional: a lane past the last chunk reads chunk 0 (cc) and
+          // its scales are zero, so it adds exactly nothing
+          const float4 x0 = *(const float4 *)(ar + 16 * j);
+          const float4 x1 = *(const float4 *)(ar + 16 * j + 4);
+          av[m][8 * j + 0] = x0.x; av[m][8 * j + 1] = x0.y;
+          av[m][8 * j + 2] = x0.z; av[m][8 * j + 3] = x0.w;
+          av[m][8 * j + 4] = x1.x; av[m][8 * j + 5] = x1.y;
+          av[m][8 * j + 6] = x1.z; av[m][8 * j + 7] = x1.w;
+        } else {
+          const int k0 = s * kSegK + 8 * g + 16 * j;
+#pragma unroll
+          for (int e = 0; e < 8; e++) av[m][8 * j + e] = (cv && k0 + e < K) ? ar[16 * j + e] : 0.0f;
+        }
+      }
+    }
     // raw scale / zero-point loads (no arithmetic on loaded values here, so
     // the loads stay in flight together)
     float sraw[R][NBPC];
@@ -173,26 +194,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
         zsh[r][q] = (zi & 1) * 4;
       }
     }
-    float av[M][32];
+    uint4 wv[R];
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-      const float *ar = A + (int64_t)m * lda + s * kSegK + 8 * g;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        if (fast) {
-          const float4 x0 = cv ? *(const float4 *)(ar + 16 * j) : make_float4(0, 0, 0, 0);
-          const float4 x1 = cv ? *(const float4 *)(ar + 16 * j + 4) : make_float4(0, 0, 0, 0);
-          av[m][8 * j + 0] = x0.x; av[m][8 * j + 1] = x0.y;
-          av[m][8 * j + 2] = x0.z; av[m][8 * j + 3] = x0.w;
-          av[m][8 * j + 4] = x1.x; av[m][8 * j + 5] = x1.y;
-          av[m][8 * j + 6] = x1.z; av[m][8 * j + 7] = x1.w;
-        } else {
-          const int k0 = s * kSegK + 8 * g + 16 * j;
-#pragma unroll
-          for (int e = 0; e < 8; e++) av[m][8 * j + e] = (cv && k0 + e < K) ? ar[16 * j + e] : 0.0f;
-        }
-      }
-    }
+    for (int r = 0; r < R; r++)
+      wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
     // ---- arithmetic
     float sc[R][NBPC], sz[R][NBPC];
 #pragma unroll

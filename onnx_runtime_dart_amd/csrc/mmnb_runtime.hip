@@ -125,9 +125,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
       return check_hip(e, "hipEventCreate");
     }
   }
-  e = hipMalloc(&ctx->d_pad, 2048);
+  e = hipMalloc(&ctx->d_pad, 4096);
   if (e == hipSuccess) e = hipMemset(ctx->d_pad, 0, 1024);
   if (e == hipSuccess) e = hipMemset((char *)ctx->d_pad + 1024, 0x80, 1024);
+  if (e == hipSuccess) e = hipMemset((char *)ctx->d_pad + 2048, 0, 2048);
   if (e != hipSuccess) {
     delete ctx;
     return check_hip(e, "hipMalloc(pad page)");
@@ -649,7 +650,8 @@ int mmnb_event_elapsed_ms(mmnb_ctx *ctx, int slot_start, int slot_end, float *ms
 
 static const char *kKernelNames[kKernCount] = {
     "k_gemv_valu", "k_prep_a", "k_gemm_mfma", "k_dql_minmax",
-    "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b"};
+    "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b", "k_probe_empty",
+    "k_probe_read"};
 
 const char *mmnb_kernel_name(int kernel_id) {
   if (kernel_id < 0 || kernel_id >= kKernCount) return nullptr;
@@ -703,6 +705,25 @@ int mmnb_kernel_timing_read(mmnb_ctx *ctx, int kernel_id, int64_t *count, double
   if (min_ms) *min_ms = mn;
   if (max_ms) *max_ms = mx;
   return MMNB_OK;
+}
+
+int mmnb_probe_empty(mmnb_ctx *ctx, int blocks) {
+  MMNB_GUARD_CTX(ctx);
+  if (blocks < 1 || blocks > (1 << 20)) return fail(MMNB_ERR_ARG, "blocks out of range");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  return launch_probe_empty(ctx, blocks);
+}
+
+int mmnb_probe_stream_read(mmnb_ctx *ctx, const void *d_buf, size_t bytes) {
+  MMNB_GUARD_CTX(ctx);
+  if (!d_buf || bytes == 0 || (bytes & 15) || (((uintptr_t)d_buf) & 15))
+    return fail(MMNB_ERR_ARG, "probe buffer must be 16-byte aligned, size a multiple of 16");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  return launch_probe_read(ctx, d_buf, bytes);
 }
 
 int mmnb_graph_begin(mmnb_ctx *ctx) {
