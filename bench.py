@@ -296,25 +296,48 @@ def cpu_baseline(synth, m, k, n, bs, zp, budget_s):
                              "ms_per_call": float(np.min(tmt)) * 1e3}}
 
 
-def profile_pass(ctx, lib, ops, synth):
-    """Kernels for a rocprofv3 counter run: the headline GEMV and a copy of
-    known size (the calibration reference for FETCH_SIZE / WRITE_SIZE)."""
-    m, k, n, bs = 1, 4096, 4096, 128
-    count = int(np.ceil(ROTATE_BYTES / (k * n // 2 + n * (k // bs) * 4)))
-    packs = make_packs(ctx, ops, synth, m, k, n, bs, False, count, 1)
-    da = ctx.to_device(synth.activations(m, k, 1))
-    dy = ctx.alloc(m * n * 4)
-    for i in range(100):
-        lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, packs[i % count].handle, da.ptr, m,
-                                                dy.ptr))
+def profile_pass(ctx, lib, ops, synth, kind):
+    """Kernels for a rocprofv3 counter run: one operator workload and a copy
+    of known size (the calibration reference for FETCH_SIZE / WRITE_SIZE)."""
+    if kind == "gemv":
+        m, k, n, bs = 1, 4096, 4096, 128
+        count = int(np.ceil(ROTATE_BYTES / (k * n // 2 + n * (k // bs) * 4)))
+        packs = make_packs(ctx, ops, synth, m, k, n, bs, False, count, 1)
+        da = ctx.to_device(synth.activations(m, k, 1))
+        dy = ctx.alloc(m * n * 4)
+        for i in range(100):
+            lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, packs[i % count].handle, da.ptr,
+                                                    m, dy.ptr))
+        what = f"100 GEMV calls ({mmnb_bytes(m, k, n, bs, False)} algorithmic bytes each)"
+    elif kind == "gemm":
+        m, k, n, bs = 512, 4096, 4096, 32
+        p = synth.mmnb_problem(m, k, n, bs, True, seed=2, outlier_frac=0.01)
+        pack = ops.pack_nbits(p.b_q, p.scales, p.zero_points, k=k, n=n, bits=4,
+                              block_size=bs, ctx=ctx)
+        da = ctx.to_device(p.a)
+        dy = ctx.alloc(m * n * 4)
+        for _ in range(20):
+            lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, pack.handle, da.ptr, m, dy.ptr))
+        what = "20 GEMM calls (M=512 K=N=4096 block 32, zero points)"
+    else:
+        m, k, n = 512, 1024, 3072
+        x, b = synth.int8_chain_problem(m, k, n)
+        pack = ops.pack_integer(b, np.array(0, np.int8), ctx=ctx)
+        dx, dbs = ctx.to_device(x), ctx.to_device(np.array([0.01], np.float32))
+        daq, dsc, dzp = ctx.alloc(m * k), ctx.alloc(4), ctx.alloc(4)
+        dacc, dy = ctx.alloc(m * n * 4), ctx.alloc(m * n * 4)
+        for _ in range(50):
+            lib.check(ctx.lib.mmnb_dynamic_matmul_dev(ctx.handle, pack.handle, dx.ptr, m,
+                                                      dbs.ptr, 1, daq.ptr, dsc.ptr, dzp.ptr,
+                                                      dacc.ptr, dy.ptr))
+        what = "50 int8 chains (DQL [512,1024] -> MatMulInteger [1024,3072] -> rescale)"
     ctx.synchronize()
     nbytes = 64 << 20
     src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
     for _ in range(10):
         lib.check(ctx.lib.mmnb_memcpy_d2d(ctx.handle, dst.ptr, src.ptr, nbytes))
     ctx.synchronize()
-    print(f"# profile pass: {100} GEMV calls ({mmnb_bytes(m, k, n, bs, False)} algorithmic "
-          f"bytes each), 10 copies of {nbytes} bytes", file=sys.stderr, flush=True)
+    print(f"# profile pass: {what}, 10 copies of {nbytes} bytes", file=sys.stderr, flush=True)
 
 
 def main():
@@ -325,9 +348,13 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no extras")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--profile", action="store_true",
-                    help="counter pass for rocprofv3: the headline GEMV (100 calls over the "
-                         "rotated packs) and a 64 MiB device-to-device copy (10 calls) as the "
-                         "counter calibration; prints no JSON")
+                    help="counter pass for rocprofv3 (prints no JSON): the kernel chosen by "
+                         "--profile-kind, then a 64 MiB device-to-device copy (10 calls) as "
+                         "the counter calibration")
+    ap.add_argument("--profile-kind", default="gemv", choices=["gemv", "gemm", "int8"],
+                    help="gemv: headline GEMV, 100 calls over the rotated packs; gemm: "
+                         "M=512 K=N=4096 block 32 with zero points, 20 calls; int8: the "
+                         "DQL -> MatMulInteger -> rescale chain, 50 calls")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs the kernel on a single "
@@ -338,7 +365,7 @@ def main():
 
     ctx = lib.default_context()
     if args.profile:
-        profile_pass(ctx, lib, ops, synth)
+        profile_pass(ctx, lib, ops, synth, args.profile_kind)
         return
     info = ctx.info()
     print(f"# device {info}", file=sys.stderr, flush=True)

@@ -147,11 +147,18 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     const bool cv = c < C;
     const int cc = cv ? c : 0;
     const int s = cc >> 1, g = cc & 1;
-    // ---- issue every load of this chunk: activations first (L2 hits, used
-    // by every column), then scales / zero points, then the weights in
-    // column order, so the arithmetic of column 0 can start while the later
-    // columns' weights are still arriving.
+    // ---- issue every load of this chunk.  M = 1: activations first (L2
+    // hits, used by every column), then scales / zero points, then the weights
+    // in column order, so column 0's arithmetic starts while later columns'
+    // weights are in flight.  M > 1: weights first (the activation registers
+    // grow with M; issuing them last keeps the weight stream ahead).
     float av[M][32];
+    uint4 wv[R];
+    if constexpr (M > 1) {
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+    }
 #pragma unroll
     for (int m = 0; m < M; m++) {
       const float *ar = A + (int64_t)m * lda + s * kSegK + 8 * g;
@@ -194,10 +201,11 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
         zsh[r][q] = (zi & 1) * 4;
       }
     }
-    uint4 wv[R];
+    if constexpr (M == 1) {
 #pragma unroll
-    for (int r = 0; r < R; r++)
-      wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+      for (int r = 0; r < R; r++)
+        wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+    }
     // ---- arithmetic
     float sc[R][NBPC], sz[R][NBPC];
 #pragma unroll
