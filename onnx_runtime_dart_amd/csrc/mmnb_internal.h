@@ -54,6 +54,8 @@ struct mmnb_ctx {
   std::mutex mu;
   hipEvent_t events[16] = {};
   int cu_count = 0;
+  // Largest dynamic LDS allocation one workgroup may take (bytes).
+  int lds_max = 65536;
   // Device staging/scratch buffers, grown on demand and kept for reuse:
   //  0: activations in (fp32 / uint8), 1: outputs, 2: prepared activations
   //  (fp16 hi/lo), 3: small reductions, 4: misc.
@@ -70,6 +72,9 @@ struct mmnb_ctx {
   void *d_pad = nullptr;
   // Tuning override of the GEMV columns-per-lane R (MMNB_GEMV_R; 0 = auto).
   int gemv_r = 0;
+  // Tuning override of the multi-row GEMV column groups per workgroup
+  // (MMNB_GEMV_CG; 0 = auto).
+  int gemv_cg = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
 };

@@ -79,6 +79,40 @@ int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n, int64_t
                 d_src, n, src_col, dst_col, k, d_dst);
 }
 
+// (a & mask) | orv in one VALU op.  gfx9 VOP3 takes no literal, so the
+// compiler splits this into v_and + v_or; with the mask in an SGPR and the
+// magic in a VGPR it is one v_and_or_b32.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(orv));
+  return r;
+}
+
+// 8 nibbles of one dword -> 8 fp16 values (q - zp), exact.  (q | 0x6400)
+// as fp16 is 1024 + q; (16q | 0x6400) is 1024 + 16q, so
+//   lo nibble pairs: (1024 + q) - (1024 + zp)
+//   hi nibble pairs: (1024 + 16q) / 16 - (64 + zp)
+// Output order {n0, n4, n1, n5, n2, n6, n3, n7}; the prepared activations
+// use the same k permutation.
+__device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) {
+  const uint32_t t0 = and_or(w, 0x000F000Fu, magic);
+  const uint32_t t1 = and_or(w, 0x00F000F0u, magic);
+  const uint32_t w8 = w >> 8;
+  const uint32_t t2 = and_or(w8, 0x000F000Fu, magic);
+  const uint32_t t3 = and_or(w8, 0x00F000F0u, magic);
+  const _Float16 z1024 = (_Float16)(1024 + zp);
+  const _Float16 z64 = (_Float16)(64 + zp);
+  const half2_t zz = {z1024, z1024};
+  const half2_t zs = {z64, z64};
+  const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const half2_t h0 = __builtin_bit_cast(half2_t, t0) - zz;
+  const half2_t h1 = __builtin_bit_cast(half2_t, t1) * sixteenth - zs;
+  const half2_t h2 = __builtin_bit_cast(half2_t, t2) - zz;
+  const half2_t h3 = __builtin_bit_cast(half2_t, t3) * sixteenth - zs;
+  half8_t r = {h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // Decode-shape GEMV on the vector ALUs (fp32 FMA), M <= 8.
 //
@@ -309,14 +343,320 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
   return launch_gemv_mr<M, 1>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
 }
 
+// ---------------------------------------------------------------------------
+// Decode-shape GEMV for 2 <= M <= 8, activations staged in LDS.
+//
+// Holding a chunk's 32 activations per row in registers (the M = 1 kernel)
+// costs 32*M VGPRs and re-reads A through L1 for every pair of columns; at
+// M = 8 that spills.  Here the workgroup first copies A (all rows, K padded
+// to the staged chunk range, zeros past K) into LDS in chunk-major order,
+//     slot((m, j, h4), c) = ((m*4 + j)*2 + h4) * P + c    (float4 slots)
+// holding k = 64(c/2) + 16j + 8(c%2) + 4*h4 .. +3, so the 32 lanes of a
+// half-wave (consecutive chunks c) read consecutive 16-byte slots (no bank
+// conflicts; P = slots + 1 spreads the staging writes over banks).
+//
+// Work split: a "column group" is 2R columns; kw waves split its K (lane
+// (w, h, t) owns chunk 32w + t (+ 32*kw per iteration) of columns 2r + h,
+// r < R).  A workgroup runs cg column groups side by side (cg*kw waves)
+// and walks the groups grid-stride, reusing the staged activations.  Per
+// dword j of a chunk a lane reads its 8*M activations once and applies them
+// to its R columns.  Dequantisation yields (q - zp) exactly in fp16
+// (dequant8), so the fp32 FMA takes the fp16 operand directly
+// (v_fma_mix_f32) and no separate zero-point term is needed.
+// ---------------------------------------------------------------------------
+// Weight, scale and zero-point loads of one chunk (lane's chunk c of its R
+// columns); kept separate so the first group's loads can be issued before
+// the activations are staged.
+template <int R, int NBPC, bool HAS_ZP>
+struct GemvChunk {
+  u4vec wv[R];
+  float sraw[R][NBPC];
+  uint32_t zraw[R][NBPC];
+  int zsh[R][NBPC];
+  bool inbq[NBPC];
+
+  __device__ __forceinline__ void load(const uint8_t *__restrict__ W, int64_t col_bytes,
+                                       const float *__restrict__ S,
+                                       const uint8_t *__restrict__ Z, int nb, int bs_log2,
+                                       const int (&colr)[R], int c, int C) {
+    const bool cv = c < C;
+    const int cc = cv ? c : 0;
+    const int s = cc >> 1, gg = cc & 1;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      wv[r] = *(const u4vec *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+#pragma unroll
+    for (int q = 0; q < NBPC; q++) {
+      const int kq = s * kSegK + 16 * (q * (4 / NBPC)) + (NBPC == 4 ? 8 * gg : 0);
+      int blk = kq >> bs_log2;
+      inbq[q] = cv && blk < nb;
+      blk = blk < nb ? blk : nb - 1;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int zi = colr[r] * nb + blk;
+        sraw[r][q] = S[zi];
+        if (HAS_ZP) zraw[r][q] = Z[zi >> 1];
+        zsh[r][q] = (zi & 1) * 4;
+      }
+    }
+  }
+};
+
+template <int M, int R, int NBPC, bool HAS_ZP>
+__global__ __launch_bounds__(512) void k_gemv_lds(
+    const float *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W,
+    int64_t col_bytes, const float *__restrict__ S, const uint8_t *__restrict__ Z, int nb,
+    int bs_log2, int K, int N, float *__restrict__ Y, int C, int kw, int iters, int groups,
+    int vec) {
+  extern __shared__ float4 sact[];
+  __shared__ float red[8][M][2 * R];
+  const int cs = 32 * kw * iters;  // staged chunk slots
+  const int P = cs + 1;            // slot pitch (float4)
+  const int nthr = blockDim.x;
+  const int cg = nthr / (64 * kw);  // column groups side by side
+  const int wg = threadIdx.x >> 6;        // wave in workgroup
+  const int sub = wg / kw, w = wg % kw;   // column group slot, K part
+  const int l = threadIdx.x & 63, h = l >> 5, t = l & 31;
+  const uint32_t magic = 0x64006400u;
+
+  int g0 = blockIdx.x * cg;
+  int colr[R];
+  auto set_cols = [&](int gbase) {
+    const int g = gbase + sub;
+    const int col0 = (g < groups ? g : 0) * (2 * R);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int c = col0 + 2 * r + h;
+      colr[r] = c < N ? c : N - 1;
+    }
+  };
+  // first group's weights in flight before the activations are staged
+  GemvChunk<R, NBPC, HAS_ZP> ch;
+  set_cols(g0);
+  ch.load(W, col_bytes, S, Z, nb, bs_log2, colr, 32 * w + t, C);
+
+  // ---- stage A -> LDS: up to 8 independent 16-byte loads per thread in flight
+  const int k4n = cs * 8;  // float4 per row
+  const int total = M * k4n;
+  for (int base = threadIdx.x; base < total; base += 8 * nthr) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = base + u * nthr;
+      const int m = i / k4n, k = 4 * (i - m * k4n);
+      const float *ar = A + (int64_t)m * lda + k;
+      if (i >= total) {
+        v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      } else if (vec && k + 4 <= K) {
+        v[u] = *(const float4 *)ar;
+      } else {
+        v[u].x = k + 0 < K ? ar[0] : 0.0f;
+        v[u].y = k + 1 < K ? ar[1] : 0.0f;
+        v[u].z = k + 2 < K ? ar[2] : 0.0f;
+        v[u].w = k + 3 < K ? ar[3] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = base + u * nthr;
+      if (i < total) {
+        const int m = i / k4n, k = 4 * (i - m * k4n);
+        const int c = 2 * (k >> 6) + ((k >> 3) & 1);
+        const int j = (k >> 4) & 3, h4 = (k >> 2) & 1;
+        sact[((m * 4 + j) * 2 + h4) * P + c] = v[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  for (; g0 < groups; g0 += gridDim.x * cg) {
+    float acc[M][R];
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
+
+    for (int it = 0; it < iters; it++) {
+      const int c = 32 * w + t + it * 32 * kw;  // < cs: a staged slot
+      if (it > 0) ch.load(W, col_bytes, S, Z, nb, bs_log2, colr, c, C);
+      float d[M][R];
+#pragma unroll
+      for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) d[m][r] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int q = j / (4 / NBPC);
+        float av[M][8];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          const float4 x0 = sact[((m * 4 + j) * 2 + 0) * P + c];
+          const float4 x1 = sact[((m * 4 + j) * 2 + 1) * P + c];
+          av[m][0] = x0.x; av[m][1] = x0.y; av[m][2] = x0.z; av[m][3] = x0.w;
+          av[m][4] = x1.x; av[m][5] = x1.y; av[m][6] = x1.z; av[m][7] = x1.w;
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const int zpv = HAS_ZP ? (int)((ch.zraw[r][q] >> ch.zsh[r][q]) & 0xF) : 8;
+          // element p of b is nibble {0,4,1,5,2,6,3,7}[p] of the dword
+          const half8_t b = dequant8(ch.wv[r][j], zpv, magic);
+#pragma unroll
+          for (int m = 0; m < M; m++) {
+            float x = d[m][r];
+            x = fmaf(av[m][0], (float)b[0], x);
+            x = fmaf(av[m][4], (float)b[1], x);
+            x = fmaf(av[m][1], (float)b[2], x);
+            x = fmaf(av[m][5], (float)b[3], x);
+            x = fmaf(av[m][2], (float)b[4], x);
+            x = fmaf(av[m][6], (float)b[5], x);
+            x = fmaf(av[m][3], (float)b[6], x);
+            x = fmaf(av[m][7], (float)b[7], x);
+            d[m][r] = x;
+          }
+        }
+        if (((j + 1) % (4 / NBPC)) == 0) {
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const float sc = ch.inbq[q] ? ch.sraw[r][q] : 0.0f;
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+              acc[m][r] = fmaf(sc, d[m][r], acc[m][r]);
+              d[m][r] = 0.0f;
+            }
+          }
+        }
+      }
+    }
+    // next group's first chunk in flight during the reductions
+    const int g1 = g0 + gridDim.x * cg;
+    if (g1 < groups) {
+      set_cols(g1);
+      ch.load(W, col_bytes, S, Z, nb, bs_log2, colr, 32 * w + t, C);
+    }
+    // ---- reductions: 32 lanes of a half-wave, then the kw waves of the group
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const float v = half_wave_sum(acc[m][r]);
+        if (t == 0) red[wg][m][2 * r + h] = v;
+      }
+    __syncthreads();
+    for (int i = threadIdx.x; i < cg * M * 2 * R; i += nthr) {
+      const int sg = i / (M * 2 * R), rem = i % (M * 2 * R);
+      const int m = rem / (2 * R), cl = rem % (2 * R);
+      const int gi = g0 + sg;
+      float v = 0.0f;
+      for (int ww = 0; ww < kw; ww++) v += red[sg * kw + ww][m][cl];
+      const int col = gi * (2 * R) + cl;
+      if (gi < groups && col < N) Y[(int64_t)m * N + col] = v;
+    }
+    __syncthreads();
+  }
+}
+
+template <int M, int R>
+static int launch_gemv_lds_mr(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, size_t shmem,
+                              const float *A, int64_t lda, const mmnb_pack *p, float *Y,
+                              int C, int kw, int iters, int groups, int vec, int bs_log2) {
+  const int nb = (int)p->n_blocks, K = (int)p->k, N = (int)p->n;
+#define MMNB_GEMV_LDS_LAUNCH(Q, ZP)                                                          \
+  {                                                                                          \
+    auto kern = k_gemv_lds<M, R, Q, ZP>;                                                     \
+    if (shmem > 65536) {                                                                     \
+      hipError_t e_ = hipFuncSetAttribute((const void *)kern,                               \
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,        \
+                                          (int)shmem);                                       \
+      if (e_ != hipSuccess) return check_hip(e_, "hipFuncSetAttribute");                     \
+    }                                                                                        \
+    return launch(ctx, kKernGemv, kern, grid, block, shmem, A, lda, p->d_w, p->col_bytes,   \
+                  p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C, kw, iters, groups, vec);   \
+  }
+  if (p->has_zp) {
+    if (nbpc == 4) MMNB_GEMV_LDS_LAUNCH(4, true);
+    if (nbpc == 2) MMNB_GEMV_LDS_LAUNCH(2, true);
+    MMNB_GEMV_LDS_LAUNCH(1, true);
+  }
+  if (nbpc == 4) MMNB_GEMV_LDS_LAUNCH(4, false);
+  if (nbpc == 2) MMNB_GEMV_LDS_LAUNCH(2, false);
+  MMNB_GEMV_LDS_LAUNCH(1, false);
+#undef MMNB_GEMV_LDS_LAUNCH
+}
+
+template <int M>
+static int launch_gemv_lds_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
+                             size_t shmem, const float *A, int64_t lda, const mmnb_pack *p,
+                             float *Y, int C, int kw, int iters, int groups, int vec,
+                             int bs_log2) {
+  if (R == 4)
+    return launch_gemv_lds_mr<M, 4>(ctx, nbpc, grid, block, shmem, A, lda, p, Y, C, kw, iters,
+                                    groups, vec, bs_log2);
+  if (R == 2)
+    return launch_gemv_lds_mr<M, 2>(ctx, nbpc, grid, block, shmem, A, lda, p, Y, C, kw, iters,
+                                    groups, vec, bs_log2);
+  return launch_gemv_lds_mr<M, 1>(ctx, nbpc, grid, block, shmem, A, lda, p, Y, C, kw, iters,
+                                  groups, vec, bs_log2);
+}
+
 static int ilog2(int64_t v) {
   int r = 0;
   while ((int64_t(1) << (r + 1)) <= v) r++;
   return r;
 }
 
+static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
+                       int64_t m, float *d_y);
+
+// 2 <= M <= 8: the LDS-staged kernel, or the MFMA GEMM when A does not fit
+// the workgroup's LDS.
+static int launch_gemv_multi(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
+                             int64_t lda, int64_t m, float *d_y) {
+  const int C = (int)(p->col_bytes / 16);
+  int kw = (C + 31) / 32, iters = 1;
+  if (kw > 4) {
+    iters = (kw + 3) / 4;
+    kw = (C + 32 * iters - 1) / (32 * iters);
+  }
+  const int cs = 32 * kw * iters;
+  const size_t shmem = (size_t)m * 8 * (cs + 1) * 16;
+  // the kernel also holds a static 8 x M x 8 float reduction buffer
+  if (shmem + 8 * 8 * 8 * 4 > (size_t)ctx->lds_max) return launch_gemm(ctx, p, d_a, lda, m, d_y);
+  const int64_t n = p->n;
+  // Every workgroup stages all of A, so fewer, wider workgroups win: up to
+  // 8 waves (cg column groups of kw waves), then the most columns per lane
+  // (R) that still leaves a workgroup on three quarters of the CUs.
+  int cg = 8 / kw;
+  if (ctx->gemv_cg > 0 && ctx->gemv_cg * kw <= 8) cg = ctx->gemv_cg;  // tuning override
+  int R = 4;
+  while (R > 1 && (n + 2 * R * cg - 1) / (2 * R * cg) < 3 * ctx->cu_count / 4) R >>= 1;
+  if (ctx->gemv_r > 0 && ctx->gemv_r <= 4) R = ctx->gemv_r;  // tuning override
+  const int groups = (int)((n + 2 * R - 1) / (2 * R));
+  const dim3 grid((unsigned)((groups + cg - 1) / cg));
+  const dim3 block((unsigned)(64 * kw * cg));
+  const int vec = ((lda % 4 == 0) && (((uintptr_t)d_a & 15) == 0)) ? 1 : 0;
+  const int bs_log2 = ilog2(p->block);
+  const int nbpc = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
+  switch (m) {
+#define MMNB_CASE(MM)                                                                        \
+  case MM:                                                                                   \
+    return launch_gemv_lds_m<MM>(ctx, R, nbpc, grid, block, shmem, d_a, lda, p, d_y, C, kw, \
+                                 iters, groups, vec, bs_log2);
+    MMNB_CASE(2)
+    MMNB_CASE(3)
+    MMNB_CASE(4)
+    MMNB_CASE(5)
+    MMNB_CASE(6)
+    MMNB_CASE(7)
+    MMNB_CASE(8)
+#undef MMNB_CASE
+    default:
+      return fail(MMNB_ERR_ARG, "GEMV: M out of range");
+  }
+}
+
 static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y) {
+  if (m > 1) return launch_gemv_multi(ctx, p, d_a, lda, m, d_y);
   const int C = (int)(p->col_bytes / 16);  // chunks per column
   // waves splitting K: one chunk per lane up to 16 waves, then iterate
   int nw = (C + 31) / 32;
@@ -327,7 +667,7 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   }
   // columns per workgroup 2R: as many as keep >= 2 workgroups per CU
   const int64_t n = p->n;
-  int R = m <= 2 ? 8 : (m <= 4 ? 4 : 2);
+  int R = 8;
   while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
   if (ctx->gemv_r > 0) R = ctx->gemv_r;  // tuning override
   const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
@@ -338,16 +678,7 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   const int f = ((lda % 4 == 0) && (((uintptr_t)d_a & 15) == 0) && (lda >= p->k64)) ? 1 : 0;
   const int bs_log2 = ilog2(p->block);
   const int nbpc = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
-  switch (m) {
-    case 1: return launch_gemv_m<1>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    case 2: return launch_gemv_m<2>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    case 3: return launch_gemv_m<3>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    case 4: return launch_gemv_m<4>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    case 5: return launch_gemv_m<5>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    case 6: return launch_gemv_m<6>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    case 7: return launch_gemv_m<7>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-    default: return launch_gemv_m<8>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
-  }
+  return launch_gemv_m<1>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
 }
 
 // ---------------------------------------------------------------------------
@@ -438,40 +769,6 @@ __global__ __launch_bounds__(256) void k_prep_convert(
 // at each quantisation-block boundary acc += scale[n, blk] * D.  The 16-byte
 // weight load of a lane covers four 16-k steps (one 64-k segment).
 // ---------------------------------------------------------------------------
-// (a & mask) | orv in one VALU op.  gfx9 VOP3 takes no literal, so the
-// compiler splits this into v_and + v_or; with the mask in an SGPR and the
-// magic in a VGPR it is one v_and_or_b32.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(orv));
-  return r;
-}
-
-// 8 nibbles of one dword -> 8 fp16 values (q - zp), exact.  (q | 0x6400)
-// as fp16 is 1024 + q; (16q | 0x6400) is 1024 + 16q, so
-//   lo nibble pairs: (1024 + q) - (1024 + zp)
-//   hi nibble pairs: (1024 + 16q) / 16 - (64 + zp)
-// Output order {n0, n4, n1, n5, n2, n6, n3, n7}; the prepared activations
-// use the same k permutation.
-__device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) {
-  const uint32_t t0 = and_or(w, 0x000F000Fu, magic);
-  const uint32_t t1 = and_or(w, 0x00F000F0u, magic);
-  const uint32_t w8 = w >> 8;
-  const uint32_t t2 = and_or(w8, 0x000F000Fu, magic);
-  const uint32_t t3 = and_or(w8, 0x00F000F0u, magic);
-  const _Float16 z1024 = (_Float16)(1024 + zp);
-  const _Float16 z64 = (_Float16)(64 + zp);
-  const half2_t zz = {z1024, z1024};
-  const half2_t zs = {z64, z64};
-  const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const half2_t h0 = __builtin_bit_cast(half2_t, t0) - zz;
-  const half2_t h1 = __builtin_bit_cast(half2_t, t1) * sixteenth - zs;
-  const half2_t h2 = __builtin_bit_cast(half2_t, t2) - zz;
-  const half2_t h3 = __builtin_bit_cast(half2_t, t3) * sixteenth - zs;
-  half8_t r = {h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
-  return r;
-}
-
 constexpr int kGemmBM = 64;   // two 32-row blocks
 constexpr int kGemmBN = 128;  // four 32-column blocks
 constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)

@@ -109,9 +109,20 @@ int mmnb_init(int device, mmnb_ctx **out) {
   if (!ctx) return fail(MMNB_ERR_OOM, "mmnb_init: out of host memory");
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
+  {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) ==
+            hipSuccess &&
+        v > 0)
+      ctx->lds_max = v;
+  }
   if (const char *r = std::getenv("MMNB_GEMV_R")) {
     const int v = std::atoi(r);
     if (v == 1 || v == 2 || v == 4 || v == 8) ctx->gemv_r = v;
+  }
+  if (const char *r = std::getenv("MMNB_GEMV_CG")) {
+    const int v = std::atoi(r);
+    if (v >= 1 && v <= 8) ctx->gemv_cg = v;
   }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {

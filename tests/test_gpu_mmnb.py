@@ -120,6 +120,13 @@ def test_prefill_full_size_row_sample(ctx, m, n, block):
     (65, 1000, 130, 128, True),  # GEMM path, K not a multiple of 64
     (8, 3000, 17, 64, False),
     (1, 4096, 1, 128, True),    # single column
+    # decode GEMV for 2 <= M <= 8 (activations staged in LDS)
+    (2, 9000, 33, 128, True),   # K > 4096: several chunk iterations
+    (4, 5000, 100, 16, True),   # block 16, iterations
+    (7, 1000, 300, 32, True),
+    (6, 64, 1000, 64, False),   # one chunk per column, many column groups
+    (3, 3072, 1024, 128, False),
+    (8, 8192, 40, 64, True),    # A too large for one workgroup's LDS: GEMM path
 ])
 def test_edge_shapes(ctx, m, k, n, block, zp):
     p = synth.mmnb_problem(m, k, n, block, zp, seed=11 + m + n)
@@ -166,7 +173,8 @@ def test_all_zero_nibbles_closed_form(ctx):
 
 def test_device_entry_point_matches_host_entry_point(ctx):
     # K a multiple of 64 (aligned path) and not (masked path)
-    for (m, k, n, bs) in [(1, 1024, 256, 32), (4, 1000, 96, 8 * 16), (24, 320, 200, 64)]:
+    for (m, k, n, bs) in [(1, 1024, 256, 32), (4, 1000, 96, 8 * 16), (24, 320, 200, 64),
+                          (5, 1001, 64, 32), (2, 4097, 48, 128)]:
         p = synth.mmnb_problem(m, k, n, bs, True, seed=k)
         pack = ops.pack_nbits(p.b_q, p.scales, p.zero_points, k=k, n=n, bits=4,
                               block_size=bs, ctx=ctx)
