@@ -360,9 +360,8 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
 // r < R).  A workgroup runs cg column groups side by side (cg*kw waves)
 // and walks the groups grid-stride, reusing the staged activations.  Per
 // dword j of a chunk a lane reads its 8*M activations once and applies them
-// to its R columns.  Dequantisation yields (q - zp) exactly in fp16
-// (dequant8), so the fp32 FMA takes the fp16 operand directly
-// (v_fma_mix_f32) and no separate zero-point term is needed.
+// to its R columns.  Each nibble becomes float(q) - zp (exact) before the
+// fp32 FMAs, so no separate zero-point term is needed.
 // ---------------------------------------------------------------------------
 // Weight, scale and zero-point loads of one chunk (lane's chunk c of its R
 // columns); kept separate so the first group's loads can be issued before
@@ -417,7 +416,6 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
   const int wg = threadIdx.x >> 6;        // wave in workgroup
   const int sub = wg / kw, w = wg % kw;   // column group slot, K part
   const int l = threadIdx.x & 63, h = l >> 5, t = l & 31;
-  const uint32_t magic = 0x64006400u;
 
   int g0 = blockIdx.x * cg;
   int colr[R];
@@ -497,20 +495,25 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
         }
 #pragma unroll
         for (int r = 0; r < R; r++) {
-          const int zpv = HAS_ZP ? (int)((ch.zraw[r][q] >> ch.zsh[r][q]) & 0xF) : 8;
-          // element p of b is nibble {0,4,1,5,2,6,3,7}[p] of the dword
-          const half8_t b = dequant8(ch.wv[r][j], zpv, magic);
+          const float zf = HAS_ZP ? (float)((ch.zraw[r][q] >> ch.zsh[r][q]) & 0xF) : 8.0f;
+          // byte converts and subtracts run at the full VALU rate (mixed
+          // fp16/fp32 FMAs and packed fp16 ops at half rate on gfx950)
+          const uint32_t wd = ch.wv[r][j];
+          const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+          float qv[8];
+          qv[0] = (float)(lo & 0xFF) - zf;
+          qv[1] = (float)(hi & 0xFF) - zf;
+          qv[2] = (float)((lo >> 8) & 0xFF) - zf;
+          qv[3] = (float)((hi >> 8) & 0xFF) - zf;
+          qv[4] = (float)((lo >> 16) & 0xFF) - zf;
+          qv[5] = (float)((hi >> 16) & 0xFF) - zf;
+          qv[6] = (float)(lo >> 24) - zf;
+          qv[7] = (float)(hi >> 24) - zf;
 #pragma unroll
           for (int m = 0; m < M; m++) {
             float x = d[m][r];
-            x = fmaf(av[m][0], (float)b[0], x);
-            x = fmaf(av[m][4], (float)b[1], x);
-            x = fmaf(av[m][1], (float)b[2], x);
-            x = fmaf(av[m][5], (float)b[3], x);
-            x = fmaf(av[m][2], (float)b[4], x);
-            x = fmaf(av[m][6], (float)b[5], x);
-            x = fmaf(av[m][3], (float)b[6], x);
-            x = fmaf(av[m][7], (float)b[7], x);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x = fmaf(av[m][e], qv[e], x);
             d[m][r] = x;
           }
         }
