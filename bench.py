@@ -137,7 +137,7 @@ def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
     n_steps, ms_step, kt = time_mmnb(ctx, lib, [pack], da, m, dy, steps, warmup)
     flops = 2.0 * m * k * n
     gk = kernel_avg_ms(kt, "k_gemm_mfma")
-    # k_prep_a counts both prep launches (row exponents, hi/lo split)
+    # k_prep_a: the activation prep launch (row exponents and hi/lo split)
     pk = kt["k_prep_a"][1] / kt["k_gemm_mfma"][0] if "k_prep_a" in kt else 0.0
     achieved = flops / (gk * 1e-3) / 1e12
     res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "steps": n_steps,

@@ -75,6 +75,8 @@ struct mmnb_ctx {
   // Tuning override of the multi-row GEMV column groups per workgroup
   // (MMNB_GEMV_CG; 0 = auto).
   int gemv_cg = 0;
+  // Prefill GEMM LDS stages (2 or 3; MMNB_GEMM_STAGES tuning override).
+  int gemm_stages = 2;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
 };

@@ -7,6 +7,7 @@
 // a[k] * (q - zp), which differs from the reference only in rounding.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "mmnb_internal.h"
@@ -698,116 +699,167 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
 // lane order: lane l -> row rb*32 + l%32, k = 64s + 16j + 8(l/32) + perm[e],
 // perm = {0,4,1,5,2,6,3,7} (the order the weight dequantisation produces).
 // Rows >= M and k >= K are zero.
+//
+// One launch: a workgroup owns kPrepRows consecutive rows (so each store
+// fills a contiguous run of a unit: lanes rl .. rl+kPrepRows-1), finds each
+// row's maximum over K, then converts.  Thread t covers k = 16t .. 16t+15 of
+// every 4096-k chunk (one 16-k step: both 8-k halves); the first chunk stays
+// in registers between the two passes, so K <= 4096 reads A once.
 // ---------------------------------------------------------------------------
-// Row exponents: one wave per row, e_m = 13 - floor(log2(max|a_m|)).
-__global__ __launch_bounds__(256) void k_prep_rowexp(const float *__restrict__ A, int64_t lda,
-                                                     int64_t M, int64_t K,
-                                                     int *__restrict__ row_exp) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const float *ar = A + row * lda;
-  float mx = 0.0f;
-  const bool vec = ((((uintptr_t)ar) & 15) == 0);
-  int64_t k0 = 0;
-  if (vec) {
-    const int64_t k4 = K >> 2;
-    for (int64_t i = lane; i < k4; i += 64) {
-      const float4 v = ((const float4 *)ar)[i];
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+constexpr int kPrepRows = 2;
+
+__global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int64_t lda,
+                                                int64_t M, int64_t K, int64_t segsp,
+                                                int *__restrict__ row_exp,
+                                                uint4 *__restrict__ out) {
+  __shared__ float wmax[kPrepRows][4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * kPrepRows;
+  const int64_t kp = segsp * kSegK;  // padded K
+  const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
+  auto load8 = [&](int64_t row, int64_t k0, float *v) {
+    const float *ar = A + row * lda + k0;
+    if (row < M && vec && k0 + 8 <= K) {
+      const float4 x0 = *(const float4 *)ar;
+      const float4 x1 = *(const float4 *)(ar + 4);
+      v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+      v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = (row < M && k0 + e < K) ? ar[e] : 0.0f;
     }
-    k0 = k4 << 2;
-  }
-  for (int64_t k = k0 + lane; k < K; k += 64) mx = fmaxf(mx, fabsf(ar[k]));
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (lane == 0) {
-    int e = 0;
-    if (mx > 0.0f && mx < INFINITY) e = 13 - ilogbf(mx);
-    row_exp[row] = e;
-  }
-}
-
-// Split into fp16 hi/lo in the MFMA operand layout.  One workgroup per
-// (32-row block, 64-k segment); thread (j, l) writes unit (j, lane l) of the
-// hi and the lo piece.
-__global__ __launch_bounds__(256) void k_prep_convert(
-    const float *__restrict__ A, int64_t lda, int64_t M, int64_t K, int64_t segs,
-    const int *__restrict__ row_exp, uint4 *__restrict__ out) {
-  const int64_t s = blockIdx.x, rb = blockIdx.y;
-  const int l = threadIdx.x & 63, j = threadIdx.x >> 6;
-  const int r = l & 31, g = l >> 5;
-  const int64_t row = rb * 32 + r;
-  const int64_t k0 = s * kSegK + 16 * j + 8 * g;
-  float v[8];
-  if (row < M && k0 + 8 <= K && (((uintptr_t)(A + row * lda + k0)) & 15) == 0) {
-    const float4 x0 = *(const float4 *)(A + row * lda + k0);
-    const float4 x1 = *(const float4 *)(A + row * lda + k0 + 4);
-    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-  } else {
+  };
+  // ---- row maxima (first chunk kept)
+  float keep[kPrepRows][16];
+  float mx[kPrepRows];
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = (row < M && k0 + e < K) ? A[row * lda + k0 + e] : 0.0f;
+  for (int r = 0; r < kPrepRows; r++) {
+    load8(r0 + r, 16 * t, &keep[r][0]);
+    load8(r0 + r, 16 * t + 8, &keep[r][8]);
   }
-  const int ex = row < M ? row_exp[row] : 0;
-  _Float16 hi[8], lo[8];
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float x = ldexpf(v[e], ex);
-    const _Float16 h = (_Float16)x;
-    hi[e] = h;
-    lo[e] = (_Float16)(x - (float)h);
+  for (int r = 0; r < kPrepRows; r++) {
+    mx[r] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) mx[r] = fmaxf(mx[r], fabsf(keep[r][e]));
+    for (int64_t k0 = 16 * t + 4096; k0 < K; k0 += 4096) {
+      float v[16];
+      load8(r0 + r, k0, &v[0]);
+      load8(r0 + r, k0 + 8, &v[8]);
+#pragma unroll
+      for (int e = 0; e < 16; e++) mx[r] = fmaxf(mx[r], fabsf(v[e]));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off, 64));
+    if (lane == 0) wmax[r][wave] = mx[r];
   }
-  // permute to the dequantised-weight order {0,4,1,5,2,6,3,7}
-  half8_t H = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
-  half8_t L = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
-  const int64_t base = ((rb * segs + s) * 4 + j) * 2;
-  out[(base + 0) * 64 + l] = __builtin_bit_cast(uint4, H);
-  out[(base + 1) * 64 + l] = __builtin_bit_cast(uint4, L);
+  __syncthreads();
+  int ex[kPrepRows];
+#pragma unroll
+  for (int r = 0; r < kPrepRows; r++) {
+    const float m_ = fmaxf(fmaxf(wmax[r][0], wmax[r][1]), fmaxf(wmax[r][2], wmax[r][3]));
+    ex[r] = (m_ > 0.0f && m_ < INFINITY) ? 13 - ilogbf(m_) : 0;
+    if (t == 0 && r0 + r < M) row_exp[r0 + r] = ex[r];
+  }
+  // ---- convert: thread t writes, per 4096-k chunk, step j = t%4 of segment
+  // s = chunk*64 + t/4, both halves g, both parts, for its rows
+  const int64_t rb = r0 >> 5;
+  const int rl = (int)(r0 & 31);
+  for (int64_t k0 = 16 * t; k0 < kp; k0 += 4096) {
+    const int64_t s = k0 >> 6;
+    const int j = (int)((k0 >> 4) & 3);
+    const int64_t base = ((rb * segsp + s) * 4 + j) * 2;  // unit index of part 0
+    float v[kPrepRows][16];
+#pragma unroll
+    for (int r = 0; r < kPrepRows; r++) {
+      if (k0 < 4096) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) v[r][e] = keep[r][e];
+      } else {
+        load8(r0 + r, k0, &v[r][0]);
+        load8(r0 + r, k0 + 8, &v[r][8]);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+#pragma unroll
+      for (int r = 0; r < kPrepRows; r++) {
+        _Float16 hi[8], lo[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float x = ldexpf(v[r][8 * g + e], ex[r]);
+          const _Float16 h = (_Float16)x;
+          hi[e] = h;
+          lo[e] = (_Float16)(x - (float)h);
+        }
+        const half8_t hv = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
+        const half8_t lv = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
+        out[(base + 0) * 64 + 32 * g + rl + r] = __builtin_bit_cast(uint4, hv);
+        out[(base + 1) * 64 + 32 * g + rl + r] = __builtin_bit_cast(uint4, lv);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Prefill GEMM: WG tile 64 (M) x 128 (N), 4 waves in 2 x 2, wave tile
-// 32 x 64 = one 32-row A block x two 32-column B blocks.  For every 16-k step
-// the wave issues 2 (B blocks) x 2 (hi, lo) MFMAs into per-block partials D;
-// at each quantisation-block boundary acc += scale[n, blk] * D.  The 16-byte
-// weight load of a lane covers four 16-k steps (one 64-k segment).
+// Prefill GEMM, fed by direct global->LDS DMA.
+//
+// Workgroup tile 64 (M) x 128 (N).  A group of 4 waves in 1 x 4 owns the
+// tile over a range of K: wave tile 64 x 32 (both 32-row A blocks, one
+// 32-column weight block, so every weight is dequantised once per group).
+// GROUPS = 2 splits K between two such groups (8 waves, two per SIMD, so one
+// wave's MFMAs overlap the other's vector work) when the tiles alone leave a
+// single wave per SIMD; the partial tiles are summed through LDS at the end.
+//
+// Every operand of a 64-k segment -- the prepared activations (16 KB), the
+// packed weights (128 columns x 32 B), the tile's scales and the dwords that
+// hold its zero points (128 x NBPS each) -- is copied by global_load_lds into
+// one of NST LDS stages, so NST-1 segments are in flight without a register
+// round trip.  Every thread issues the same number of DMA loads per stage
+// (kL), so "stage s has landed" is vmcnt <= (NST-2)*kL once the next stages
+// are issued; a barrier then publishes the stage to all waves.
+//
+// Each 16-k step issues 2 (row blocks) x 2 (hi, lo) v_mfma_f32_32x32x16_f16
+// into per-block partials D; at each quantisation block boundary
+// acc += scale[n, blk] * D.  Blocks that end inside a segment (block 16, 32)
+// start with a zero accumulator input and alternate between two partial
+// sets, so one block's epilogue can overlap the next block's MFMAs.
 // ---------------------------------------------------------------------------
 constexpr int kGemmBM = 64;   // two 32-row blocks
 constexpr int kGemmBN = 128;  // four 32-column blocks
 constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 
-// Prefill GEMM.  Workgroup tile 64 (M) x 128 (N), 4 waves in 1 x 4, wave
-// tile 64 x 32 (both 32-row A blocks, one 32-column weight block, so every
-// weight is dequantised once per workgroup).  Per 64-k
-// segment the workgroup stages the prepared activations (16 x 1 KB units:
-// 2 row blocks x 4 steps x hi/lo) and the packed weights (128 columns x 32 B)
-// in LDS (double-buffered).  The global loads run kGemmDepth-1 segments
-// ahead of the MFMAs through a ring of registers (the segment loop is
-// unrolled by the ring depth so every ring slot is a fixed register set),
-// so each segment's data has had several segments of compute time to
-// arrive.  Each 16-k step issues 2 (weight blocks) x 2 (hi, lo)
-// v_mfma_f32_32x32x16_f16 into per-block partials D; at each quantisation
-// block boundary acc += scale[n, blk] * D.
-constexpr int kGemmDepth = 4;
+// s_waitcnt immediate that waits for vmcnt <= n (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <int NBPS>  // quantisation blocks per 64-k segment: 1 (block >= 64), 2, 4
-__global__ __launch_bounds__(256) void k_gemm_mfma(
-    const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs, int segs4,
+template <int NBPS, int NST, int GROUPS>
+__global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
+    const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs, int segsp,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S,
     const uint8_t *__restrict__ Z, int nb, int bs_log2, int M, int N, int grid_x, int grid_y,
     float *__restrict__ Y) {
-  __shared__ uint4 sA[2][16 * 64];
-  __shared__ uint4 sW[2][kGemmBN * 2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kSz = 128 * NBPS;                 // scale (and zero-point) dwords per stage
+  constexpr int kStageU4 = 1024 + 256 + kSz / 2;  // uint4 per stage: A, W, scales + zp
+  constexpr int kL = 5 + NBPS;                    // DMA loads per thread per stage
+  extern __shared__ uint4 smem_all[];
+  // wave-uniform indices in scalar registers
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = wid >> 2, wave = wid & 3;
+  const int tid = threadIdx.x & 255, lane = tid & 63;
   const int cl = lane & 31, g = lane >> 5;
   const uint32_t magic = 0x64006400u;
+  uint4 *smem = smem_all + grp * NST * kStageU4;
+  // this group's contiguous segment range [sbeg, sbeg + nseg)
+  const int nseg = segsp / GROUPS;
+  const int sbeg = grp * nseg;
 
   // XCD-aware tile order: consecutive workgroup ids go to different XCDs
   // (round robin), so regroup them into contiguous chunks per XCD, then walk
   // the chunk kGemmGroup row bands at a time.
-  const int G = grid_x * grid_y;
+  const int Gt = grid_x * grid_y;
   int L = blockIdx.x;
-  if ((G & 7) == 0) L = (L & 7) * (G >> 3) + (L >> 3);
+  if ((Gt & 7) == 0) L = (L & 7) * (Gt >> 3) + (L >> 3);
   const int per_group = kGemmGroup * grid_x;
   const int first_y = (L / per_group) * kGemmGroup;
   const int rows_in_group = min(grid_y - first_y, kGemmGroup);
@@ -816,134 +868,150 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
   const int rb0 = ty * 2;
   const int n0 = tx * kGemmBN;
 
-  // global -> register -> LDS assignment (per segment: 4 A units + 1 weight
-  // piece per thread)
-  // The prepared activations hold segs4 (a multiple of kGemmDepth) segments,
-  // zero past K, so the pipelined loop below runs without guards.
-  const uint4 *a_base = Ap + (size_t)rb0 * segs4 * 8 * 64;
+  // DMA sources.  Activations: thread's unit pieces idx = tid + 256 i
+  // (unit idx/64 = row block (idx/64)/8, step*2+part (idx/64)%8); the
+  // prepared buffer holds segsp segments, zero past K.
+  const uint4 *a_base = Ap + (size_t)rb0 * segsp * 8 * 64;
   int a_off[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int idx = tid + 256 * i;
     const int u = idx >> 6;
-    a_off[i] = ((u >> 3) * segs4 * 8 + (u & 7)) * 64 + (idx & 63);
+    a_off[i] = ((u >> 3) * segsp * 8 + (u & 7)) * 64 + (idx & 63);
   }
   const int wcol = min(n0 + (tid >> 1), N - 1);
   const uint8_t *w_base = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
+  // scale / zero-point slots of this thread: slot = tid + 256 i, i < NBPS;
+  // slots [0, kSz) are scales, [kSz, 2 kSz) zero-point dwords, each indexed
+  // (column c, block q) as c * NBPS + q.
+  int sz_col[NBPS], sz_q[NBPS];
+  bool sz_isz[NBPS];
+#pragma unroll
+  for (int i = 0; i < NBPS; i++) {
+    int slot = tid + 256 * i;
+    sz_isz[i] = slot >= kSz;
+    if (sz_isz[i]) slot -= kSz;
+    sz_col[i] = min(n0 + slot / NBPS, N - 1);
+    sz_q[i] = slot % NBPS;
+  }
 
   // this lane's output column
   const int ccol = n0 + wave * 32 + cl;
   const bool colok = ccol < N;
   const int col = colok ? ccol : N - 1;
-  const float *s_base = S + (size_t)col * nb;
+  const int my_slot = (wave * 32 + cl) * NBPS;
 
-  float16_t acc[2], D[2];
+  auto issue = [&](int seg, int buf) {
+    const int sa_ = min(seg, segsp - 1);
+    const int sg = min(seg, segs - 1);
+    uint4 *st = smem + buf * kStageU4;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __builtin_amdgcn_global_load_lds(a_base + a_off[i] + sa_ * 512, st + 256 * i + 64 * wave,
+                                       16, 0, 0);
+    __builtin_amdgcn_global_load_lds(w_base + sg * kSegBytes, st + 1024 + 64 * wave, 16, 0, 0);
+    uint32_t *sz = (uint32_t *)(st + 1280);
+#pragma unroll
+    for (int i = 0; i < NBPS; i++) {
+      const int blk = (sa_ * kSegK + sz_q[i] * (kSegK / NBPS)) >> bs_log2;
+      const int b2 = blk < nb ? blk : nb - 1;
+      const int zi = sz_col[i] * nb + b2;
+      const void *src = sz_isz[i] ? (const void *)(Z + ((zi >> 1) & ~3))
+                                  : (const void *)(S + zi);
+      __builtin_amdgcn_global_load_lds(src, sz + 256 * i + 64 * wave, 4, 0, 0);
+    }
+  };
+
+  constexpr int kDSets = NBPS > 1 ? 2 : 1;
+  float16_t acc[2], D[kDSets][2];
+  const float16_t zero16 = {};
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       acc[t][r] = 0.0f;
-      D[t][r] = 0.0f;
+#pragma unroll
+      for (int ds = 0; ds < kDSets; ds++) D[ds][t][r] = 0.0f;
     }
 
-  // Ring slot: ext-vector members (not arrays) so every field stays in
-  // registers even before the loops over blocks are unrolled.
-  struct Stage {
-    u4vec a0, a1, a2, a3, w;
-    f4vec sc;  // raw scale loads
-    u4vec zb;  // raw zero-point bytes
-  };
-  Stage st0, st1, st2, st3;
-  const u4vec *a_vbase = (const u4vec *)a_base;
-  u4vec *sAv = (u4vec *)&sA[0][0];
-  u4vec *sWv = (u4vec *)&sW[0][0];
-
-#define MMNB_ISSUE(SLOT, SEG)                                                        \
-  {                                                                                  \
-    const int sa_ = min((SEG), segs4 - 1);                                           \
-    const int sg = min((SEG), segs - 1);                                             \
-    st##SLOT.a0 = a_vbase[a_off[0] + sa_ * 512];                                     \
-    st##SLOT.a1 = a_vbase[a_off[1] + sa_ * 512];                                     \
-    st##SLOT.a2 = a_vbase[a_off[2] + sa_ * 512];                                     \
-    st##SLOT.a3 = a_vbase[a_off[3] + sa_ * 512];                                     \
-    st##SLOT.w = *(const u4vec *)(w_base + sg * kSegBytes);                          \
-    /* loads only: arithmetic on loaded values waits for them */                   \
-    _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
-      const int blk = (sa_ * kSegK + q * (kSegK / NBPS)) >> bs_log2;                 \
-      const int b2 = blk < nb ? blk : nb - 1;                                        \
-      st##SLOT.sc[q] = s_base[b2];                                                   \
-      st##SLOT.zb[q] = Z[(col * nb + b2) >> 1];                                      \
-    }                                                                                \
+#pragma unroll
+  for (int p = 0; p < NST - 1; p++) issue(sbeg + p, p);
+  int buf = 0;
+  for (int seg = sbeg; seg < sbeg + nseg; seg++) {
+    // this thread's DMA for stage `seg` has landed; the barrier (without a
+    // fence, which would wait for every outstanding load) makes all of it
+    // visible, and frees the stage computed in the previous iteration
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kL));
+    __builtin_amdgcn_s_barrier();
+    issue(seg + NST - 1, buf == 0 ? NST - 1 : buf - 1);
+    const uint4 *st = smem + buf * kStageU4;
+    const u4vec *sAv = (const u4vec *)st;
+    const uint32_t *sS = (const uint32_t *)(st + 1280);
+    const u4vec wv = ((const u4vec *)(st + 1024))[(wave * 32 + cl) * 2 + g];
+    int zpv[NBPS];
+    float scv[NBPS];
+#pragma unroll
+    for (int q = 0; q < NBPS; q++) {
+      const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
+      const int b2 = blk < nb ? blk : nb - 1;
+      const int zi = col * nb + b2;
+      const uint32_t zd = sS[kSz + my_slot + q];
+      const float sv = __builtin_bit_cast(float, sS[my_slot + q]);
+      zpv[q] = (int)((zd >> (8 * ((zi >> 1) & 3) + 4 * (zi & 1))) & 0xF);
+      scv[q] = blk < nb ? sv : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int q = j / (4 / NBPS);
+      const int ds = (NBPS > 1) ? (q & 1) : 0;
+      const half8_t b = dequant8(wv[j], zpv[q], magic);
+      const bool fresh = (NBPS > 1) && ((j % (4 / NBPS)) == 0);
+#pragma unroll
+      for (int rb = 0; rb < 2; rb++) {
+        const half8_t ah = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + 0) * 64 + lane]);
+        const half8_t al = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + 1) * 64 + lane]);
+        D[ds][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, fresh ? zero16 : D[ds][rb],
+                                                           0, 0, 0);
+        D[ds][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[ds][rb], 0, 0, 0);
+      }
+      const bool boundary = (NBPS > 1)
+                                ? (((j + 1) % (4 / NBPS)) == 0)
+                                : (j == 3 && (((seg + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0);
+      if (boundary) {
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            acc[rb][r] = fmaf(scv[q], D[ds][rb][r], acc[rb][r]);
+            if (NBPS == 1) D[ds][rb][r] = 0.0f;
+          }
+      }
+    }
+    if (++buf == NST) buf = 0;
   }
-#define MMNB_STORE(SLOT, BUF)                                                        \
-  {                                                                                  \
-    sAv[(BUF) * 1024 + tid] = st##SLOT.a0;                                           \
-    sAv[(BUF) * 1024 + tid + 256] = st##SLOT.a1;                                     \
-    sAv[(BUF) * 1024 + tid + 512] = st##SLOT.a2;                                     \
-    sAv[(BUF) * 1024 + tid + 768] = st##SLOT.a3;                                     \
-    sWv[(BUF) * 256 + tid] = st##SLOT.w;                                             \
+  // drain the DMA still in flight (clamped stages past the end) before the
+  // LDS is reused or the workgroup exits
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if constexpr (GROUPS > 1) {
+    // partial tiles of groups 1.. -> LDS, summed by group 0
+    __syncthreads();
+    float *red = (float *)smem_all;  // (GROUPS-1) x 32 x 256 floats
+    if (grp > 0) {
+#pragma unroll
+      for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          red[((grp - 1) * 32 + rb * 16 + r) * 256 + tid] = acc[rb][r];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+    for (int gg = 1; gg < GROUPS; gg++)
+#pragma unroll
+      for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          acc[rb][r] += red[((gg - 1) * 32 + rb * 16 + r) * 256 + tid];
   }
-#define MMNB_COMPUTE(SEG, BUF, SLOT)                                                 \
-  {                                                                                  \
-    int zpv[NBPS];                                                                   \
-    float scv[NBPS];                                                                 \
-    _Pragma("unroll") for (int q = 0; q < NBPS; q++) {                               \
-      const int blk = ((SEG) * kSegK + q * (kSegK / NBPS)) >> bs_log2;               \
-      const bool inb = blk < nb;                                                     \
-      const int b2 = inb ? blk : nb - 1;                                             \
-      zpv[q] = (int)((st##SLOT.zb[q] >> (((col * nb + b2) & 1) * 4)) & 0xF);         \
-      scv[q] = inb ? st##SLOT.sc[q] : 0.0f;                                          \
-    }                                                                                \
-    const u4vec wv = sWv[(BUF) * 256 + (wave * 32 + cl) * 2 + g];                    \
-    _Pragma("unroll") for (int j = 0; j < 4; j++) {                                  \
-      const int q = j / (4 / NBPS);                                                  \
-      const half8_t b = dequant8(wv[j], zpv[q], magic);                              \
-      _Pragma("unroll") for (int rb = 0; rb < 2; rb++) {                             \
-        const half8_t ah = __builtin_bit_cast(                                       \
-            half8_t, sAv[(BUF) * 1024 + (rb * 8 + j * 2 + 0) * 64 + lane]);          \
-        const half8_t al = __builtin_bit_cast(                                       \
-            half8_t, sAv[(BUF) * 1024 + (rb * 8 + j * 2 + 1) * 64 + lane]);          \
-        D[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, D[rb], 0, 0, 0);       \
-        D[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[rb], 0, 0, 0);       \
-      }                                                                              \
-      const bool boundary =                                                          \
-          (NBPS > 1) ? (((j + 1) % (4 / NBPS)) == 0)                                 \
-                     : (j == 3 && ((((SEG) + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0); \
-      if (boundary) {                                                                \
-        _Pragma("unroll") for (int rb = 0; rb < 2; rb++)                             \
-            _Pragma("unroll") for (int r = 0; r < 16; r++) {                         \
-          acc[rb][r] = fmaf(scv[q], D[rb][r], acc[rb][r]);                           \
-          D[rb][r] = 0.0f;                                                           \
-        }                                                                            \
-      }                                                                              \
-    }                                                                                \
-  }
-// SUB(D0, ISSUE_SLOT, NEXT_SLOT): ring slots are literal tokens
-#define MMNB_SUB(D0, ISLOT, NSLOT)                                                   \
-  {                                                                                  \
-    const int s = s0 + (D0);                                                         \
-    MMNB_ISSUE(ISLOT, s + kGemmDepth - 1);                                           \
-    MMNB_COMPUTE(s, (D0) & 1, D0);                                                   \
-    MMNB_STORE(NSLOT, ((D0) + 1) & 1);                                               \
-    __syncthreads();                                                                 \
-  }
-
-  // prologue: segments 0..depth-2 in flight, segment 0 staged
-  MMNB_ISSUE(0, 0);
-  MMNB_ISSUE(1, 1);
-  MMNB_ISSUE(2, 2);
-  MMNB_STORE(0, 0);
-  __syncthreads();
-  for (int s0 = 0; s0 < segs4; s0 += kGemmDepth) {
-    MMNB_SUB(0, 3, 1);
-    MMNB_SUB(1, 0, 2);
-    MMNB_SUB(2, 1, 3);
-    MMNB_SUB(3, 2, 0);
-  }
-#undef MMNB_SUB
-#undef MMNB_COMPUTE
-#undef MMNB_STORE
-#undef MMNB_ISSUE
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
   if (colok) {
@@ -961,31 +1029,55 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(
 static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y) {
   const int64_t segs = p->k64 / kSegK;
-  const int64_t segs4 = (segs + kGemmDepth - 1) / kGemmDepth * kGemmDepth;
   const int64_t mpad = (m + kGemmBM - 1) / kGemmBM * kGemmBM;
+  const int gx = (int)((p->n + kGemmBN - 1) / kGemmBN), gy = (int)(mpad / kGemmBM);
+  const int nbps = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
+  // K split over two wave groups when the tiles alone leave CUs with one
+  // wave per SIMD; each group's range covers whole quantisation blocks.
+  const int groups = ((int64_t)gx * gy < 2 * (int64_t)ctx->cu_count && segs >= 16) ? 2 : 1;
+  const int nst = ctx->gemm_stages;
+  const int64_t align = groups * std::max<int64_t>(1, p->block / kSegK);
+  const int64_t segsp = (segs + align - 1) / align * align;
   const int64_t rblocks = mpad / 32;
-  const size_t ap_bytes = (size_t)(rblocks * segs4 * 4 * 2 * 64) * 16;
+  const size_t ap_bytes = (size_t)(rblocks * segsp * 4 * 2 * 64) * 16;
+  const size_t shmem = (size_t)groups * nst * (1024 + 256 + 64 * nbps) * 16;
+  if (shmem > (size_t)ctx->lds_max)
+    return fail(MMNB_ERR_UNSUPPORTED, "GEMM: LDS stages exceed the device limit");
   void *d_ap = nullptr, *d_exp = nullptr;
   int rc;
   if ((rc = scratch_get(ctx, 2, ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)mpad * 4, &d_exp))) return rc;
-  if ((rc = launch(ctx, kKernPrep, k_prep_rowexp, dim3((unsigned)((m + 3) / 4)), dim3(256), 0,
-                    d_a, lda, m, p->k, (int *)d_exp)))
+  if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(mpad / kPrepRows)), dim3(256), 0,
+                    d_a, lda, m, p->k, segsp, (int *)d_exp, (uint4 *)d_ap)))
     return rc;
-  if ((rc = launch(ctx, kKernPrep, k_prep_convert, dim3((unsigned)segs4, (unsigned)rblocks),
-                    dim3(256), 0, d_a, lda, m, p->k, segs4, (const int *)d_exp, (uint4 *)d_ap)))
-    return rc;
-  const int gx = (int)((p->n + kGemmBN - 1) / kGemmBN), gy = (int)(mpad / kGemmBM);
   const int bs_log2 = ilog2(p->block);
   const dim3 grid((unsigned)(gx * gy));
-#define MMNB_GEMM_LAUNCH(Q)                                                                   \
-  return launch(ctx, kKernGemm, k_gemm_mfma<Q>, grid, dim3(256), 0, (const uint4 *)d_ap,     \
-                (const int *)d_exp, (int)segs, (int)segs4, p->d_w, p->col_bytes,            \
-                p->d_scales, p->d_zp,                                                         \
-                (int)p->n_blocks, bs_log2, (int)m, (int)p->n, gx, gy, d_y)
-  if (p->block >= 64) MMNB_GEMM_LAUNCH(1);
-  if (p->block == 32) MMNB_GEMM_LAUNCH(2);
-  MMNB_GEMM_LAUNCH(4);
+#define MMNB_GEMM_LAUNCH(Q, NS, GR)                                                          \
+  {                                                                                          \
+    auto kern = k_gemm_mfma<Q, NS, GR>;                                                      \
+    if (shmem > 65536) {                                                                     \
+      hipError_t e_ = hipFuncSetAttribute(                                                   \
+          (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);       \
+      if (e_ != hipSuccess) return check_hip(e_, "hipFuncSetAttribute");                     \
+    }                                                                                        \
+    return launch(ctx, kKernGemm, kern, grid, dim3(256 * GR), shmem, (const uint4 *)d_ap,   \
+                  (const int *)d_exp, (int)segs, (int)segsp, p->d_w, p->col_bytes,          \
+                  p->d_scales, p->d_zp, (int)p->n_blocks, bs_log2, (int)m, (int)p->n, gx,   \
+                  gy, d_y);                                                                  \
+  }
+#define MMNB_GEMM_NB(NS, GR)                     \
+  {                                              \
+    if (nbps == 1) MMNB_GEMM_LAUNCH(1, NS, GR);  \
+    if (nbps == 2) MMNB_GEMM_LAUNCH(2, NS, GR);  \
+    MMNB_GEMM_LAUNCH(4, NS, GR);                 \
+  }
+  if (groups == 2) {
+    if (nst == 3) MMNB_GEMM_NB(3, 2);
+    MMNB_GEMM_NB(2, 2);
+  }
+  if (nst == 3) MMNB_GEMM_NB(3, 1);
+  MMNB_GEMM_NB(2, 1);
+#undef MMNB_GEMM_NB
 #undef MMNB_GEMM_LAUNCH
 }
 

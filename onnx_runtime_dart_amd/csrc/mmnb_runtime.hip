@@ -120,6 +120,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v == 1 || v == 2 || v == 4 || v == 8) ctx->gemv_r = v;
   }
+  if (const char *r = std::getenv("MMNB_GEMM_STAGES")) {
+    const int v = std::atoi(r);
+    if (v == 2 || v == 3) ctx->gemm_stages = v;
+  }
   if (const char *r = std::getenv("MMNB_GEMV_CG")) {
     const int v = std::atoi(r);
     if (v >= 1 && v <= 8) ctx->gemv_cg = v;

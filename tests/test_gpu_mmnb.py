@@ -127,6 +127,11 @@ def test_prefill_full_size_row_sample(ctx, m, n, block):
     (6, 64, 1000, 64, False),   # one chunk per column, many column groups
     (3, 3072, 1024, 128, False),
     (8, 8192, 40, 64, True),    # A too large for one workgroup's LDS: GEMM path
+    # GEMM with K split over two wave groups (few tiles, K >= 1024)
+    (64, 2000, 100, 16, True),  # block 16, K not a multiple of 64
+    (33, 5000, 130, 256, True),  # block 256: group ranges aligned to 4 segments
+    (128, 1024, 256, 512, False),  # block 512: 8 segments per block
+    (100, 1100, 96, 32, True),
 ])
 def test_edge_shapes(ctx, m, k, n, block, zp):
     p = synth.mmnb_problem(m, k, n, block, zp, seed=11 + m + n)
