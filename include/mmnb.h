@@ -179,6 +179,93 @@ int mmnb_dynamic_matmul_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
                             int32_t *d_a_zero_point, int32_t *d_acc,
                             float *d_y);
 
+/* ---- decoder ops around MatMulNBits -------------------------------------
+ * Device buffers, asynchronous on the context stream (like the _dev entry
+ * points above).  fp32 throughout. */
+
+/* RMSNorm over the last axis: y[r] = x[r] * gamma / sqrt(mean(x[r]^2) + eps)
+ * for rows x dim row-major x and y, gamma [dim].  Sum of squares, the
+ * normaliser and the products in double, one binary32 rounding per output.
+ * Replaces: opRMSNorm (lib/src/onnx_ops.dart:1436-1461, last-axis case), as
+ * dispatched for the fused RMSNorm pattern and SimplifiedLayerNormalization
+ * (lib/src/onnx_graph.dart:973-977, :1008-1013). */
+int mmnb_rmsnorm_dev(mmnb_ctx *ctx, const float *d_x, int64_t rows, int64_t dim,
+                     const float *d_gamma, float eps, float *d_y);
+
+/* RotaryEmbedding of x [batch, seq, hidden] (heads = num_heads, or
+ * hidden / (2 half_rot) when num_heads is 0) at positions d_pos (int64,
+ * [seq] when pos_rank is 1, [batch, seq] when 2); cos/sin caches
+ * [max_pos, half_rot].  Rotation in double as the reference.
+ * Replaces: opRotaryEmbedding (lib/src/onnx_ops.dart:2121-2181), dispatch
+ * arm 'RotaryEmbedding' (lib/src/onnx_graph.dart:1001-1007). */
+int mmnb_rotary_dev(mmnb_ctx *ctx, const float *d_x, int64_t batch, int64_t seq,
+                    int64_t hidden, int64_t num_heads, const int64_t *d_pos,
+                    int64_t pos_rank, const float *d_cos, const float *d_sin,
+                    int64_t half_rot, int interleaved, float *d_y);
+
+/* GroupQueryAttention: q [batch, seq, num_heads*head_size], k/v [batch, seq,
+ * kv_heads*head_size], optional past [batch, kv_heads, past_len, head_size],
+ * optional rotary (cos/sin [max_pos, half_rot], positions past_len..),
+ * optional additive bias [batch, bias_heads, seq, past_len+seq]; scale <= 0
+ * means 1/sqrt(head_size).  Writes out [batch, seq, num_heads*head_size] and
+ * present_k/present_v [batch, kv_heads, past_len+seq, head_size].
+ * head_size <= 128.  Rotary with batch > 1 is rejected (MMNB_ERR_ARG), as
+ * the reference's position ids [1, seq] are indexed per batch and throw.
+ * Replaces: opGroupQueryAttention (lib/src/onnx_ops.dart:1508-1640), dispatch
+ * arm 'GroupQueryAttention' (lib/src/onnx_graph.dart:978-993). */
+int mmnb_gqa_dev(mmnb_ctx *ctx, const float *d_q, const float *d_k, const float *d_v,
+                 int64_t batch, int64_t seq, int64_t num_heads, int64_t kv_heads,
+                 int64_t head_size, float scale, const float *d_past_k,
+                 const float *d_past_v, int64_t past_len, const float *d_cos,
+                 const float *d_sin, int64_t half_rot, int do_rotary, int interleaved,
+                 const float *d_bias, int64_t bias_heads, float *d_out,
+                 float *d_present_k, float *d_present_v);
+
+/* ---- decoder session ----------------------------------------------------
+ * A Qwen3-shaped int4 decoder (per layer: RMSNorm, MatMulNBits q/k/v,
+ * per-head q/k RMSNorm, GroupQueryAttention with rotary and KV cache,
+ * MatMulNBits o + residual, RMSNorm, MatMulNBits gate/up, SiLU * up,
+ * MatMulNBits down + residual; final RMSNorm, MatMulNBits lm_head, greedy
+ * argmax) with every weight, the KV cache and the step state in HBM.
+ * Packs (mmnb_pack_nbits, block >= 64, no zero points) are the caller's and
+ * must outlive the session: q/k/v concatenated along N (q | k | v), gate/up
+ * interleaved along N (column 2j = gate j, 2j+1 = up j).  A decode step is
+ * recorded once as a HIP graph and replayed per token.
+ * Replaces: the node sequence an int4 export runs through the reference's
+ * executor for one forward pass (OnnxModel.run, lib/onnx_runtime_dart.dart
+ * :45-141) and the greedy loop around it (tool/smollm2_generate.dart:48-83);
+ * MatMulNBits nodes use the kernels of mmnb_matmul_nbits. */
+typedef struct mmnb_decoder mmnb_decoder;
+typedef struct mmnb_decoder_config {
+  int64_t layers, hidden, heads, kv_heads, head_dim, intermediate, vocab, max_len;
+  float eps;        /* RMSNorm epsilon */
+  float rope_theta; /* rotary base: angle = pos * theta^(-2i/head_dim) */
+} mmnb_decoder_config;
+
+/* embed fp32 [vocab, hidden] and final_norm [hidden] are copied to HBM. */
+int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg,
+                        const float *embed, const float *final_norm,
+                        const mmnb_pack *lm_head, mmnb_decoder **out);
+/* Norm weights are copied; packs are referenced. */
+int mmnb_decoder_set_layer(mmnb_decoder *dec, int64_t layer, const float *ln1,
+                           const float *ln2, const float *q_norm, const float *k_norm,
+                           const mmnb_pack *qkv, const mmnb_pack *o,
+                           const mmnb_pack *gate_up, const mmnb_pack *down);
+/* Prompt tokens through the model (KV cache grows by n); *next_token is the
+ * greedy token of the last row. */
+int mmnb_decoder_prefill(mmnb_decoder *dec, const int64_t *tokens, int64_t n,
+                         int32_t *next_token);
+/* `steps` greedy decode steps, each feeding the previous step's token;
+ * tokens[i] (may be NULL) receives step i's token. */
+int mmnb_decoder_decode(mmnb_decoder *dec, int64_t steps, int32_t *tokens);
+/* Logits [vocab] of the last position computed. */
+int mmnb_decoder_logits(mmnb_decoder *dec, float *logits);
+/* Tokens held in the KV cache. */
+int mmnb_decoder_position(mmnb_decoder *dec, int64_t *pos);
+/* Empty the KV cache (weights stay). */
+int mmnb_decoder_reset(mmnb_decoder *dec);
+int mmnb_decoder_free(mmnb_decoder *dec);
+
 /* ---- packs ------------------------------------------------------------- */
 
 /* Free a pack's device memory.  Mirrors dropping the initializer Tensor

@@ -63,7 +63,28 @@ SIGNATURES = {
     "mmnb_graph_end": (_int, [_vp, _P(_vp)]),
     "mmnb_graph_launch": (_int, [_vp, _vp]),
     "mmnb_graph_destroy": (_int, [_vp, _vp]),
+    "mmnb_rmsnorm_dev": (_int, [_vp, _vp, _i64, _i64, _vp, ctypes.c_float, _vp]),
+    "mmnb_rotary_dev": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64,
+                               _int, _vp]),
+    "mmnb_gqa_dev": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+                            _vp, _vp, _i64, _vp, _vp, _i64, _int, _int, _vp, _i64, _vp, _vp,
+                            _vp]),
+    "mmnb_decoder_create": (_int, [_vp, _vp, _vp, _vp, _vp, _P(_vp)]),
+    "mmnb_decoder_set_layer": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mmnb_decoder_prefill": (_int, [_vp, _vp, _i64, _P(ctypes.c_int32)]),
+    "mmnb_decoder_decode": (_int, [_vp, _i64, _vp]),
+    "mmnb_decoder_logits": (_int, [_vp, _vp]),
+    "mmnb_decoder_position": (_int, [_vp, _P(_i64)]),
+    "mmnb_decoder_reset": (_int, [_vp]),
+    "mmnb_decoder_free": (_int, [_vp]),
 }
+
+
+class DecoderConfig(ctypes.Structure):
+    """mmnb_decoder_config (include/mmnb.h)."""
+    _fields_ = [("layers", _i64), ("hidden", _i64), ("heads", _i64), ("kv_heads", _i64),
+                ("head_dim", _i64), ("intermediate", _i64), ("vocab", _i64),
+                ("max_len", _i64), ("eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
 
 _lib = None
 _lock = threading.RLock()

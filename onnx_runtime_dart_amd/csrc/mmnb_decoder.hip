@@ -1,0 +1,970 @@
+// Decoder ops around MatMulNBits on gfx950, and a Qwen3-shaped int4 decoder
+// session built from them.
+//
+//   RMSNorm              opRMSNorm (lib/src/onnx_ops.dart:1436-1490)
+//   RotaryEmbedding      opRotaryEmbedding (:2121-2181)
+//   GroupQueryAttention  opGroupQueryAttention (:1508-1640)
+//
+// The op kernels keep the reference's arithmetic where it is cheap to do so
+// (sums of squares, rotations and the softmax normaliser in double, one
+// binary32 rounding per stored value); the attention products run in fp32.
+//
+// The decoder session keeps every weight pack, the KV cache and the step
+// state in HBM.  Prefill runs the general kernels over all prompt rows; a
+// decode step is five launches per layer (fused RMSNorm + MatMulNBits
+// prologues, residual / SwiGLU / greedy-argmax epilogues, one attention
+// kernel) and is captured once as a HIP graph whose kernels read the
+// position and token from device memory, so replaying it advances the
+// sequence with no host work.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "mmnb_internal.h"
+
+namespace mmnb {
+
+// ---------------------------------------------------------------------------
+// Block-wide sums (256 threads).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double block_sum_d(double v, double *sh) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) sh[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  const int nw = (blockDim.x + 63) >> 6;
+  for (int i = 0; i < nw; i++) t += sh[i];
+  return t;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm over the last axis, one workgroup per row.  With `add` non-null
+// the row is first replaced by x + add (the residual Add node before the
+// norm), written back to `xsum`.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *X, int64_t dim,
+                                                 const float *__restrict__ G, float eps,
+                                                 float *__restrict__ Y, const float *add,
+                                                 float *xsum) {
+  __shared__ double sh[4];
+  const int64_t r = blockIdx.x;
+  const float *x = X + r * dim;
+  double ss = 0.0;
+  for (int64_t k = threadIdx.x; k < dim; k += blockDim.x) {
+    float v = x[k];
+    if (add) {
+      v = v + add[r * dim + k];
+      xsum[r * dim + k] = v;
+    }
+    ss += (double)v * (double)v;
+  }
+  ss = block_sum_d(ss, sh);
+  const double inv = 1.0 / sqrt(ss / (double)dim + (double)eps);
+  const float *xs = add ? xsum + r * dim : x;
+  for (int64_t k = threadIdx.x; k < dim; k += blockDim.x)
+    Y[r * dim + k] = (float)((double)xs[k] * inv * (double)G[k]);
+}
+
+// ---------------------------------------------------------------------------
+// Rotary embedding of one [heads, head] row block at position p (3-D layout
+// [b, s, heads * head]).  Rotated pairs in double, as the reference.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void rotate_row(const float *x, float *y, int heads, int head,
+                                           int half_rot, int interleaved, const float *cos,
+                                           const float *sin, int64_t p) {
+  const int rot = 2 * half_rot;
+  for (int e = threadIdx.x; e < heads * head; e += blockDim.x) {
+    const int h = e / head, i = e % head;
+    const float *xh = x + (int64_t)h * head;
+    float out;
+    if (i >= rot) {
+      out = xh[i];
+    } else if (interleaved) {
+      const int pi = i >> 1;
+      const double c = cos[p * half_rot + pi], sn = sin[p * half_rot + pi];
+      const double x0 = xh[2 * pi], x1 = xh[2 * pi + 1];
+      out = (float)((i & 1) ? x1 * c + x0 * sn : x0 * c - x1 * sn);
+    } else {
+      const int hr = half_rot;
+      const int pi = i < hr ? i : i - hr;
+      const double c = cos[p * half_rot + pi], sn = sin[p * half_rot + pi];
+      const double x0 = xh[pi], x1 = xh[pi + hr];
+      out = (float)(i < hr ? x0 * c - x1 * sn : x1 * c + x0 * sn);
+    }
+    y[(int64_t)h * head + i] = out;
+  }
+}
+
+// One workgroup per (b, s) row.  pos: int64 [s] (rank 1) or [b, s].
+__global__ __launch_bounds__(256) void k_rotary(const float *__restrict__ X, int64_t seq,
+                                                int heads, int head,
+                                                const int64_t *__restrict__ pos, int pos_rank,
+                                                int64_t pos_const, const float *__restrict__ cos,
+                                                const float *__restrict__ sin, int half_rot,
+                                                int interleaved, float *__restrict__ Y) {
+  const int64_t row = blockIdx.x;  // b * seq + s
+  const int64_t s = row % seq;
+  const int64_t p = pos ? (pos_rank == 1 ? pos[s] : pos[row]) : pos_const + s;
+  const int64_t hid = (int64_t)heads * head;
+  rotate_row(X + row * hid, Y + row * hid, heads, head, half_rot, interleaved, cos, sin, p);
+}
+
+// ---------------------------------------------------------------------------
+// present[b, kvh, cap] = past[b, kvh, 0:P] ++ new[b, s, kvh] (k and v)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_gqa_present(
+    const float *__restrict__ past_k, const float *__restrict__ past_v, int64_t P,
+    const float *__restrict__ k, const float *__restrict__ v, int64_t seq, int kvh, int hd,
+    int64_t cap, float *__restrict__ pk, float *__restrict__ pv) {
+  const int64_t b = blockIdx.y, hh = blockIdx.x % kvh, j = blockIdx.x / kvh;  // j < P + seq
+  const int64_t dst = ((b * kvh + hh) * cap + j) * hd;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float kv, vv;
+    if (j < P) {
+      const int64_t src = ((b * kvh + hh) * P + j) * hd + d;
+      kv = past_k[src];
+      vv = past_v[src];
+    } else {
+      const int64_t src = ((b * seq + (j - P)) * kvh + hh) * hd + d;
+      kv = k[src];
+      vv = v[src];
+    }
+    pk[dst + d] = kv;
+    pv[dst + d] = vv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attention rows: query i (absolute position P + i) of head h attends
+// causally to keys 0..P+i of the present cache [b, kvh, cap, hd], plus an
+// optional additive bias [b, bias_heads, seq, total].  A workgroup takes
+// 16 queries of one head; key tiles of 32 are staged in LDS; thread
+// (query qi, lane kl of 16) scores keys kl and kl+16 of a tile and owns
+// output dims d = kl (mod 16); online softmax per query.  hd <= 128.
+// ---------------------------------------------------------------------------
+constexpr int kAttnQ = 16, kAttnKT = 32, kAttnMaxHd = 128;
+
+__global__ __launch_bounds__(256) void k_attn_rows(
+    const float *__restrict__ Q, int64_t q_row_stride, int64_t seq, int nh, int kvh, int hd,
+    const float *__restrict__ pk, const float *__restrict__ pv, int64_t cap, int64_t P,
+    float scale, const float *__restrict__ bias, int bias_heads, float *__restrict__ out,
+    int64_t out_row_stride) {
+  __shared__ float sK[kAttnKT][kAttnMaxHd + 1];
+  __shared__ float sV[kAttnKT][kAttnMaxHd];
+  __shared__ float sQ[kAttnQ][kAttnMaxHd];
+  __shared__ float sP[kAttnQ][kAttnKT];
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int kv = h / (nh / kvh);
+  const int qi = threadIdx.x >> 4, kl = threadIdx.x & 15;
+  const int64_t i = (int64_t)blockIdx.x * kAttnQ + qi;  // query row
+  const bool qok = i < seq;
+  const int64_t T = P + seq;
+  for (int e = threadIdx.x; e < kAttnQ * hd; e += blockDim.x) {
+    const int r = e / hd, d = e % hd;
+    const int64_t ii = (int64_t)blockIdx.x * kAttnQ + r;
+    sQ[r][d] = ii < seq ? Q[(b * seq + ii) * q_row_stride + (int64_t)h * hd + d] : 0.0f;
+  }
+  const float *Kb = pk + (b * kvh + kv) * cap * hd;
+  const float *Vb = pv + (b * kvh + kv) * cap * hd;
+  const int64_t last = qok ? P + i : -1;  // last key this query sees
+  const int64_t q0 = (int64_t)blockIdx.x * kAttnQ;
+  const int64_t qmax = std::min<int64_t>(q0 + kAttnQ, seq) - 1;
+  const int64_t kend = P + qmax + 1;  // keys any query of the block sees
+  float m = -INFINITY, l = 0.0f;
+  float o[kAttnMaxHd / 16];
+#pragma unroll
+  for (int e = 0; e < kAttnMaxHd / 16; e++) o[e] = 0.0f;
+  for (int64_t k0 = 0; k0 < kend; k0 += kAttnKT) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kAttnKT * hd; e += blockDim.x) {
+      const int j = e / hd, d = e % hd;
+      const bool ok = k0 + j < T;
+      sK[j][d] = ok ? Kb[(k0 + j) * hd + d] : 0.0f;
+      sV[j][d] = ok ? Vb[(k0 + j) * hd + d] : 0.0f;
+    }
+    __syncthreads();
+    float sc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int j = kl + 16 * u;
+      const int64_t kj = k0 + j;
+      float dot = 0.0f;
+      for (int d = 0; d < hd; d++) dot = fmaf(sQ[qi][d], sK[j][d], dot);
+      float v = dot * scale;
+      if (bias && qok && kj <= last)
+        v += bias[((b * bias_heads + (h % bias_heads)) * seq + i) * T + kj];
+      sc[u] = (qok && kj <= last) ? v : -INFINITY;
+    }
+    // tile max over the 16 lanes of this query
+    float tm = fmaxf(sc[0], sc[1]);
+    for (int off = 8; off > 0; off >>= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 16));
+    const float mn = fmaxf(m, tm);
+    float p0 = 0.0f, p1 = 0.0f, corr = 1.0f;
+    if (mn != -INFINITY) {
+      p0 = sc[0] == -INFINITY ? 0.0f : expf(sc[0] - mn);
+      p1 = sc[1] == -INFINITY ? 0.0f : expf(sc[1] - mn);
+      corr = m == -INFINITY ? 0.0f : expf(m - mn);
+    }
+    float ps = p0 + p1;
+    for (int off = 8; off > 0; off >>= 1) ps += __shfl_xor(ps, off, 16);
+    l = l * corr + ps;
+    m = mn;
+    sP[qi][kl] = p0;
+    sP[qi][kl + 16] = p1;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kAttnMaxHd / 16; e++) {
+      const int d = kl + 16 * e;
+      if (d < hd) {
+        float acc = o[e] * corr;
+        for (int j = 0; j < kAttnKT; j++) acc = fmaf(sP[qi][j], sV[j][d], acc);
+        o[e] = acc;
+      }
+    }
+  }
+  if (qok) {
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int e = 0; e < kAttnMaxHd / 16; e++) {
+      const int d = kl + 16 * e;
+      if (d < hd) out[(b * seq + i) * out_row_stride + (int64_t)h * hd + d] = o[e] * inv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decoder prefill helpers.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_embed_rows(const int64_t *__restrict__ tok,
+                                                    const float *__restrict__ table, int64_t H,
+                                                    float *__restrict__ x) {
+  const int64_t r = blockIdx.x;
+  const float *src = table + tok[r] * H;
+  for (int64_t k = threadIdx.x; k < H; k += blockDim.x) x[r * H + k] = src[k];
+}
+
+// Per-head RMSNorm of q / k then rotary, one workgroup (hd threads) per
+// (row, head); k and v land in the cache at position P + row.
+__device__ __forceinline__ float head_norm_rope(float x, const float *__restrict__ g, float eps,
+                                                int hd, const float *__restrict__ cos,
+                                                const float *__restrict__ sin, int64_t p,
+                                                float *sh, double *shd) {
+  const int d = threadIdx.x;
+  const double ss = block_sum_d((double)x * (double)x, shd);
+  const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
+  const float xn = (float)((double)x * inv * (double)g[d]);
+  sh[d] = xn;
+  __syncthreads();
+  const int hr = hd / 2;
+  const int pi = d < hr ? d : d - hr;
+  const double c = cos[p * hr + pi], sn = sin[p * hr + pi];
+  const double x0 = sh[pi], x1 = sh[pi + hr];
+  const float r = (float)(d < hr ? x0 * c - x1 * sn : x1 * c + x0 * sn);
+  __syncthreads();
+  return r;
+}
+
+__global__ void k_qk_prep_rows(const float *__restrict__ qkv, int64_t qkv_stride, int nh,
+                               int kvh, int hd, const float *__restrict__ qn,
+                               const float *__restrict__ kn, float eps,
+                               const float *__restrict__ cos, const float *__restrict__ sin,
+                               int64_t P, float *__restrict__ qout, float *__restrict__ ck,
+                               float *__restrict__ cv, int64_t cap) {
+  __shared__ float sh[kAttnMaxHd];
+  __shared__ double shd[4];
+  const int64_t r = blockIdx.x;
+  const int hi = blockIdx.y;
+  const int d = threadIdx.x;
+  const float *row = qkv + r * qkv_stride;
+  const int64_t p = P + r;
+  if (hi < nh) {
+    const float y = head_norm_rope(row[hi * hd + d], qn, eps, hd, cos, sin, p, sh, shd);
+    qout[r * (int64_t)nh * hd + hi * hd + d] = y;
+  } else {
+    const int kh = hi - nh;
+    const float y = head_norm_rope(row[(nh + kh) * hd + d], kn, eps, hd, cos, sin, p, sh, shd);
+    ck[((int64_t)kh * cap + p) * hd + d] = y;
+    cv[((int64_t)kh * cap + p) * hd + d] = row[(nh + kvh + kh) * hd + d];
+  }
+}
+
+// a[r, j] = silu(gu[r, 2j]) * gu[r, 2j+1]: sigmoid in double stored as
+// binary32, then two binary32 products (the Sigmoid, Mul, Mul nodes).
+__global__ __launch_bounds__(256) void k_swiglu_rows(const float *__restrict__ gu, int64_t I,
+                                                     float *__restrict__ a) {
+  const int64_t r = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= I) return;
+  const float g = gu[r * 2 * I + 2 * j], u = gu[r * 2 * I + 2 * j + 1];
+  const float sig = (float)(1.0 / (1.0 + exp(-(double)g)));
+  a[r * I + j] = (g * sig) * u;
+}
+
+// ---------------------------------------------------------------------------
+// Decode step.  State lives in device memory so a captured graph advances
+// the sequence by itself.
+// ---------------------------------------------------------------------------
+struct DecState {
+  int pos;    // position of the token being fed
+  int token;  // token being fed
+  int step;   // decode steps taken (index into the output list)
+  int pad;
+  unsigned long long argmax;  // (orderable logit, ~index) of the best logit
+};
+
+__global__ __launch_bounds__(256) void k_dec_begin(DecState *__restrict__ st,
+                                                   const float *__restrict__ table, int64_t H,
+                                                   int64_t vocab, float *__restrict__ x) {
+  // the token comes from the previous step's argmax, always in range; the
+  // clamp only keeps a corrupted state from reading outside the table
+  int64_t tok = st->token;
+  tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+  for (int64_t k = threadIdx.x; k < H; k += blockDim.x) x[k] = table[tok * H + k];
+  if (threadIdx.x == 0) st->argmax = 0ull;
+}
+
+__global__ void k_dec_end(DecState *__restrict__ st, int32_t *__restrict__ out_tokens,
+                          int out_cap) {
+  if (threadIdx.x == 0) {
+    const unsigned long long key = st->argmax;
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+    st->token = tok;
+    if (st->step >= 0 && st->step < out_cap) out_tokens[st->step] = tok;
+    st->step += 1;
+    st->pos += 1;
+  }
+}
+
+// Decode attention for one token.  Grid (splits, heads): split s scores keys
+// [32 s, 32 s + 32) of the L = pos + 1 visible ones and writes a partial
+// (max, sum, o[hd]); the last split of a head to finish (device-scope
+// counter, reset by it) combines them.  Every workgroup first forms its
+// head's q (per-head RMSNorm, rotary at pos); the split holding key pos
+// forms the new k and v itself (and the first head of the group writes them
+// into the cache at pos), so no workgroup reads a cache entry written in
+// the same launch.  hd == 128 threads' worth of work per 128-thread group.
+constexpr int kDecKeys = 32;
+
+__global__ __launch_bounds__(256) void k_dec_attn(
+    const DecState *__restrict__ st, const float *__restrict__ qkv, int nh, int kvh, int hd,
+    const float *__restrict__ qn, const float *__restrict__ kn, float eps,
+    const float *__restrict__ cos, const float *__restrict__ sin, float *ck, float *cv,
+    int64_t cap, float scale, float *part, int *counters, float *__restrict__ out) {
+  __shared__ float sq[kAttnMaxHd], skn[kAttnMaxHd], svn[kAttnMaxHd], sh[kAttnMaxHd];
+  __shared__ double shd[4];
+  __shared__ float ssc[kDecKeys];
+  __shared__ float sred[2][kAttnMaxHd];
+  __shared__ int s_last;
+  const int split = blockIdx.x, h = blockIdx.y;
+  const int group = nh / kvh, kh = h / group;
+  const int pos = st->pos;
+  const int L = pos + 1;
+  const int nsplit = (L + kDecKeys - 1) / kDecKeys;
+  if (split >= nsplit) return;  // uniform per workgroup
+  const int t = threadIdx.x;
+  const int d = t & (kAttnMaxHd - 1);
+  const bool lo = t < hd;       // first hd threads do the per-head vector work
+  // ---- q (and the new k, v for the split holding key pos); the vector
+  // work below is done by threads [0, hd) with blockDim == 256 and
+  // hd <= 128; the block sums include every thread (zeros from the rest)
+  {
+    const float xq = lo ? qkv[h * hd + d] : 0.0f;
+    const double ss = block_sum_d((double)xq * (double)xq, shd);
+    const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
+    if (lo) sh[d] = (float)((double)xq * inv * (double)qn[d]);
+    __syncthreads();
+    if (lo) {
+      const int hr = hd / 2, pi = d < hr ? d : d - hr;
+      const double c = cos[(int64_t)pos * hr + pi], sn = sin[(int64_t)pos * hr + pi];
+      const double x0 = sh[pi], x1 = sh[pi + hr];
+      sq[d] = (float)(d < hr ? x0 * c - x1 * sn : x1 * c + x0 * sn);
+    }
+    __syncthreads();
+  }
+  const bool has_new = split == nsplit - 1;
+  if (has_new) {
+    const float xk = lo ? qkv[(nh + kh) * hd + d] : 0.0f;
+    const double ss = block_sum_d((double)xk * (double)xk, shd);
+    const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
+    if (lo) sh[d] = (float)((double)xk * inv * (double)kn[d]);
+    __syncthreads();
+    if (lo) {
+      const int hr = hd / 2, pi = d < hr ? d : d - hr;
+      const double c = cos[(int64_t)pos * hr + pi], sn = sin[(int64_t)pos * hr + pi];
+      const double x0 = sh[pi], x1 = sh[pi + hr];
+      const float kr = (float)(d < hr ? x0 * c - x1 * sn : x1 * c + x0 * sn);
+      const float vv = qkv[(nh + kvh + kh) * hd + d];
+      skn[d] = kr;
+      svn[d] = vv;
+      if (h % group == 0) {
+        ck[((int64_t)kh * cap + pos) * hd + d] = kr;
+        cv[((int64_t)kh * cap + pos) * hd + d] = vv;
+      }
+    }
+    __syncthreads();
+  }
+  // ---- scores of this split's keys: 8 threads per key, hd/8 dims each
+  const int j0 = split * kDecKeys;
+  const int nk = min(kDecKeys, L - j0);
+  const float *Kb = ck + (int64_t)kh * cap * hd;
+  const float *Vb = cv + (int64_t)kh * cap * hd;
+  {
+    const int jl = t >> 3, part8 = t & 7;
+    const int j = j0 + jl;
+    float dot = 0.0f;
+    if (jl < nk) {
+      const int dpt = hd / 8;
+      for (int e = 0; e < dpt; e++) {
+        const int dd = part8 * dpt + e;
+        const float kvv = (j == pos) ? skn[dd] : Kb[(int64_t)j * hd + dd];
+        dot = fmaf(sq[dd], kvv, dot);
+      }
+    }
+    for (int off = 4; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 8);
+    if (part8 == 0 && jl < kDecKeys) ssc[jl] = jl < nk ? dot * scale : -INFINITY;
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int jl = 0; jl < nk; jl++) mx = fmaxf(mx, ssc[jl]);
+  // ---- o = sum p_j v_j: thread (d, half) sums half of the keys
+  {
+    const int half = t >> 7;
+    float acc = 0.0f, ls = 0.0f;
+    if (d < hd) {
+      for (int jl = half; jl < nk; jl += 2) {
+        const float p = expf(ssc[jl] - mx);
+        const int j = j0 + jl;
+        const float vv = (j == pos) ? svn[d] : Vb[(int64_t)j * hd + d];
+        acc = fmaf(p, vv, acc);
+        ls += p;
+      }
+    }
+    sred[half][d] = acc;
+    __syncthreads();
+    if (t < hd) {
+      float* pp = part + ((int64_t)h * gridDim.x + split) * (hd + 2);
+      pp[2 + t] = sred[0][t] + sred[1][t];
+      if (t == 0) {
+        float lsum = 0.0f;
+        for (int jl = 0; jl < nk; jl++) lsum += expf(ssc[jl] - mx);
+        pp[0] = mx;
+        pp[1] = lsum;
+      }
+    }
+    (void)ls;
+  }
+  // ---- publish the partial; the last split of this head combines
+  __syncthreads();
+  if (t == 0) {
+    __threadfence();
+    const int prev = atomicAdd(&counters[h], 1);
+    s_last = prev == nsplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (t < hd) {
+    const float *p0 = part + (int64_t)h * gridDim.x * (hd + 2);
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < nsplit; s2++) M = fmaxf(M, __builtin_nontemporal_load(p0 + s2 * (hd + 2)));
+    float num = 0.0f, den = 0.0f;
+    for (int s2 = 0; s2 < nsplit; s2++) {
+      const float *pp = p0 + s2 * (hd + 2);
+      const float w = expf(__builtin_nontemporal_load(pp) - M);
+      num = fmaf(w, __builtin_nontemporal_load(pp + 2 + t), num);
+      den = fmaf(w, __builtin_nontemporal_load(pp + 1), den);
+    }
+    out[h * hd + t] = num / den;
+  }
+  if (t == 0) counters[h] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Op launchers
+// ---------------------------------------------------------------------------
+static int launch_rmsnorm(mmnb_ctx *ctx, const float *x, int64_t rows, int64_t dim,
+                          const float *g, float eps, float *y, const float *add, float *xsum) {
+  if (rows == 0) return MMNB_OK;
+  return launch(ctx, kKernDecOps, k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, x, dim, g, eps,
+                y, add, xsum);
+}
+
+static int launch_attn_rows(mmnb_ctx *ctx, const float *q, int64_t q_stride, int64_t batch,
+                            int64_t seq, int nh, int kvh, int hd, const float *pk,
+                            const float *pv, int64_t cap, int64_t P, float scale,
+                            const float *bias, int bias_heads, float *out, int64_t out_stride) {
+  const dim3 grid((unsigned)((seq + kAttnQ - 1) / kAttnQ), (unsigned)nh, (unsigned)batch);
+  return launch(ctx, kKernDecAttn, k_attn_rows, grid, dim3(256), 0, q, q_stride, seq, nh, kvh,
+                hd, pk, pv, cap, P, scale, bias, bias_heads, out, out_stride);
+}
+
+}  // namespace mmnb
+
+using namespace mmnb;
+
+// ---------------------------------------------------------------------------
+// C ABI: ops
+// ---------------------------------------------------------------------------
+int mmnb_rmsnorm_dev(mmnb_ctx *ctx, const float *d_x, int64_t rows, int64_t dim,
+                     const float *d_gamma, float eps, float *d_y) {
+  MMNB_GUARD_CTX(ctx);
+  if (rows < 0 || dim <= 0) return fail(MMNB_ERR_ARG, "RMSNorm: bad shape");
+  if (rows == 0) return MMNB_OK;
+  if (!d_x || !d_gamma || !d_y) return fail(MMNB_ERR_ARG, "RMSNorm: null buffer");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  return launch_rmsnorm(ctx, d_x, rows, dim, d_gamma, eps, d_y, nullptr, nullptr);
+}
+
+int mmnb_rotary_dev(mmnb_ctx *ctx, const float *d_x, int64_t batch, int64_t seq,
+                    int64_t hidden, int64_t num_heads, const int64_t *d_pos, int64_t pos_rank,
+                    const float *d_cos, const float *d_sin, int64_t half_rot, int interleaved,
+                    float *d_y) {
+  MMNB_GUARD_CTX(ctx);
+  if (batch < 0 || seq < 0 || hidden <= 0 || half_rot <= 0 || num_heads < 0)
+    return fail(MMNB_ERR_ARG, "RotaryEmbedding: bad shape");
+  const int64_t head = num_heads > 0 ? hidden / num_heads : 2 * half_rot;
+  if (head <= 0 || hidden % head != 0 || 2 * half_rot > head)
+    return fail(MMNB_ERR_ARG, "RotaryEmbedding: hidden, num_heads and rotary dim disagree");
+  if (pos_rank != 1 && pos_rank != 2) return fail(MMNB_ERR_ARG, "RotaryEmbedding: pos rank");
+  if (batch * seq == 0) return MMNB_OK;
+  if (!d_x || !d_pos || !d_cos || !d_sin || !d_y)
+    return fail(MMNB_ERR_ARG, "RotaryEmbedding: null buffer");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  return launch(ctx, kKernDecOps, k_rotary, dim3((unsigned)(batch * seq)), dim3(256), 0, d_x,
+                seq, (int)(hidden / head), (int)head, d_pos, (int)pos_rank, (int64_t)0, d_cos,
+                d_sin, (int)half_rot, interleaved, d_y);
+}
+
+int mmnb_gqa_dev(mmnb_ctx *ctx, const float *d_q, const float *d_k, const float *d_v,
+                 int64_t batch, int64_t seq, int64_t num_heads, int64_t kv_heads,
+                 int64_t head_size, float scale, const float *d_past_k, const float *d_past_v,
+                 int64_t past_len, const float *d_cos, const float *d_sin, int64_t half_rot,
+                 int do_rotary, int interleaved, const float *d_bias, int64_t bias_heads,
+                 float *d_out, float *d_present_k, float *d_present_v) {
+  MMNB_GUARD_CTX(ctx);
+  if (batch < 0 || seq < 0 || num_heads <= 0 || kv_heads <= 0 || head_size <= 0 ||
+      past_len < 0)
+    return fail(MMNB_ERR_ARG, "GroupQueryAttention: bad shape");
+  if (num_heads % kv_heads != 0)
+    return fail(MMNB_ERR_ARG, "GroupQueryAttention: num_heads % kv_num_heads != 0");
+  if (head_size > kAttnMaxHd)
+    return fail(MMNB_ERR_UNSUPPORTED, "GroupQueryAttention: head size above 128");
+  if (do_rotary && (!d_cos || !d_sin || 2 * half_rot > head_size || half_rot <= 0))
+    return fail(MMNB_ERR_ARG, "GroupQueryAttention: rotary caches");
+  if (d_bias && bias_heads <= 0) return fail(MMNB_ERR_ARG, "GroupQueryAttention: bias heads");
+  // The reference builds rotary positions as [1, seq] and indexes them by
+  // batch (onnx_ops.dart:1537-1541, :2150): batch > 1 with rotary throws.
+  if (do_rotary && batch > 1)
+    return fail(MMNB_ERR_ARG, "GroupQueryAttention: rotary with batch > 1 (position ids are [1, seq])");
+  if (batch * seq == 0) return MMNB_OK;
+  if (!d_q || !d_k || !d_v || !d_out || !d_present_k || !d_present_v ||
+      (past_len > 0 && (!d_past_k || !d_past_v)))
+    return fail(MMNB_ERR_ARG, "GroupQueryAttention: null buffer");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  const int nh = (int)num_heads, kvh = (int)kv_heads, hd = (int)head_size;
+  const int64_t T = past_len + seq;
+  const float *q = d_q, *k = d_k;
+  if (do_rotary) {
+    void *tmp = nullptr;
+    const size_t qn = (size_t)(batch * seq * nh * hd), kn = (size_t)(batch * seq * kvh * hd);
+    if ((rc = scratch_get(ctx, 4, (qn + kn) * 4, &tmp))) return rc;
+    float *qr = (float *)tmp, *kr = qr + qn;
+    if ((rc = launch(ctx, kKernDecOps, k_rotary, dim3((unsigned)(batch * seq)), dim3(256), 0,
+                     d_q, seq, nh, hd, (const int64_t *)nullptr, 1, past_len, d_cos, d_sin,
+                     (int)half_rot, interleaved, qr)))
+      return rc;
+    if ((rc = launch(ctx, kKernDecOps, k_rotary, dim3((unsigned)(batch * seq)), dim3(256), 0,
+                     d_k, seq, kvh, hd, (const int64_t *)nullptr, 1, past_len, d_cos, d_sin,
+                     (int)half_rot, interleaved, kr)))
+      return rc;
+    q = qr;
+    k = kr;
+  }
+  if ((rc = launch(ctx, kKernDecOps, k_gqa_present, dim3((unsigned)(kvh * T), (unsigned)batch),
+                   dim3(128), 0, d_past_k, d_past_v, past_len, k, d_v, seq, kvh, hd, T,
+                   d_present_k, d_present_v)))
+    return rc;
+  const float sc = scale > 0.0f ? scale : (float)(1.0 / std::sqrt((double)hd));
+  return launch_attn_rows(ctx, q, (int64_t)nh * hd, batch, seq, nh, kvh, hd, d_present_k,
+                          d_present_v, T, past_len, sc, d_bias, (int)bias_heads, d_out,
+                          (int64_t)nh * hd);
+}
+
+// ---------------------------------------------------------------------------
+// Decoder session
+// ---------------------------------------------------------------------------
+struct mmnb_decoder {
+  mmnb_ctx *ctx = nullptr;
+  mmnb_decoder_config cfg{};
+  struct Layer {
+    float *ln1 = nullptr, *ln2 = nullptr, *qn = nullptr, *kn = nullptr;
+    const mmnb_pack *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
+  };
+  std::vector<Layer> layers;
+  const mmnb_pack *lm = nullptr;
+  float *embed = nullptr, *final_norm = nullptr;
+  float *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
+        *gu = nullptr, *act = nullptr, *tmp = nullptr, *logits = nullptr;
+  float *cache_k = nullptr, *cache_v = nullptr, *cos = nullptr, *sin = nullptr;
+  float *part = nullptr;
+  int *counters = nullptr;
+  DecState *state = nullptr;
+  int32_t *out_tokens = nullptr;
+  int64_t *tok = nullptr;
+  int64_t pos = 0;        // host mirror of the sequence length
+  int64_t steps_done = 0; // host mirror of DecState::step
+  bool primed = false;    // a token is waiting in DecState::token
+  hipGraphExec_t graph = nullptr;
+  std::vector<void *> allocs;
+};
+
+static int dec_alloc(mmnb_decoder *d, size_t bytes, void **p) {
+  int rc = device_alloc(bytes, p);
+  if (rc) return rc;
+  d->allocs.push_back(*p);
+  return MMNB_OK;
+}
+
+static int dec_upload(mmnb_decoder *d, const float *host, size_t n, float **out) {
+  int rc = dec_alloc(d, n * 4, (void **)out);
+  if (rc) return rc;
+  MMNB_HIP(hipMemcpy(*out, host, n * 4, hipMemcpyHostToDevice));
+  return MMNB_OK;
+}
+
+int mmnb_decoder_free(mmnb_decoder *d) {
+  if (!d) return MMNB_OK;
+  if (d->ctx) (void)hipSetDevice(d->ctx->device);
+  if (d->ctx) (void)hipStreamSynchronize(d->ctx->stream);
+  if (d->graph) (void)hipGraphExecDestroy(d->graph);
+  for (void *p : d->allocs) (void)hipFree(p);
+  delete d;
+  return MMNB_OK;
+}
+
+int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const float *embed,
+                        const float *final_norm, const mmnb_pack *lm_head,
+                        mmnb_decoder **out) {
+  MMNB_GUARD_CTX(ctx);
+  if (!cfg || !embed || !final_norm || !lm_head || !out)
+    return fail(MMNB_ERR_ARG, "decoder: null argument");
+  const mmnb_decoder_config &c = *cfg;
+  if (c.layers <= 0 || c.hidden <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.head_dim <= 0 ||
+      c.intermediate <= 0 || c.vocab <= 0 || c.max_len <= 0 || c.heads % c.kv_heads != 0)
+    return fail(MMNB_ERR_ARG, "decoder: bad configuration");
+  if (c.head_dim > kAttnMaxHd || (c.head_dim % 16) || c.hidden % 64 || (c.heads * c.head_dim) % 64 ||
+      c.intermediate % 64 || c.hidden > 4096 || c.intermediate > 4096 ||
+      c.heads * c.head_dim > 4096)
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "decoder: needs head_dim <= 128 (a multiple of 16) and hidden, heads*head_dim, "
+                "intermediate multiples of 64 and <= 4096");
+  if (lm_head->kind != kPackNBits || lm_head->k != c.hidden || lm_head->n != c.vocab ||
+      lm_head->ctx != ctx)
+    return fail(MMNB_ERR_ARG, "decoder: lm_head pack shape");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  mmnb_decoder *d = new (std::nothrow) mmnb_decoder();
+  if (!d) return fail(MMNB_ERR_OOM, "decoder: out of host memory");
+  d->ctx = ctx;
+  d->cfg = c;
+  d->layers.resize((size_t)c.layers);
+  d->lm = lm_head;
+  const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim,
+                I = c.intermediate, Lmax = c.max_len;
+  const int64_t QKV = (nh + 2 * kvh) * hd;
+  const int64_t nsplit = (Lmax + kDecKeys - 1) / kDecKeys;
+  auto A = [&](size_t bytes, void **p) { return dec_alloc(d, bytes, p); };
+  if ((rc = dec_upload(d, embed, (size_t)(c.vocab * H), &d->embed)) ||
+      (rc = dec_upload(d, final_norm, (size_t)H, &d->final_norm)) ||
+      (rc = A((size_t)(Lmax * H) * 4, (void **)&d->x)) ||
+      (rc = A((size_t)(Lmax * H) * 4, (void **)&d->h)) ||
+      (rc = A((size_t)(Lmax * QKV) * 4, (void **)&d->qkv)) ||
+      (rc = A((size_t)(Lmax * nh * hd) * 4, (void **)&d->q)) ||
+      (rc = A((size_t)(Lmax * nh * hd) * 4, (void **)&d->attn)) ||
+      (rc = A((size_t)(Lmax * 2 * I) * 4, (void **)&d->gu)) ||
+      (rc = A((size_t)(Lmax * I) * 4, (void **)&d->act)) ||
+      (rc = A((size_t)(Lmax * H) * 4, (void **)&d->tmp)) ||
+      (rc = A((size_t)c.vocab * 4, (void **)&d->logits)) ||
+      (rc = A((size_t)(c.layers * kvh * Lmax * hd) * 4, (void **)&d->cache_k)) ||
+      (rc = A((size_t)(c.layers * kvh * Lmax * hd) * 4, (void **)&d->cache_v)) ||
+      (rc = A((size_t)(nh * nsplit * (hd + 2)) * 4, (void **)&d->part)) ||
+      (rc = A((size_t)nh * 4, (void **)&d->counters)) ||
+      (rc = A(sizeof(DecState), (void **)&d->state)) ||
+      (rc = A((size_t)Lmax * 4, (void **)&d->out_tokens)) ||
+      (rc = A((size_t)Lmax * 8, (void **)&d->tok))) {
+    mmnb_decoder_free(d);
+    return rc;
+  }
+  // rotary caches [Lmax, hd/2]: angle = pos * theta^(-2i/hd), in double
+  std::vector<float> cs((size_t)(Lmax * hd / 2)), sn((size_t)(Lmax * hd / 2));
+  for (int64_t p = 0; p < Lmax; p++)
+    for (int64_t i = 0; i < hd / 2; i++) {
+      const double inv = 1.0 / std::pow((double)c.rope_theta, (double)(2 * i) / (double)hd);
+      const double ang = (double)p * inv;
+      cs[(size_t)(p * hd / 2 + i)] = (float)std::cos(ang);
+      sn[(size_t)(p * hd / 2 + i)] = (float)std::sin(ang);
+    }
+  if ((rc = dec_upload(d, cs.data(), cs.size(), &d->cos)) ||
+      (rc = dec_upload(d, sn.data(), sn.size(), &d->sin))) {
+    mmnb_decoder_free(d);
+    return rc;
+  }
+  hipError_t e = hipMemset(d->counters, 0, (size_t)nh * 4);
+  if (e == hipSuccess) e = hipMemset(d->state, 0, sizeof(DecState));
+  if (e != hipSuccess) {
+    mmnb_decoder_free(d);
+    return check_hip(e, "hipMemset");
+  }
+  *out = d;
+  return MMNB_OK;
+}
+
+int mmnb_decoder_set_layer(mmnb_decoder *d, int64_t layer, const float *ln1, const float *ln2,
+                           const float *q_norm, const float *k_norm, const mmnb_pack *qkv,
+                           const mmnb_pack *o, const mmnb_pack *gate_up,
+                           const mmnb_pack *down) {
+  if (!d) return fail(MMNB_ERR_ARG, "decoder: null handle");
+  const mmnb_decoder_config &c = d->cfg;
+  if (layer < 0 || layer >= c.layers) return fail(MMNB_ERR_ARG, "decoder: layer index");
+  if (!ln1 || !ln2 || !q_norm || !k_norm || !qkv || !o || !gate_up || !down)
+    return fail(MMNB_ERR_ARG, "decoder: null argument");
+  const int64_t H = c.hidden, hd = c.head_dim, nh = c.heads, kvh = c.kv_heads,
+                I = c.intermediate;
+  auto ok = [&](const mmnb_pack *p, int64_t k, int64_t n) {
+    return p->kind == kPackNBits && p->ctx == d->ctx && p->k == k && p->n == n;
+  };
+  if (!ok(qkv, H, (nh + 2 * kvh) * hd) || !ok(o, nh * hd, H) || !ok(gate_up, H, 2 * I) ||
+      !ok(down, I, H))
+    return fail(MMNB_ERR_ARG, "decoder: layer pack shapes do not match the configuration");
+  CtxLock lk(d->ctx);
+  int rc = set_device(d->ctx);
+  if (rc) return rc;
+  mmnb_decoder::Layer &L = d->layers[(size_t)layer];
+  if (L.ln1) return fail(MMNB_ERR_ARG, "decoder: layer already set");
+  if ((rc = dec_upload(d, ln1, (size_t)H, &L.ln1)) || (rc = dec_upload(d, ln2, (size_t)H, &L.ln2)) ||
+      (rc = dec_upload(d, q_norm, (size_t)hd, &L.qn)) ||
+      (rc = dec_upload(d, k_norm, (size_t)hd, &L.kn)))
+    return rc;
+  L.qkv = qkv;
+  L.o = o;
+  L.gu = gate_up;
+  L.down = down;
+  return MMNB_OK;
+}
+
+static int dec_check_ready(mmnb_decoder *d) {
+  for (auto &L : d->layers)
+    if (!L.ln1) return fail(MMNB_ERR_ARG, "decoder: a layer is not set");
+  return MMNB_OK;
+}
+
+int mmnb_decoder_reset(mmnb_decoder *d) {
+  if (!d) return fail(MMNB_ERR_ARG, "decoder: null handle");
+  CtxLock lk(d->ctx);
+  int rc = set_device(d->ctx);
+  if (rc) return rc;
+  MMNB_HIP(hipStreamSynchronize(d->ctx->stream));
+  MMNB_HIP(hipMemset(d->state, 0, sizeof(DecState)));
+  d->pos = 0;
+  d->steps_done = 0;
+  d->primed = false;
+  return MMNB_OK;
+}
+
+// Prompt rows through every layer (the general kernels), then the greedy
+// token of the last row.  The KV cache grows by n.
+int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
+                         int32_t *next_token) {
+  if (!d) return fail(MMNB_ERR_ARG, "decoder: null handle");
+  mmnb_ctx *ctx = d->ctx;
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "decoder: prefill during graph capture");
+  const mmnb_decoder_config &c = d->cfg;
+  if (n <= 0 || !tokens) return fail(MMNB_ERR_ARG, "decoder: empty prompt");
+  if (d->pos + n > c.max_len) return fail(MMNB_ERR_ARG, "decoder: prompt exceeds max_len");
+  for (int64_t i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= c.vocab) return fail(MMNB_ERR_ARG, "decoder: token id");
+  int rc = dec_check_ready(d);
+  if (rc) return rc;
+  CtxLock lk(ctx);
+  if ((rc = set_device(ctx))) return rc;
+  hipStream_t s = ctx->stream;
+  const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim,
+                I = c.intermediate, Lmax = c.max_len;
+  const int64_t QKV = (nh + 2 * kvh) * hd;
+  const int64_t P = d->pos;
+  const float eps = c.eps;
+  const float scale = (float)(1.0 / std::sqrt((double)hd));
+  MMNB_HIP(hipMemcpyAsync(d->tok, tokens, (size_t)n * 8, hipMemcpyHostToDevice, s));
+  if ((rc = launch(ctx, kKernDecOps, k_embed_rows, dim3((unsigned)n), dim3(256), 0,
+                   (const int64_t *)d->tok, (const float *)d->embed, H, d->x)))
+    return rc;
+  for (int64_t li = 0; li < c.layers; li++) {
+    const mmnb_decoder::Layer &L = d->layers[(size_t)li];
+    float *ck = d->cache_k + li * kvh * Lmax * hd, *cv = d->cache_v + li * kvh * Lmax * hd;
+    if ((rc = launch_rmsnorm(ctx, d->x, n, H, L.ln1, eps, d->h, nullptr, nullptr))) return rc;
+    if ((rc = launch_matmul_nbits(ctx, L.qkv, d->h, H, n, d->qkv))) return rc;
+    if ((rc = launch(ctx, kKernDecOps, k_qk_prep_rows, dim3((unsigned)n, (unsigned)(nh + kvh)),
+                     dim3((unsigned)hd), 0, (const float *)d->qkv, QKV, (int)nh, (int)kvh,
+                     (int)hd, (const float *)L.qn, (const float *)L.kn, eps,
+                     (const float *)d->cos, (const float *)d->sin, P, d->q, ck, cv, Lmax)))
+      return rc;
+    if ((rc = launch_attn_rows(ctx, d->q, nh * hd, 1, n, (int)nh, (int)kvh, (int)hd, ck, cv,
+                               Lmax, P, scale, nullptr, 1, d->attn, nh * hd)))
+      return rc;
+    if ((rc = launch_matmul_nbits(ctx, L.o, d->attn, nh * hd, n, d->tmp))) return rc;
+    // x += o; h = rmsnorm(x)
+    if ((rc = launch_rmsnorm(ctx, d->x, n, H, L.ln2, eps, d->h, d->tmp, d->x))) return rc;
+    if ((rc = launch_matmul_nbits(ctx, L.gu, d->h, H, n, d->gu))) return rc;
+    if ((rc = launch(ctx, kKernDecOps, k_swiglu_rows,
+                     dim3((unsigned)((I + 255) / 256), (unsigned)n), dim3(256), 0,
+                     (const float *)d->gu, I, d->act)))
+      return rc;
+    if ((rc = launch_matmul_nbits(ctx, L.down, d->act, I, n, d->tmp))) return rc;
+    // x += down (the next norm reads x)
+    if ((rc = launch(ctx, kKernDecOps, k_rmsnorm, dim3((unsigned)n), dim3(256), 0,
+                     (const float *)d->x, H, (const float *)d->final_norm, eps, d->h,
+                     (const float *)d->tmp, d->x)))
+      return rc;
+  }
+  // greedy token of the last row: final norm fused into lm_head
+  MMNB_HIP(hipMemsetAsync(&d->state->argmax, 0, 8, s));
+  if ((rc = launch_dec_gemv(ctx, d->lm, d->x + (n - 1) * H, d->final_norm, eps, kDecArgmax,
+                            nullptr, d->logits, &d->state->argmax)))
+    return rc;
+  // state: token = argmax, pos = P + n (k_dec_end advances pos by one and
+  // records the token; set pos so that it lands on P + n)
+  DecState hs{};
+  hs.pos = (int)(P + n - 1);
+  hs.step = 0;
+  MMNB_HIP(hipMemcpyAsync(d->state, &hs, 8 + 4 + 4, hipMemcpyHostToDevice, s));
+  // the argmax field (offset 16) is kept; k_dec_end turns it into the token
+  if ((rc = launch(ctx, kKernDecOps, k_dec_end, dim3(1), dim3(64), 0, d->state, d->out_tokens,
+                   (int)c.max_len)))
+    return rc;
+  int32_t tok = 0;
+  MMNB_HIP(hipMemcpyAsync(&tok, &d->state->token, 4, hipMemcpyDeviceToHost, s));
+  MMNB_HIP(hipMemsetAsync(&d->state->step, 0, 4, s));
+  MMNB_HIP(hipStreamSynchronize(s));
+  d->pos = P + n;
+  d->steps_done = 0;
+  d->primed = true;
+  if (next_token) *next_token = tok;
+  return MMNB_OK;
+}
+
+static int dec_record_step(mmnb_decoder *d) {
+  mmnb_ctx *ctx = d->ctx;
+  const mmnb_decoder_config &c = d->cfg;
+  const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim, Lmax = c.max_len;
+  const float eps = c.eps;
+  const float scale = (float)(1.0 / std::sqrt((double)hd));
+  const int64_t nsplit = (Lmax + kDecKeys - 1) / kDecKeys;
+  int rc;
+  if ((rc = launch(ctx, kKernDecOps, k_dec_begin, dim3(1), dim3(256), 0, d->state,
+                   (const float *)d->embed, H, c.vocab, d->x)))
+    return rc;
+  for (int64_t li = 0; li < c.layers; li++) {
+    const mmnb_decoder::Layer &L = d->layers[(size_t)li];
+    float *ck = d->cache_k + li * kvh * Lmax * hd, *cv = d->cache_v + li * kvh * Lmax * hd;
+    if ((rc = launch_dec_gemv(ctx, L.qkv, d->x, L.ln1, eps, kDecPlain, nullptr, d->qkv, nullptr)))
+      return rc;
+    if ((rc = launch(ctx, kKernDecAttn, k_dec_attn, dim3((unsigned)nsplit, (unsigned)nh),
+                     dim3(256), 0, (const DecState *)d->state, (const float *)d->qkv, (int)nh,
+                     (int)kvh, (int)hd, (const float *)L.qn, (const float *)L.kn, eps,
+                     (const float *)d->cos, (const float *)d->sin, ck, cv, Lmax, scale, d->part,
+                     d->counters, d->attn)))
+      return rc;
+    if ((rc = launch_dec_gemv(ctx, L.o, d->attn, nullptr, eps, kDecResidual, d->x, d->x, nullptr)))
+      return rc;
+    if ((rc = launch_dec_gemv(ctx, L.gu, d->x, L.ln2, eps, kDecSwiglu, nullptr, d->act, nullptr)))
+      return rc;
+    if ((rc = launch_dec_gemv(ctx, L.down, d->act, nullptr, eps, kDecResidual, d->x, d->x,
+                              nullptr)))
+      return rc;
+  }
+  if ((rc = launch_dec_gemv(ctx, d->lm, d->x, d->final_norm, eps, kDecArgmax, nullptr, d->logits,
+                            &d->state->argmax)))
+    return rc;
+  return launch(ctx, kKernDecOps, k_dec_end, dim3(1), dim3(64), 0, d->state, d->out_tokens,
+                (int)c.max_len);
+}
+
+// `steps` greedy decode steps (graph replays); tokens[i] is the token
+// generated by step i.
+int mmnb_decoder_decode(mmnb_decoder *d, int64_t steps, int32_t *tokens) {
+  if (!d) return fail(MMNB_ERR_ARG, "decoder: null handle");
+  mmnb_ctx *ctx = d->ctx;
+  if (ctx->capturing) return fail(MMNB_ERR_ARG, "decoder: decode during graph capture");
+  if (steps < 0) return fail(MMNB_ERR_ARG, "decoder: negative step count");
+  if (steps == 0) return MMNB_OK;
+  if (!d->primed) return fail(MMNB_ERR_ARG, "decoder: prefill first");
+  if (d->pos + steps > d->cfg.max_len)
+    return fail(MMNB_ERR_ARG, "decoder: steps would exceed max_len");
+  if (d->steps_done + steps > d->cfg.max_len)
+    return fail(MMNB_ERR_ARG, "decoder: output list full");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  hipStream_t s = ctx->stream;
+  if (!d->graph) {
+    MMNB_HIP(hipStreamSynchronize(s));
+    MMNB_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    rc = dec_record_step(d);
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return check_hip(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&d->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      d->graph = nullptr;
+      return check_hip(e, "hipGraphInstantiate");
+    }
+  }
+  const int64_t first = d->steps_done;
+  for (int64_t i = 0; i < steps; i++) MMNB_HIP(hipGraphLaunch(d->graph, s));
+  if (tokens)
+    MMNB_HIP(hipMemcpyAsync(tokens, d->out_tokens + first, (size_t)steps * 4,
+                            hipMemcpyDeviceToHost, s));
+  MMNB_HIP(hipStreamSynchronize(s));
+  d->pos += steps;
+  d->steps_done += steps;
+  return MMNB_OK;
+}
+
+int mmnb_decoder_logits(mmnb_decoder *d, float *logits) {
+  if (!d || !logits) return fail(MMNB_ERR_ARG, "decoder: null argument");
+  CtxLock lk(d->ctx);
+  int rc = set_device(d->ctx);
+  if (rc) return rc;
+  MMNB_HIP(hipMemcpyAsync(logits, d->logits, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost,
+                          d->ctx->stream));
+  MMNB_HIP(hipStreamSynchronize(d->ctx->stream));
+  return MMNB_OK;
+}
+
+int mmnb_decoder_position(mmnb_decoder *d, int64_t *pos) {
+  if (!d || !pos) return fail(MMNB_ERR_ARG, "decoder: null argument");
+  *pos = d->pos;
+  return MMNB_OK;
+}

@@ -125,7 +125,10 @@ enum KernelId {
   kKernPrepIntB = 7,
   kKernProbeEmpty = 8,
   kKernProbeRead = 9,
-  kKernCount = 10
+  kKernDecGemv = 10,
+  kKernDecAttn = 11,
+  kKernDecOps = 12,
+  kKernCount = 13
 };
 
 // Launch `kern` on the context stream; in timing mode the dispatch records
@@ -148,6 +151,38 @@ int launch(mmnb_ctx *ctx, int kid, void (*kern)(KArgs...), dim3 grid, dim3 block
 
 // Grow-only device scratch owned by the context.
 int scratch_get(mmnb_ctx *ctx, int slot, size_t bytes, void **out);
+
+// hipMalloc with kTailPad bytes of slack.
+int device_alloc(size_t bytes, void **p);
+
+// Serialises calls on one context.
+struct CtxLock {
+  explicit CtxLock(mmnb_ctx *c) : ctx(c) { ctx->mu.lock(); }
+  ~CtxLock() { ctx->mu.unlock(); }
+  mmnb_ctx *ctx;
+};
+
+inline int set_device(mmnb_ctx *ctx) {
+  MMNB_HIP(hipSetDevice(ctx->device));
+  return MMNB_OK;
+}
+
+#define MMNB_GUARD_CTX(ctx)                                          \
+  do {                                                               \
+    if (!(ctx)) return ::mmnb::fail(MMNB_ERR_ARG, "null context");  \
+  } while (0)
+
+// Fused M = 1 MatMulNBits for the decoder step (a pack without zero points,
+// block >= 64):  y = W * a with optional RMSNorm prologue and epilogue.
+//   norm_gamma != null: a = x * rsqrt(mean(x^2) + eps) * gamma (x = d_x)
+//   epi kDecPlain:  y[n] = v;   kDecResidual: y[n] = resid[n] + v;
+//   kDecSwiglu:  columns are gate/up interleaved, y[j] = silu(v[2j]) * v[2j+1];
+//   kDecArgmax:  y[n] = v and the greatest (value, lowest index) is folded
+//                into *d_argmax with a 64-bit atomic max.
+enum DecEpilogue { kDecPlain = 0, kDecResidual = 1, kDecSwiglu = 2, kDecArgmax = 3 };
+int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
+                    const float *norm_gamma, float eps, int epi, const float *resid,
+                    float *d_y, unsigned long long *d_argmax);
 
 // Kernel launchers (return MMNB_OK or an error code) -------------------------
 // MatMulNBits: y[m, n] = a[m, k] * W;  lda = row stride of a (elements).

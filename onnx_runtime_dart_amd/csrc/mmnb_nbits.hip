@@ -14,6 +14,12 @@
 
 namespace mmnb {
 
+static int ilog2(int64_t v) {
+  int r = 0;
+  while ((int64_t(1) << (r + 1)) <= v) r++;
+  return r;
+}
+
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
@@ -345,6 +351,201 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
 }
 
 // ---------------------------------------------------------------------------
+// Decoder-step MatMulNBits (M = 1, no zero points, block >= 64) with the
+// neighbouring graph nodes folded in, so one decoder layer needs five
+// launches instead of a dozen:
+//   NORM   RMSNorm prologue (SimplifiedLayerNormalization before q/k/v,
+//          gate/up and lm_head): every workgroup sums x^2 over its chunks
+//          (the 32 lanes of half 0 of each wave cover K once), then scales
+//          its activations by rsqrt(mean + eps) * gamma;
+//   EPI    kDecResidual (the residual Add after o and down),
+//          kDecSwiglu (gate/up columns interleaved 2j/2j+1 in the pack, so a
+//          workgroup holds both halves of its outputs: silu(g) * u),
+//          kDecArgmax (lm_head: greedy token by a 64-bit atomic max of
+//          (orderable value, ~index), ties to the lowest index).
+// Lane layout and arithmetic follow k_gemv_valu with M = 1 and one
+// quantisation block per chunk; K is at most 4096 (one chunk per lane).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned long long argmax_key(float v, int col) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)col);
+}
+
+template <int R, bool NORM, int EPI>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
+    const float *__restrict__ X, const float *__restrict__ gamma, float eps,
+    const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S, int nb,
+    int bs_log2, int K, int N, const float *resid, float *Y,
+    unsigned long long *__restrict__ argmax, int C) {
+  __shared__ float red[kGemvMaxWaves][2 * R];
+  __shared__ float nrm[kGemvMaxWaves];
+  __shared__ float outv[2 * R];
+  const int nw = blockDim.x >> 6;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int h = l >> 5, t = l & 31;
+  const int col0 = blockIdx.x * (2 * R);
+  int colr[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int c = col0 + 2 * r + h;
+    colr[r] = c < N ? c : N - 1;
+  }
+  const int c = 32 * w + t;
+  const bool cv = c < C;
+  const int cc = cv ? c : 0;
+  const int s = cc >> 1, g = cc & 1;
+  // ---- loads: activations (and gamma), scales, then weights
+  float av[32], gv[32];
+  {
+    const float *xr = X + s * kSegK + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float4 x0 = *(const float4 *)(xr + 16 * j);
+      const float4 x1 = *(const float4 *)(xr + 16 * j + 4);
+      av[8 * j + 0] = x0.x; av[8 * j + 1] = x0.y; av[8 * j + 2] = x0.z; av[8 * j + 3] = x0.w;
+      av[8 * j + 4] = x1.x; av[8 * j + 5] = x1.y; av[8 * j + 6] = x1.z; av[8 * j + 7] = x1.w;
+    }
+    if constexpr (NORM) {
+      const float *gr = gamma + s * kSegK + 8 * g;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 x0 = *(const float4 *)(gr + 16 * j);
+        const float4 x1 = *(const float4 *)(gr + 16 * j + 4);
+        gv[8 * j + 0] = x0.x; gv[8 * j + 1] = x0.y; gv[8 * j + 2] = x0.z; gv[8 * j + 3] = x0.w;
+        gv[8 * j + 4] = x1.x; gv[8 * j + 5] = x1.y; gv[8 * j + 6] = x1.z; gv[8 * j + 7] = x1.w;
+      }
+    }
+  }
+  const int blk = (s * kSegK) >> bs_log2;
+  float sraw[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) sraw[r] = S[colr[r] * nb + blk];
+  uint4 wv[R];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+  if constexpr (NORM) {
+    float ss = 0.0f;
+    if (h == 0 && cv) {
+#pragma unroll
+      for (int e = 0; e < 32; e++) ss = fmaf(av[e], av[e], ss);
+    }
+    ss = half_wave_sum(ss);
+    if (l == 0) nrm[w] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int ww = 0; ww < nw; ww++) tot += nrm[ww];
+    const float inv = (float)(1.0 / sqrt((double)tot / (double)K + (double)eps));
+#pragma unroll
+    for (int e = 0; e < 32; e++) av[e] = av[e] * inv * gv[e];
+  }
+  // ---- arithmetic (zero point 8: acc += sc * sum(a q) - 8 sc * sum(a))
+  float sa = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; e++) sa += av[e];
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint32_t wd[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+    float d = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
+      float qv[8];
+      qv[0] = (float)(lo & 0xFF);
+      qv[1] = (float)(hi & 0xFF);
+      qv[2] = (float)((lo >> 8) & 0xFF);
+      qv[3] = (float)((hi >> 8) & 0xFF);
+      qv[4] = (float)((lo >> 16) & 0xFF);
+      qv[5] = (float)((hi >> 16) & 0xFF);
+      qv[6] = (float)(lo >> 24);
+      qv[7] = (float)(hi >> 24);
+#pragma unroll
+      for (int e = 0; e < 8; e++) d = fmaf(av[8 * j + e], qv[e], d);
+    }
+    const float sc = cv ? sraw[r] : 0.0f;
+    acc[r] = fmaf(sc, d, 0.0f);
+    acc[r] = fmaf(-8.0f * sc, sa, acc[r]);
+  }
+  // ---- reductions: 32 lanes of a half-wave, then the waves
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const float v = half_wave_sum(acc[r]);
+    if (t == 0) red[w][2 * r + h] = v;
+  }
+  __syncthreads();
+  float v = 0.0f;
+  const int i = threadIdx.x;
+  if (i < 2 * R) {
+    for (int ww = 0; ww < nw; ww++) v += red[ww][i];
+  }
+  const int col = col0 + i;
+  if constexpr (EPI == kDecPlain) {
+    if (i < 2 * R && col < N) Y[col] = v;
+  } else if constexpr (EPI == kDecResidual) {
+    if (i < 2 * R && col < N) Y[col] = resid[col] + v;
+  } else if constexpr (EPI == kDecSwiglu) {
+    if (i < 2 * R) outv[i] = v;
+    __syncthreads();
+    if (i < R && col0 + 2 * i + 1 < N) {
+      const float gg = outv[2 * i], uu = outv[2 * i + 1];
+      const float sig = 1.0f / (1.0f + expf(-gg));
+      Y[col0 / 2 + i] = (gg * sig) * uu;
+    }
+  } else {  // kDecArgmax
+    __shared__ unsigned long long keys[2 * R];
+    if (i < 2 * R) {
+      if (col < N) Y[col] = v;
+      keys[i] = col < N ? argmax_key(v, col) : 0ull;
+    }
+    __syncthreads();
+    if (i == 0) {
+      unsigned long long best = keys[0];
+      for (int q = 1; q < 2 * R; q++) best = keys[q] > best ? keys[q] : best;
+      atomicMax(argmax, best);
+    }
+  }
+}
+
+int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
+                    const float *norm_gamma, float eps, int epi, const float *resid,
+                    float *d_y, unsigned long long *d_argmax) {
+  if (p->has_zp || p->block < 64)
+    return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV: needs block >= 64 and no zero points");
+  if (p->k % kSegK != 0 || p->k > 4096)
+    return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV: K must be a multiple of 64, <= 4096");
+  const int C = (int)(p->col_bytes / 16);
+  const int nw = (C + 31) / 32;
+  const int64_t n = p->n;
+  int R = 8;
+  while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
+  const dim3 block((unsigned)(64 * nw));
+  const int bs_log2 = ilog2(p->block);
+  const bool norm = norm_gamma != nullptr;
+#define MMNB_DEC(RR, NN, EE)                                                                   \
+  return launch(ctx, kKernDecGemv, k_dec_gemv<RR, NN, EE>, grid, block, 0, d_x, norm_gamma, eps, \
+                p->d_w, p->col_bytes, p->d_scales, (int)p->n_blocks, bs_log2, (int)p->k,     \
+                (int)n, resid, d_y, d_argmax, C)
+#define MMNB_DEC_R(NN, EE)              \
+  {                                     \
+    if (R == 8) MMNB_DEC(8, NN, EE);    \
+    if (R == 4) MMNB_DEC(4, NN, EE);    \
+    if (R == 2) MMNB_DEC(2, NN, EE);    \
+    MMNB_DEC(1, NN, EE);                \
+  }
+  if (epi == kDecResidual && !norm) MMNB_DEC_R(false, kDecResidual);
+  if (epi == kDecSwiglu && norm) MMNB_DEC_R(true, kDecSwiglu);
+  if (epi == kDecArgmax && norm) MMNB_DEC_R(true, kDecArgmax);
+  if (epi == kDecPlain && norm) MMNB_DEC_R(true, kDecPlain);
+  if (epi == kDecPlain && !norm) MMNB_DEC_R(false, kDecPlain);
+#undef MMNB_DEC_R
+#undef MMNB_DEC
+  return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV: unsupported prologue/epilogue pair");
+}
+
+// ---------------------------------------------------------------------------
 // Decode-shape GEMV for 2 <= M <= 8, activations staged in LDS.
 //
 // Holding a chunk's 32 activations per row in registers (the M = 1 kernel)
@@ -602,11 +803,6 @@ static int launch_gemv_lds_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 blo
                                   groups, vec, bs_log2);
 }
 
-static int ilog2(int64_t v) {
-  int r = 0;
-  while ((int64_t(1) << (r + 1)) <= v) r++;
-  return r;
-}
 
 static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y);

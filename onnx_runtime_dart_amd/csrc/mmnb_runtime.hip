@@ -55,21 +55,10 @@ int scratch_get(mmnb_ctx *ctx, int slot, size_t bytes, void **out) {
   return MMNB_OK;
 }
 
-static int device_alloc(size_t bytes, void **p) {
+int device_alloc(size_t bytes, void **p) {
   size_t cap = bytes + kTailPad;
   hipError_t e = hipMalloc(p, cap);
   if (e != hipSuccess) return check_hip(e, "hipMalloc");
-  return MMNB_OK;
-}
-
-struct CtxLock {
-  explicit CtxLock(mmnb_ctx *c) : ctx(c) { ctx->mu.lock(); }
-  ~CtxLock() { ctx->mu.unlock(); }
-  mmnb_ctx *ctx;
-};
-
-static int set_device(mmnb_ctx *ctx) {
-  MMNB_HIP(hipSetDevice(ctx->device));
   return MMNB_OK;
 }
 
@@ -77,10 +66,6 @@ static int set_device(mmnb_ctx *ctx) {
 
 using namespace mmnb;
 
-#define MMNB_GUARD_CTX(ctx)                                          \
-  do {                                                               \
-    if (!(ctx)) return fail(MMNB_ERR_ARG, "null context");          \
-  } while (0)
 
 extern "C" {
 
@@ -666,7 +651,7 @@ int mmnb_event_elapsed_ms(mmnb_ctx *ctx, int slot_start, int slot_end, float *ms
 static const char *kKernelNames[kKernCount] = {
     "k_gemv_valu", "k_prep_a", "k_gemm_mfma", "k_dql_minmax",
     "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b", "k_probe_empty",
-    "k_probe_read"};
+    "k_probe_read", "k_dec_gemv", "k_dec_attn", "k_dec_ops"};
 
 const char *mmnb_kernel_name(int kernel_id) {
   if (kernel_id < 0 || kernel_id >= kKernCount) return nullptr;

@@ -4,7 +4,9 @@
 Reads ``test/fixtures/<case>/{model.onnx,case.json}`` from the reference
 source tree (default ``/root/reference``) for the eight fixtures that pin the
 int4 ``MatMulNBits`` and int8 ``DynamicQuantizeLinear``/``MatMulInteger``
-path, decodes the initializers and node attributes out of ``model.onnx`` with
+path, and the six that pin the decoder ops around it (RMSNorm chain,
+``RotaryEmbedding``, ``GroupQueryAttention`` with and without KV cache,
+rotary and bias), decodes the initializers and node attributes out of ``model.onnx`` with
 a minimal protobuf wire-format reader (no ``onnx`` package needed), and writes
 ``tests/golden/<case>.json``.  The fixtures are data: the inputs the
 reference's ORT-oracle fixture test feeds (``test/fixture_parity_test.dart``)
@@ -29,6 +31,13 @@ CASES = [
     "matmulinteger_nozp",
     "matmulinteger_batched",
     "matmulinteger_percol_bzp",
+    # decoder ops (RMSNorm 7-node chain, rotary, grouped-query attention)
+    "rmsnorm_pattern",
+    "rotary_embedding",
+    "gqa_causal",
+    "gqa_kvcache",
+    "gqa_kvcache_rotary",
+    "gqa_kvcache_bias",
 ]
 
 # ONNX TensorProto.DataType codes used by these fixtures.
@@ -178,7 +187,6 @@ def main():
         d = src / case
         nodes, inits = decode_model((d / "model.onnx").read_bytes())
         cj = json.loads((d / "case.json").read_text())
-        assert len(nodes) == 1, case
         out = {
             "provenance": f"onnx_runtime_dart test/fixtures/{case} "
                           "(ORT CPU outputs, tool/gen_fixtures.py seed 42)",
@@ -190,6 +198,8 @@ def main():
             "inputs": cj["inputs"],
             "expected": cj["expected"],
         }
+        if len(nodes) > 1:  # a multi-node pattern (the RMSNorm chain)
+            out["nodes"] = nodes
         (dst / f"{case}.json").write_text(json.dumps(out, indent=None) + "\n")
         print(case, nodes[0]["op_type"], nodes[0]["attrs"],
               {k: v["shape"] for k, v in inits.items()})
