@@ -20,6 +20,8 @@ Also reported (extra keys on the same line):
   int8          DynamicQuantizeLinear [512,1024] -> MatMulInteger
                 [1024,3072] -> fp32 rescale
   decode_sweep  M in {1,4,8} x the four decode projections, block 128
+  decoder       end-to-end Qwen3-0.6B-shaped int4 decoder: 256-token prefill
+                and 64 greedy decode steps, tokens/s
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -204,6 +206,49 @@ def bench_int8(ctx, lib, ops, synth, steps, warmup):
         bf.free()
     pack.free()
     return res
+
+
+def bench_decoder(ctx, lib, runs=3):
+    """The end-to-end synthetic decoder (Qwen3-0.6B shape: 28 layers, hidden
+    1024, 16/8 heads of 128, SwiGLU 3072, vocab 151936, random int4 weights,
+    block 128): 256-token prefill, then 64 greedy decode steps, every
+    MatMulNBits on the GPU.  Best of `runs` (the first untimed run also
+    records the decode-step graph)."""
+    from onnx_runtime_dart_amd import decoder as G
+
+    cfg = G.QWEN3_0_6B
+    w = G.random_weights(cfg, seed=0)
+    dec = G.GpuDecoder(w, ctx)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, 256)
+    steps = 64
+    try:
+        dec.prefill(prompt)
+        dec.decode(steps)
+        best = None
+        for _ in range(runs):
+            dec.reset()
+            ctx.synchronize()
+            t0 = time.perf_counter()
+            dec.prefill(prompt)
+            t1 = time.perf_counter()
+            dec.decode(steps)
+            t2 = time.perf_counter()
+            r = (t1 - t0, t2 - t1)
+            if best is None or sum(r) < sum(best):
+                best = r
+    finally:
+        dec.free()
+    pf, dc = best
+    per_tok = cfg.weight_bytes_per_token()
+    return {"config": "Qwen3-0.6B shape, 28 layers, int4 block 128, random weights",
+            "prefill_tokens": 256, "decode_steps": steps,
+            "prefill_ms": pf * 1e3, "decode_ms": dc * 1e3,
+            "prefill_tok_s": 256 / pf, "decode_tok_s": steps / dc,
+            "e2e_tok_s": (256 + steps) / (pf + dc),
+            "decode_ms_per_token": dc * 1e3 / steps,
+            "weight_bytes_per_token": per_tok,
+            "decode_weight_gbs": per_tok * steps / dc / 1e9,
+            "launches_per_token": 5 * cfg.layers + 3}
 
 
 def bench_platform(ctx, lib):
@@ -425,6 +470,9 @@ def main():
                                                        "kernel_ms", "bytes_per_call")})
             out["decode_sweep"] = sweep
             print("# decode sweep done", file=sys.stderr, flush=True)
+            out["decoder"] = bench_decoder(ctx, lib)
+            print(f"# decoder: decode {out['decoder']['decode_tok_s']:.0f} tok/s, prefill "
+                  f"{out['decoder']['prefill_tok_s']:.0f} tok/s", file=sys.stderr, flush=True)
             out["platform"] = bench_platform(ctx, lib)
             print(f"# platform: {out['platform']}", file=sys.stderr, flush=True)
         except Exception as e:  # extras must not hide the headline

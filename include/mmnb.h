@@ -262,6 +262,9 @@ int mmnb_decoder_decode(mmnb_decoder *dec, int64_t steps, int32_t *tokens);
 int mmnb_decoder_logits(mmnb_decoder *dec, float *logits);
 /* Tokens held in the KV cache. */
 int mmnb_decoder_position(mmnb_decoder *dec, int64_t *pos);
+/* Decode steps replay the recorded HIP graph (use_graph != 0, the default)
+ * or launch the step's kernels one by one (for per-kernel timing). */
+int mmnb_decoder_set_graph(mmnb_decoder *dec, int use_graph);
 /* Empty the KV cache (weights stay). */
 int mmnb_decoder_reset(mmnb_decoder *dec);
 int mmnb_decoder_free(mmnb_decoder *dec);

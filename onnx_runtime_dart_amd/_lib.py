@@ -76,6 +76,7 @@ SIGNATURES = {
     "mmnb_decoder_logits": (_int, [_vp, _vp]),
     "mmnb_decoder_position": (_int, [_vp, _P(_i64)]),
     "mmnb_decoder_reset": (_int, [_vp]),
+    "mmnb_decoder_set_graph": (_int, [_vp, _int]),
     "mmnb_decoder_free": (_int, [_vp]),
 }
 

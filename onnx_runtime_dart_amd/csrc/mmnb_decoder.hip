@@ -184,11 +184,29 @@ __global__ __launch_bounds__(256) void k_attn_rows(
   for (int e = 0; e < kAttnMaxHd / 16; e++) o[e] = 0.0f;
   for (int64_t k0 = 0; k0 < kend; k0 += kAttnKT) {
     __syncthreads();
-    for (int e = threadIdx.x; e < kAttnKT * hd; e += blockDim.x) {
-      const int j = e / hd, d = e % hd;
-      const bool ok = k0 + j < T;
-      sK[j][d] = ok ? Kb[(k0 + j) * hd + d] : 0.0f;
-      sV[j][d] = ok ? Vb[(k0 + j) * hd + d] : 0.0f;
+    {
+      // all of this thread's tile elements in flight before any store
+      constexpr int kPer = kAttnKT * kAttnMaxHd / 256;
+      float kk[kPer], vv[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; u++) {
+        const int e = threadIdx.x + 256 * u;
+        const int j = e / hd, d = e % hd;
+        const bool ok = e < kAttnKT * hd && k0 + j < T;
+        const int64_t idx = ok ? (k0 + j) * hd + d : 0;  // unconditional load
+        const float k_ = Kb[idx], v_ = Vb[idx];
+        kk[u] = ok ? k_ : 0.0f;
+        vv[u] = ok ? v_ : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; u++) {
+        const int e = threadIdx.x + 256 * u;
+        if (e < kAttnKT * hd) {
+          const int j = e / hd, d = e % hd;
+          sK[j][d] = kk[u];
+          sV[j][d] = vv[u];
+        }
+      }
     }
     __syncthreads();
     float sc[2];
@@ -317,7 +335,7 @@ struct DecState {
   int token;  // token being fed
   int step;   // decode steps taken (index into the output list)
   int pad;
-  unsigned long long argmax;  // (orderable logit, ~index) of the best logit
+  unsigned long long argmax;  // (orderable logit << 32 | ~index) of the best logit
 };
 
 __global__ __launch_bounds__(256) void k_dec_begin(DecState *__restrict__ st,
@@ -328,13 +346,26 @@ __global__ __launch_bounds__(256) void k_dec_begin(DecState *__restrict__ st,
   int64_t tok = st->token;
   tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
   for (int64_t k = threadIdx.x; k < H; k += blockDim.x) x[k] = table[tok * H + k];
-  if (threadIdx.x == 0) st->argmax = 0ull;
 }
 
-__global__ void k_dec_end(DecState *__restrict__ st, int32_t *__restrict__ out_tokens,
-                          int out_cap) {
+// Greedy token: the maximum of the lm_head workgroups' keys (one workgroup).
+__global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
+                                                  const unsigned long long *__restrict__ keys,
+                                                  int nkeys, int32_t *__restrict__ out_tokens,
+                                                  int out_cap) {
+  __shared__ unsigned long long sk[16];
+  unsigned long long best = 0ull;
+  for (int i = threadIdx.x; i < nkeys; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned long long key = st->argmax;
+    unsigned long long key = sk[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) key = sk[w] > key ? sk[w] : key;
+    st->argmax = key;
     const int tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
     st->token = tok;
     if (st->step >= 0 && st->step < out_cap) out_tokens[st->step] = tok;
@@ -343,148 +374,257 @@ __global__ void k_dec_end(DecState *__restrict__ st, int32_t *__restrict__ out_t
   }
 }
 
-// Decode attention for one token.  Grid (splits, heads): split s scores keys
-// [32 s, 32 s + 32) of the L = pos + 1 visible ones and writes a partial
-// (max, sum, o[hd]); the last split of a head to finish (device-scope
-// counter, reset by it) combines them.  Every workgroup first forms its
-// head's q (per-head RMSNorm, rotary at pos); the split holding key pos
-// forms the new k and v itself (and the first head of the group writes them
-// into the cache at pos), so no workgroup reads a cache entry written in
-// the same launch.  hd == 128 threads' worth of work per 128-thread group.
-constexpr int kDecKeys = 32;
+// Decode attention for one token, spread over the GPU: one workgroup per
+// (split of kDecKS keys, KV head), serving every query head of that KV
+// group, so each cached key and value is read once per layer and the read
+// is shared by many CUs (one CU alone streams only a few tens of GB/s of
+// dependent loads).  The workgroup issues its K / V tile first
+// (unconditional float4 loads: a conditional load would end in a full
+// vmcnt wait), forms the group's q heads and the new k (per-head RMSNorm,
+// rotary at pos) meanwhile, scores its keys (8 lanes per key, DPP
+// reduction) and writes a partial (max, sum, o[hd]) per query head.  The
+// last split of a KV head to finish (counter, reset by it) merges the
+// partials.  Partials and counters go through agent-scope atomics, which
+// are coherent across XCDs without an L2 flush.  The split holding position
+// pos uses the new k / v directly and also writes them into the cache; no
+// workgroup reads an entry written in the same launch.
+constexpr int kDecKS = 32;          // keys per split
+constexpr int kDecMaxGroup = 4;     // query heads per KV head
+constexpr int kDecMaxLen = 8192;    // cache length (merge weights kept in LDS)
+constexpr int kDecMaxSplits = kDecMaxLen / kDecKS;
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_add_dec(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                false);
+  return v + __builtin_bit_cast(float, moved);
+}
+
+// Sum over each aligned group of 8 lanes (DPP within a row).
+__device__ __forceinline__ float lane8_sum(float v) {
+  v = dpp_add_dec<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add_dec<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add_dec<0x141>(v);  // row_half_mirror: lanes 0-7 <-> 7-0 of each half row
+  return v;
+}
+
+template <int HD>
 __global__ __launch_bounds__(256) void k_dec_attn(
-    const DecState *__restrict__ st, const float *__restrict__ qkv, int nh, int kvh, int hd,
+    const DecState *__restrict__ st, const float *__restrict__ qkv, int nh, int kvh,
     const float *__restrict__ qn, const float *__restrict__ kn, float eps,
     const float *__restrict__ cos, const float *__restrict__ sin, float *ck, float *cv,
     int64_t cap, float scale, float *part, int *counters, float *__restrict__ out) {
-  __shared__ float sq[kAttnMaxHd], skn[kAttnMaxHd], svn[kAttnMaxHd], sh[kAttnMaxHd];
-  __shared__ double shd[4];
-  __shared__ float ssc[kDecKeys];
-  __shared__ float sred[2][kAttnMaxHd];
+  constexpr int kDpk = HD / 8;  // dims per K lane (a multiple of 4)
+  constexpr int kHr = HD / 2;
+  __shared__ __align__(16) float sq[kDecMaxGroup][HD];
+  __shared__ __align__(16) float skn[HD];
+  __shared__ float svn[HD];
+  __shared__ float shx[kDecMaxGroup + 1][HD];
+  __shared__ double shd[kDecMaxGroup + 1][4];
+  __shared__ __align__(16) float ssc[kDecMaxGroup][kDecKS];
+  __shared__ float sred[kDecMaxGroup][2][kAttnMaxHd];
+  __shared__ float sl[kDecMaxGroup][2];
+  __shared__ float sw[kDecMaxGroup][kDecMaxSplits];
+  __shared__ float sden[kDecMaxGroup];
   __shared__ int s_last;
-  const int split = blockIdx.x, h = blockIdx.y;
-  const int group = nh / kvh, kh = h / group;
+  const int split = blockIdx.x, kh = blockIdx.y;
+  const int group = nh / kvh;
+  const int t = threadIdx.x, w = t >> 6, ln = t & 63;
+  const int d = t & (kAttnMaxHd - 1), half = t >> 7;  // V layout: dim, key half
+  const int jk = t >> 3, p8 = t & 7;                  // K layout: key, dim slice
   const int pos = st->pos;
   const int L = pos + 1;
-  const int nsplit = (L + kDecKeys - 1) / kDecKeys;
-  if (split >= nsplit) return;  // uniform per workgroup
-  const int t = threadIdx.x;
-  const int d = t & (kAttnMaxHd - 1);
-  const bool lo = t < hd;       // first hd threads do the per-head vector work
-  // ---- q (and the new k, v for the split holding key pos); the vector
-  // work below is done by threads [0, hd) with blockDim == 256 and
-  // hd <= 128; the block sums include every thread (zeros from the rest)
+  const int nsplit = (L + kDecKS - 1) / kDecKS;
+  if (split >= nsplit) return;  // whole workgroup
+  const int j0 = split * kDecKS;
+  const float *Kb = ck + (int64_t)kh * cap * HD;
+  const float *Vb = cv + (int64_t)kh * cap * HD;
+  const bool lo = t < HD;
+  const int dc = lo ? t : HD - 1;
+  // ---- loads (rows >= pos are read from row 0 and replaced or dropped)
+  float kreg[kDpk];
   {
-    const float xq = lo ? qkv[h * hd + d] : 0.0f;
-    const double ss = block_sum_d((double)xq * (double)xq, shd);
-    const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
-    if (lo) sh[d] = (float)((double)xq * inv * (double)qn[d]);
+    const int j = j0 + jk;
+    const float *kr = Kb + (int64_t)(j < pos ? j : 0) * HD + p8 * kDpk;
+#pragma unroll
+    for (int e = 0; e < kDpk; e += 4) {
+      const float4 v4 = *(const float4 *)(kr + e);
+      kreg[e] = v4.x;
+      kreg[e + 1] = v4.y;
+      kreg[e + 2] = v4.z;
+      kreg[e + 3] = v4.w;
+    }
+  }
+  const int dv = d < HD ? d : HD - 1;
+  float vreg[kDecKS / 2];
+#pragma unroll
+  for (int u = 0; u < kDecKS / 2; u++) {
+    const int j = j0 + half * (kDecKS / 2) + u;
+    vreg[u] = Vb[(int64_t)(j < pos ? j : 0) * HD + dv];
+  }
+  float xq[kDecMaxGroup];
+#pragma unroll
+  for (int g = 0; g < kDecMaxGroup; g++)
+    xq[g] = qkv[(kh * group + (g < group ? g : 0)) * HD + dc];
+  const float xk = qkv[(nh + kh) * HD + dc];
+  const float xv = qkv[(nh + kvh + kh) * HD + dc];
+  const float gq = qn[dc], gk = kn[dc];
+  const int pi = dc < kHr ? dc : dc - kHr;
+  const double cs = (double)cos[(int64_t)pos * kHr + pi];
+  const double sn = (double)sin[(int64_t)pos * kHr + pi];
+  // ---- per-head RMSNorm of the group's q heads and of k (double sums,
+  // one block reduction for all of them), then rotary at pos
+  {
+    double ss[kDecMaxGroup + 1];
+#pragma unroll
+    for (int g = 0; g <= kDecMaxGroup; g++) {
+      const float x = g < kDecMaxGroup ? xq[g] : xk;
+      ss[g] = lo ? (double)x * (double)x : 0.0;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+      for (int g = 0; g <= kDecMaxGroup; g++) ss[g] += __shfl_xor(ss[g], off, 64);
+    }
+    if (ln == 0) {
+#pragma unroll
+      for (int g = 0; g <= kDecMaxGroup; g++) shd[g][w] = ss[g];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g <= kDecMaxGroup; g++) {
+      const double tot = shd[g][0] + shd[g][1] + shd[g][2] + shd[g][3];
+      const double inv = 1.0 / sqrt(tot / (double)HD + (double)eps);
+      const float x = g < kDecMaxGroup ? xq[g] : xk;
+      const float gam = g < kDecMaxGroup ? gq : gk;
+      if (lo) shx[g][t] = (float)((double)x * inv * (double)gam);
+    }
     __syncthreads();
     if (lo) {
-      const int hr = hd / 2, pi = d < hr ? d : d - hr;
-      const double c = cos[(int64_t)pos * hr + pi], sn = sin[(int64_t)pos * hr + pi];
-      const double x0 = sh[pi], x1 = sh[pi + hr];
-      sq[d] = (float)(d < hr ? x0 * c - x1 * sn : x1 * c + x0 * sn);
+#pragma unroll
+      for (int g = 0; g <= kDecMaxGroup; g++) {
+        const double x0 = shx[g][pi], x1 = shx[g][pi + kHr];
+        const float r = (float)(t < kHr ? x0 * cs - x1 * sn : x1 * cs + x0 * sn);
+        if (g < kDecMaxGroup) sq[g][t] = r; else skn[t] = r;
+      }
+      svn[t] = xv;
     }
     __syncthreads();
   }
-  const bool has_new = split == nsplit - 1;
-  if (has_new) {
-    const float xk = lo ? qkv[(nh + kh) * hd + d] : 0.0f;
-    const double ss = block_sum_d((double)xk * (double)xk, shd);
-    const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
-    if (lo) sh[d] = (float)((double)xk * inv * (double)kn[d]);
-    __syncthreads();
-    if (lo) {
-      const int hr = hd / 2, pi = d < hr ? d : d - hr;
-      const double c = cos[(int64_t)pos * hr + pi], sn = sin[(int64_t)pos * hr + pi];
-      const double x0 = sh[pi], x1 = sh[pi + hr];
-      const float kr = (float)(d < hr ? x0 * c - x1 * sn : x1 * c + x0 * sn);
-      const float vv = qkv[(nh + kvh + kh) * hd + d];
-      skn[d] = kr;
-      svn[d] = vv;
-      if (h % group == 0) {
-        ck[((int64_t)kh * cap + pos) * hd + d] = kr;
-        cv[((int64_t)kh * cap + pos) * hd + d] = vv;
-      }
-    }
-    __syncthreads();
+  if (split == nsplit - 1 && lo) {  // this split holds position pos
+    ck[((int64_t)kh * cap + pos) * HD + t] = skn[t];
+    cv[((int64_t)kh * cap + pos) * HD + t] = xv;
   }
-  // ---- scores of this split's keys: 8 threads per key, hd/8 dims each
-  const int j0 = split * kDecKeys;
-  const int nk = min(kDecKeys, L - j0);
-  const float *Kb = ck + (int64_t)kh * cap * hd;
-  const float *Vb = cv + (int64_t)kh * cap * hd;
+  // ---- scores of this split's keys for each query head of the group
   {
-    const int jl = t >> 3, part8 = t & 7;
-    const int j = j0 + jl;
-    float dot = 0.0f;
-    if (jl < nk) {
-      const int dpt = hd / 8;
-      for (int e = 0; e < dpt; e++) {
-        const int dd = part8 * dpt + e;
-        const float kvv = (j == pos) ? skn[dd] : Kb[(int64_t)j * hd + dd];
-        dot = fmaf(sq[dd], kvv, dot);
+    const int j = j0 + jk;
+    if (j == pos) {
+#pragma unroll
+      for (int e = 0; e < kDpk; e++) kreg[e] = skn[p8 * kDpk + e];
+    }
+#pragma unroll
+    for (int g = 0; g < kDecMaxGroup; g++) {
+      if (g < group) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kDpk; e++) dot = fmaf(sq[g][p8 * kDpk + e], kreg[e], dot);
+        dot = lane8_sum(dot);
+        if (p8 == 0) ssc[g][jk] = j < L ? dot * scale : -INFINITY;
       }
     }
-    for (int off = 4; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 8);
-    if (part8 == 0 && jl < kDecKeys) ssc[jl] = jl < nk ? dot * scale : -INFINITY;
+  }
+  // values of keys past pos are dropped here (their probability is 0, but
+  // the row they were read from may hold anything)
+#pragma unroll
+  for (int u = 0; u < kDecKS / 2; u++) {
+    const int j = j0 + half * (kDecKS / 2) + u;
+    vreg[u] = j < pos ? vreg[u] : (j == pos ? svn[dv] : 0.0f);
   }
   __syncthreads();
-  float mx = -INFINITY;
-  for (int jl = 0; jl < nk; jl++) mx = fmaxf(mx, ssc[jl]);
-  // ---- o = sum p_j v_j: thread (d, half) sums half of the keys
-  {
-    const int half = t >> 7;
-    float acc = 0.0f, ls = 0.0f;
-    if (d < hd) {
-      for (int jl = half; jl < nk; jl += 2) {
-        const float p = expf(ssc[jl] - mx);
-        const int j = j0 + jl;
-        const float vv = (j == pos) ? svn[d] : Vb[(int64_t)j * hd + d];
-        acc = fmaf(p, vv, acc);
+  // ---- split-local softmax and o = sum_j p_j v_j, per query head
+#pragma unroll
+  for (int g = 0; g < kDecMaxGroup; g++) {
+    if (g < group) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kDecKS; i++) mx = fmaxf(mx, ssc[g][i]);
+      float acc = 0.0f, ls = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kDecKS / 2; u++) {
+        const float p = expf(ssc[g][half * (kDecKS / 2) + u] - mx);
         ls += p;
+        acc = fmaf(p, vreg[u], acc);
       }
-    }
-    sred[half][d] = acc;
-    __syncthreads();
-    if (t < hd) {
-      float* pp = part + ((int64_t)h * gridDim.x + split) * (hd + 2);
-      pp[2 + t] = sred[0][t] + sred[1][t];
+      sred[g][half][d] = acc;
+      if (d == 0) sl[g][half] = ls;
       if (t == 0) {
-        float lsum = 0.0f;
-        for (int jl = 0; jl < nk; jl++) lsum += expf(ssc[jl] - mx);
-        pp[0] = mx;
-        pp[1] = lsum;
+        float *pp = part + ((int64_t)(kh * group + g) * gridDim.x + split) * (HD + 2);
+        __hip_atomic_store(pp, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    (void)ls;
   }
-  // ---- publish the partial; the last split of this head combines
+  __syncthreads();
+  if (lo) {
+    for (int g = 0; g < group; g++) {
+      float *pp = part + ((int64_t)(kh * group + g) * gridDim.x + split) * (HD + 2);
+      if (t == 0)
+        __hip_atomic_store(pp + 1, sl[g][0] + sl[g][1], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pp + 2 + t, sred[g][0][t] + sred[g][1][t], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // ---- publish: every partial store has completed before the count moves
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (t == 0) {
-    __threadfence();
-    const int prev = atomicAdd(&counters[h], 1);
+    const int prev =
+        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == nsplit - 1;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  if (t < hd) {
-    const float *p0 = part + (int64_t)h * gridDim.x * (hd + 2);
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < nsplit; s2++) M = fmaxf(M, __builtin_nontemporal_load(p0 + s2 * (hd + 2)));
-    float num = 0.0f, den = 0.0f;
-    for (int s2 = 0; s2 < nsplit; s2++) {
-      const float *pp = p0 + s2 * (hd + 2);
-      const float w = expf(__builtin_nontemporal_load(pp) - M);
-      num = fmaf(w, __builtin_nontemporal_load(pp + 2 + t), num);
-      den = fmaf(w, __builtin_nontemporal_load(pp + 1), den);
-    }
-    out[h * hd + t] = num / den;
+  // ---- merge (last split of this KV head): weights exp(m_s - M) in LDS,
+  // then each thread (head g, dim) sums its dimension over the splits
+  const float *pg = part + (int64_t)kh * group * gridDim.x * (HD + 2);
+  for (int i = t; i < group * nsplit; i += 256) {
+    const int g = i / nsplit, s2 = i % nsplit;
+    sw[g][s2] = __hip_atomic_load(pg + ((int64_t)g * gridDim.x + s2) * (HD + 2),
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (t == 0) counters[h] = 0;
+  __syncthreads();
+  if (t < group) {
+    float M = -INFINITY;
+    for (int s2 = 0; s2 < nsplit; s2++) M = fmaxf(M, sw[t][s2]);
+    float den = 0.0f;
+    for (int s2 = 0; s2 < nsplit; s2++) {
+      const float wgt = expf(sw[t][s2] - M);
+      sw[t][s2] = wgt;
+      den = fmaf(wgt, __hip_atomic_load(pg + ((int64_t)t * gridDim.x + s2) * (HD + 2) + 1,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 den);
+    }
+    sden[t] = den;
+  }
+  __syncthreads();
+  for (int i = t; i < group * HD; i += 256) {
+    const int g = i / HD, dd = i % HD;
+    const float *p0 = pg + (int64_t)g * gridDim.x * (HD + 2) + 2 + dd;
+    float num = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int s2 = s0 + u < nsplit ? s0 + u : nsplit - 1;
+        v[u] = __hip_atomic_load(p0 + (int64_t)s2 * (HD + 2), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (s0 + u < nsplit) num = fmaf(sw[g][s0 + u], v[u], num);
+    }
+    out[(kh * group + g) * HD + dd] = num / sden[g];
+  }
+  if (t == 0) __hip_atomic_store(&counters[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -620,15 +760,18 @@ struct mmnb_decoder {
   float *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
         *gu = nullptr, *act = nullptr, *tmp = nullptr, *logits = nullptr;
   float *cache_k = nullptr, *cache_v = nullptr, *cos = nullptr, *sin = nullptr;
-  float *part = nullptr;
-  int *counters = nullptr;
+  float *part = nullptr;    // attention partials [heads, splits, hd + 2]
+  int *counters = nullptr;  // per KV head: attention splits finished
   DecState *state = nullptr;
+  unsigned long long *keys = nullptr;  // lm_head workgroups' best (value, ~index)
+  int64_t nkeys = 0;
   int32_t *out_tokens = nullptr;
   int64_t *tok = nullptr;
   int64_t pos = 0;        // host mirror of the sequence length
   int64_t steps_done = 0; // host mirror of DecState::step
   bool primed = false;    // a token is waiting in DecState::token
   hipGraphExec_t graph = nullptr;
+  bool use_graph = true;  // replay the recorded step (else launch it eagerly)
   std::vector<void *> allocs;
 };
 
@@ -664,13 +807,14 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
     return fail(MMNB_ERR_ARG, "decoder: null argument");
   const mmnb_decoder_config &c = *cfg;
   if (c.layers <= 0 || c.hidden <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.head_dim <= 0 ||
-      c.intermediate <= 0 || c.vocab <= 0 || c.max_len <= 0 || c.heads % c.kv_heads != 0)
+      c.intermediate <= 0 || c.vocab <= 0 || c.max_len <= 0 || c.max_len > kDecMaxLen ||
+      c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > kDecMaxGroup)
     return fail(MMNB_ERR_ARG, "decoder: bad configuration");
-  if (c.head_dim > kAttnMaxHd || (c.head_dim % 16) || c.hidden % 64 || (c.heads * c.head_dim) % 64 ||
+  if (c.head_dim > kAttnMaxHd || (c.head_dim % 32) || c.hidden % 64 || (c.heads * c.head_dim) % 64 ||
       c.intermediate % 64 || c.hidden > 4096 || c.intermediate > 4096 ||
       c.heads * c.head_dim > 4096)
     return fail(MMNB_ERR_UNSUPPORTED,
-                "decoder: needs head_dim <= 128 (a multiple of 16) and hidden, heads*head_dim, "
+                "decoder: needs head_dim <= 128 (a multiple of 32) and hidden, heads*head_dim, "
                 "intermediate multiples of 64 and <= 4096");
   if (lm_head->kind != kPackNBits || lm_head->k != c.hidden || lm_head->n != c.vocab ||
       lm_head->ctx != ctx)
@@ -684,10 +828,11 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
   d->cfg = c;
   d->layers.resize((size_t)c.layers);
   d->lm = lm_head;
+  d->nkeys = dec_gemv_blocks(ctx, c.vocab);
   const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim,
                 I = c.intermediate, Lmax = c.max_len;
   const int64_t QKV = (nh + 2 * kvh) * hd;
-  const int64_t nsplit = (Lmax + kDecKeys - 1) / kDecKeys;
+  const int64_t nsplit = (Lmax + kDecKS - 1) / kDecKS;
   auto A = [&](size_t bytes, void **p) { return dec_alloc(d, bytes, p); };
   if ((rc = dec_upload(d, embed, (size_t)(c.vocab * H), &d->embed)) ||
       (rc = dec_upload(d, final_norm, (size_t)H, &d->final_norm)) ||
@@ -703,8 +848,9 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
       (rc = A((size_t)(c.layers * kvh * Lmax * hd) * 4, (void **)&d->cache_k)) ||
       (rc = A((size_t)(c.layers * kvh * Lmax * hd) * 4, (void **)&d->cache_v)) ||
       (rc = A((size_t)(nh * nsplit * (hd + 2)) * 4, (void **)&d->part)) ||
-      (rc = A((size_t)nh * 4, (void **)&d->counters)) ||
+      (rc = A((size_t)kvh * 4, (void **)&d->counters)) ||
       (rc = A(sizeof(DecState), (void **)&d->state)) ||
+      (rc = A((size_t)dec_gemv_blocks(ctx, c.vocab) * 8, (void **)&d->keys)) ||
       (rc = A((size_t)Lmax * 4, (void **)&d->out_tokens)) ||
       (rc = A((size_t)Lmax * 8, (void **)&d->tok))) {
     mmnb_decoder_free(d);
@@ -724,8 +870,8 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
     mmnb_decoder_free(d);
     return rc;
   }
-  hipError_t e = hipMemset(d->counters, 0, (size_t)nh * 4);
-  if (e == hipSuccess) e = hipMemset(d->state, 0, sizeof(DecState));
+  hipError_t e = hipMemset(d->state, 0, sizeof(DecState));
+  if (e == hipSuccess) e = hipMemset(d->counters, 0, (size_t)kvh * 4);
   if (e != hipSuccess) {
     mmnb_decoder_free(d);
     return check_hip(e, "hipMemset");
@@ -780,6 +926,7 @@ int mmnb_decoder_reset(mmnb_decoder *d) {
   if (rc) return rc;
   MMNB_HIP(hipStreamSynchronize(d->ctx->stream));
   MMNB_HIP(hipMemset(d->state, 0, sizeof(DecState)));
+  MMNB_HIP(hipMemset(d->counters, 0, (size_t)d->cfg.kv_heads * 4));
   d->pos = 0;
   d->steps_done = 0;
   d->primed = false;
@@ -842,9 +989,8 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
       return rc;
   }
   // greedy token of the last row: final norm fused into lm_head
-  MMNB_HIP(hipMemsetAsync(&d->state->argmax, 0, 8, s));
   if ((rc = launch_dec_gemv(ctx, d->lm, d->x + (n - 1) * H, d->final_norm, eps, kDecArgmax,
-                            nullptr, d->logits, &d->state->argmax)))
+                            nullptr, d->logits, d->keys)))
     return rc;
   // state: token = argmax, pos = P + n (k_dec_end advances pos by one and
   // records the token; set pos so that it lands on P + n)
@@ -852,8 +998,8 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
   hs.pos = (int)(P + n - 1);
   hs.step = 0;
   MMNB_HIP(hipMemcpyAsync(d->state, &hs, 8 + 4 + 4, hipMemcpyHostToDevice, s));
-  // the argmax field (offset 16) is kept; k_dec_end turns it into the token
-  if ((rc = launch(ctx, kKernDecOps, k_dec_end, dim3(1), dim3(64), 0, d->state, d->out_tokens,
+  if ((rc = launch(ctx, kKernDecOps, k_dec_end, dim3(1), dim3(1024), 0, d->state,
+                   (const unsigned long long *)d->keys, (int)d->nkeys, d->out_tokens,
                    (int)c.max_len)))
     return rc;
   int32_t tok = 0;
@@ -867,13 +1013,33 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
   return MMNB_OK;
 }
 
+// Decode attention of one layer: grid (splits of the cache, KV heads);
+// splits past the current position exit at once.
+static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float *ck, float *cv) {
+  mmnb_ctx *ctx = d->ctx;
+  const mmnb_decoder_config &c = d->cfg;
+  const dim3 grid((unsigned)((c.max_len + kDecKS - 1) / kDecKS), (unsigned)c.kv_heads);
+  const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+#define MMNB_DEC_ATTN(HD)                                                                      \
+  launch(ctx, kKernDecAttn, k_dec_attn<HD>, grid, dim3(256), 0, (const DecState *)d->state,   \
+         (const float *)d->qkv, (int)c.heads, (int)c.kv_heads, (const float *)L.qn,            \
+         (const float *)L.kn, c.eps, (const float *)d->cos, (const float *)d->sin, ck, cv,     \
+         c.max_len, scale, d->part, d->counters, d->attn)
+  switch (c.head_dim) {
+    case 32: return MMNB_DEC_ATTN(32);
+    case 64: return MMNB_DEC_ATTN(64);
+    case 96: return MMNB_DEC_ATTN(96);
+    case 128: return MMNB_DEC_ATTN(128);
+    default: return fail(MMNB_ERR_UNSUPPORTED, "decoder: head_dim");
+  }
+#undef MMNB_DEC_ATTN
+}
+
 static int dec_record_step(mmnb_decoder *d) {
   mmnb_ctx *ctx = d->ctx;
   const mmnb_decoder_config &c = d->cfg;
-  const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim, Lmax = c.max_len;
+  const int64_t H = c.hidden, kvh = c.kv_heads, hd = c.head_dim, Lmax = c.max_len;
   const float eps = c.eps;
-  const float scale = (float)(1.0 / std::sqrt((double)hd));
-  const int64_t nsplit = (Lmax + kDecKeys - 1) / kDecKeys;
   int rc;
   if ((rc = launch(ctx, kKernDecOps, k_dec_begin, dim3(1), dim3(256), 0, d->state,
                    (const float *)d->embed, H, c.vocab, d->x)))
@@ -883,11 +1049,7 @@ static int dec_record_step(mmnb_decoder *d) {
     float *ck = d->cache_k + li * kvh * Lmax * hd, *cv = d->cache_v + li * kvh * Lmax * hd;
     if ((rc = launch_dec_gemv(ctx, L.qkv, d->x, L.ln1, eps, kDecPlain, nullptr, d->qkv, nullptr)))
       return rc;
-    if ((rc = launch(ctx, kKernDecAttn, k_dec_attn, dim3((unsigned)nsplit, (unsigned)nh),
-                     dim3(256), 0, (const DecState *)d->state, (const float *)d->qkv, (int)nh,
-                     (int)kvh, (int)hd, (const float *)L.qn, (const float *)L.kn, eps,
-                     (const float *)d->cos, (const float *)d->sin, ck, cv, Lmax, scale, d->part,
-                     d->counters, d->attn)))
+    if ((rc = launch_dec_attn(d, L, ck, cv)))
       return rc;
     if ((rc = launch_dec_gemv(ctx, L.o, d->attn, nullptr, eps, kDecResidual, d->x, d->x, nullptr)))
       return rc;
@@ -898,9 +1060,10 @@ static int dec_record_step(mmnb_decoder *d) {
       return rc;
   }
   if ((rc = launch_dec_gemv(ctx, d->lm, d->x, d->final_norm, eps, kDecArgmax, nullptr, d->logits,
-                            &d->state->argmax)))
+                            d->keys)))
     return rc;
-  return launch(ctx, kKernDecOps, k_dec_end, dim3(1), dim3(64), 0, d->state, d->out_tokens,
+  return launch(ctx, kKernDecOps, k_dec_end, dim3(1), dim3(1024), 0, d->state,
+                (const unsigned long long *)d->keys, (int)d->nkeys, d->out_tokens,
                 (int)c.max_len);
 }
 
@@ -921,6 +1084,18 @@ int mmnb_decoder_decode(mmnb_decoder *d, int64_t steps, int32_t *tokens) {
   int rc = set_device(ctx);
   if (rc) return rc;
   hipStream_t s = ctx->stream;
+  const int64_t first = d->steps_done;
+  if (!d->use_graph) {
+    for (int64_t i = 0; i < steps; i++)
+      if ((rc = dec_record_step(d))) return rc;
+    if (tokens)
+      MMNB_HIP(hipMemcpyAsync(tokens, d->out_tokens + first, (size_t)steps * 4,
+                              hipMemcpyDeviceToHost, s));
+    MMNB_HIP(hipStreamSynchronize(s));
+    d->pos += steps;
+    d->steps_done += steps;
+    return MMNB_OK;
+  }
   if (!d->graph) {
     MMNB_HIP(hipStreamSynchronize(s));
     MMNB_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -941,7 +1116,6 @@ int mmnb_decoder_decode(mmnb_decoder *d, int64_t steps, int32_t *tokens) {
       return check_hip(e, "hipGraphInstantiate");
     }
   }
-  const int64_t first = d->steps_done;
   for (int64_t i = 0; i < steps; i++) MMNB_HIP(hipGraphLaunch(d->graph, s));
   if (tokens)
     MMNB_HIP(hipMemcpyAsync(tokens, d->out_tokens + first, (size_t)steps * 4,
@@ -966,5 +1140,11 @@ int mmnb_decoder_logits(mmnb_decoder *d, float *logits) {
 int mmnb_decoder_position(mmnb_decoder *d, int64_t *pos) {
   if (!d || !pos) return fail(MMNB_ERR_ARG, "decoder: null argument");
   *pos = d->pos;
+  return MMNB_OK;
+}
+
+int mmnb_decoder_set_graph(mmnb_decoder *d, int use_graph) {
+  if (!d) return fail(MMNB_ERR_ARG, "decoder: null handle");
+  d->use_graph = use_graph != 0;
   return MMNB_OK;
 }

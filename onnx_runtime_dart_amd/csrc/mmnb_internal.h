@@ -125,10 +125,13 @@ enum KernelId {
   kKernPrepIntB = 7,
   kKernProbeEmpty = 8,
   kKernProbeRead = 9,
-  kKernDecGemv = 10,
-  kKernDecAttn = 11,
-  kKernDecOps = 12,
-  kKernCount = 13
+  kKernDecGemv = 10,     // decode MatMulNBits, RMSNorm prologue (q/k/v)
+  kKernDecAttn = 11,     // attention (decode step and prompt rows)
+  kKernDecOps = 12,      // norms, rotary, embedding, SwiGLU rows, step state
+  kKernDecGemvRes = 13,  // decode MatMulNBits + residual (o, down)
+  kKernDecGemvGlu = 14,  // decode MatMulNBits, RMSNorm + SwiGLU (gate/up)
+  kKernDecGemvLm = 15,   // decode MatMulNBits, RMSNorm + argmax (lm_head)
+  kKernCount = 16
 };
 
 // Launch `kern` on the context stream; in timing mode the dispatch records
@@ -177,12 +180,14 @@ inline int set_device(mmnb_ctx *ctx) {
 //   norm_gamma != null: a = x * rsqrt(mean(x^2) + eps) * gamma (x = d_x)
 //   epi kDecPlain:  y[n] = v;   kDecResidual: y[n] = resid[n] + v;
 //   kDecSwiglu:  columns are gate/up interleaved, y[j] = silu(v[2j]) * v[2j+1];
-//   kDecArgmax:  y[n] = v and the greatest (value, lowest index) is folded
-//                into *d_argmax with a 64-bit atomic max.
+//   kDecArgmax:  y[n] = v and workgroup b stores d_argmax[b] = the greatest
+//                (orderable value << 32 | ~index) key of its columns, for
+//                dec_gemv_blocks(ctx, n) workgroups.
 enum DecEpilogue { kDecPlain = 0, kDecResidual = 1, kDecSwiglu = 2, kDecArgmax = 3 };
 int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
                     const float *norm_gamma, float eps, int epi, const float *resid,
                     float *d_y, unsigned long long *d_argmax);
+int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n);
 
 // Kernel launchers (return MMNB_OK or an error code) -------------------------
 // MatMulNBits: y[m, n] = a[m, k] * W;  lda = row stride of a (elements).

@@ -361,8 +361,9 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
 //   EPI    kDecResidual (the residual Add after o and down),
 //          kDecSwiglu (gate/up columns interleaved 2j/2j+1 in the pack, so a
 //          workgroup holds both halves of its outputs: silu(g) * u),
-//          kDecArgmax (lm_head: greedy token by a 64-bit atomic max of
-//          (orderable value, ~index), ties to the lowest index).
+//          kDecArgmax (lm_head: each workgroup stores the best key
+//          (orderable value << 32 | ~index) of its columns; the greedy
+//          token is the maximum key, ties going to the lowest index).
 // Lane layout and arithmetic follow k_gemv_valu with M = 1 and one
 // quantisation block per chunk; K is at most 4096 (one chunk per lane).
 // ---------------------------------------------------------------------------
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
       const float sig = 1.0f / (1.0f + expf(-gg));
       Y[col0 / 2 + i] = (gg * sig) * uu;
     }
-  } else {  // kDecArgmax
+  } else {  // kDecArgmax: this workgroup's best key, reduced by the caller
     __shared__ unsigned long long keys[2 * R];
     if (i < 2 * R) {
       if (col < N) Y[col] = v;
@@ -503,9 +504,20 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
     if (i == 0) {
       unsigned long long best = keys[0];
       for (int q = 1; q < 2 * R; q++) best = keys[q] > best ? keys[q] : best;
-      atomicMax(argmax, best);
+      argmax[blockIdx.x] = best;
     }
   }
+}
+
+static int dec_gemv_r(const mmnb_ctx *ctx, int64_t n) {
+  int R = 8;
+  while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  return R;
+}
+
+int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n) {
+  const int R = dec_gemv_r(ctx, n);
+  return (n + 2 * R - 1) / (2 * R);
 }
 
 int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
@@ -518,14 +530,16 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
   const int C = (int)(p->col_bytes / 16);
   const int nw = (C + 31) / 32;
   const int64_t n = p->n;
-  int R = 8;
-  while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  const int R = dec_gemv_r(ctx, n);
   const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
   const dim3 block((unsigned)(64 * nw));
   const int bs_log2 = ilog2(p->block);
   const bool norm = norm_gamma != nullptr;
+  const int kid = epi == kDecResidual ? kKernDecGemvRes
+                  : epi == kDecSwiglu ? kKernDecGemvGlu
+                  : epi == kDecArgmax ? kKernDecGemvLm : kKernDecGemv;
 #define MMNB_DEC(RR, NN, EE)                                                                   \
-  return launch(ctx, kKernDecGemv, k_dec_gemv<RR, NN, EE>, grid, block, 0, d_x, norm_gamma, eps, \
+  return launch(ctx, kid, k_dec_gemv<RR, NN, EE>, grid, block, 0, d_x, norm_gamma, eps,         \
                 p->d_w, p->col_bytes, p->d_scales, (int)p->n_blocks, bs_log2, (int)p->k,     \
                 (int)n, resid, d_y, d_argmax, C)
 #define MMNB_DEC_R(NN, EE)              \

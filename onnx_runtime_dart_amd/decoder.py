@@ -203,6 +203,10 @@ class GpuDecoder:
         check(self.ctx.lib.mmnb_decoder_position(self.handle, ctypes.byref(p)))
         return int(p.value)
 
+    def use_graph(self, on):
+        """Replay the recorded step graph (default) or launch eagerly."""
+        check(self.ctx.lib.mmnb_decoder_set_graph(self.handle, int(bool(on))))
+
     def reset(self):
         check(self.ctx.lib.mmnb_decoder_reset(self.handle))
 
