@@ -364,6 +364,17 @@ def profile_pass(ctx, lib, ops, synth, kind):
         for _ in range(20):
             lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, pack.handle, da.ptr, m, dy.ptr))
         what = "20 GEMM calls (M=512 K=N=4096 block 32, zero points)"
+    elif kind == "decoder":
+        from onnx_runtime_dart_amd import decoder as G
+        cfg = G.QWEN3_0_6B
+        dec = G.GpuDecoder(G.random_weights(cfg, seed=0), ctx)
+        dec.use_graph(False)  # launched one by one, so a tracer sees every kernel
+        dec.prefill(np.random.default_rng(3).integers(0, cfg.vocab, 256))
+        dec.decode(64)
+        ctx.synchronize()
+        dec.free()
+        what = ("decoder (Qwen3-0.6B shape): 256-token prefill + 64 decode steps, "
+                "decode kernels launched eagerly")
     else:
         m, k, n = 512, 1024, 3072
         x, b = synth.int8_chain_problem(m, k, n)
@@ -396,10 +407,12 @@ def main():
                     help="counter pass for rocprofv3 (prints no JSON): the kernel chosen by "
                          "--profile-kind, then a 64 MiB device-to-device copy (10 calls) as "
                          "the counter calibration")
-    ap.add_argument("--profile-kind", default="gemv", choices=["gemv", "gemm", "int8"],
+    ap.add_argument("--profile-kind", default="gemv",
+                    choices=["gemv", "gemm", "int8", "decoder"],
                     help="gemv: headline GEMV, 100 calls over the rotated packs; gemm: "
                          "M=512 K=N=4096 block 32 with zero points, 20 calls; int8: the "
-                         "DQL -> MatMulInteger -> rescale chain, 50 calls")
+                         "DQL -> MatMulInteger -> rescale chain, 50 calls; decoder: the "
+                         "Qwen3-shaped decoder, 256-token prefill + 64 steps, eager")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs the kernel on a single "

@@ -423,8 +423,9 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   __shared__ double shd[kDecMaxGroup + 1][4];
   __shared__ __align__(16) float ssc[kDecMaxGroup][kDecKS];
   __shared__ float sred[kDecMaxGroup][2][kAttnMaxHd];
-  __shared__ float sl[kDecMaxGroup][2];
-  __shared__ float sw[kDecMaxGroup][kDecMaxSplits];
+  __shared__ __align__(16) float sp[kDecMaxGroup][kDecKS];
+  __shared__ float smx[kDecMaxGroup], sl[kDecMaxGroup];
+  __shared__ float sw[kDecMaxGroup][kDecMaxSplits], sls[kDecMaxGroup][kDecMaxSplits];
   __shared__ float sden[kDecMaxGroup];
   __shared__ int s_last;
   const int split = blockIdx.x, kh = blockIdx.y;
@@ -483,7 +484,8 @@ __global__ __launch_bounds__(256) void k_dec_attn(
     }
     for (int off = 32; off > 0; off >>= 1) {
 #pragma unroll
-      for (int g = 0; g <= kDecMaxGroup; g++) ss[g] += __shfl_xor(ss[g], off, 64);
+      for (int g = 0; g <= kDecMaxGroup; g++)
+        if (g < group || g == kDecMaxGroup) ss[g] += __shfl_xor(ss[g], off, 64);
     }
     if (ln == 0) {
 #pragma unroll
@@ -510,10 +512,6 @@ __global__ __launch_bounds__(256) void k_dec_attn(
     }
     __syncthreads();
   }
-  if (split == nsplit - 1 && lo) {  // this split holds position pos
-    ck[((int64_t)kh * cap + pos) * HD + t] = skn[t];
-    cv[((int64_t)kh * cap + pos) * HD + t] = xv;
-  }
   // ---- scores of this split's keys for each query head of the group
   {
     const int j = j0 + jk;
@@ -534,44 +532,59 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   }
   // values of keys past pos are dropped here (their probability is 0, but
   // the row they were read from may hold anything)
+  const float vnew = svn[dv];
 #pragma unroll
   for (int u = 0; u < kDecKS / 2; u++) {
     const int j = j0 + half * (kDecKS / 2) + u;
-    vreg[u] = j < pos ? vreg[u] : (j == pos ? svn[dv] : 0.0f);
+    vreg[u] = j < pos ? vreg[u] : (j == pos ? vnew : 0.0f);
   }
   __syncthreads();
-  // ---- split-local softmax and o = sum_j p_j v_j, per query head
+  // ---- split-local softmax, one thread per (head, key): max and sum over
+  // the split's keys by shuffles within 32-lane groups, p to LDS
+  if (t < group * kDecKS) {
+    const int g = t / kDecKS, i = t % kDecKS;
+    const float sc = ssc[g][i];
+    float mx = sc;
+#pragma unroll
+    for (int off = kDecKS / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kDecKS));
+    const float p = expf(sc - mx);
+    float ls = p;
+#pragma unroll
+    for (int off = kDecKS / 2; off > 0; off >>= 1) ls += __shfl_xor(ls, off, kDecKS);
+    sp[g][i] = p;
+    if (i == 0) {
+      smx[g] = mx;
+      sl[g] = ls;
+    }
+  }
+  __syncthreads();
+  // ---- o = sum_j p_j v_j over the split, thread (dim, key half) per head
 #pragma unroll
   for (int g = 0; g < kDecMaxGroup; g++) {
     if (g < group) {
-      float mx = -INFINITY;
+      float acc = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kDecKS; i++) mx = fmaxf(mx, ssc[g][i]);
-      float acc = 0.0f, ls = 0.0f;
-#pragma unroll
-      for (int u = 0; u < kDecKS / 2; u++) {
-        const float p = expf(ssc[g][half * (kDecKS / 2) + u] - mx);
-        ls += p;
-        acc = fmaf(p, vreg[u], acc);
-      }
+      for (int u = 0; u < kDecKS / 2; u++) acc = fmaf(sp[g][half * (kDecKS / 2) + u], vreg[u], acc);
       sred[g][half][d] = acc;
-      if (d == 0) sl[g][half] = ls;
-      if (t == 0) {
-        float *pp = part + ((int64_t)(kh * group + g) * gridDim.x + split) * (HD + 2);
-        __hip_atomic_store(pp, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
   }
   __syncthreads();
   if (lo) {
     for (int g = 0; g < group; g++) {
       float *pp = part + ((int64_t)(kh * group + g) * gridDim.x + split) * (HD + 2);
-      if (t == 0)
-        __hip_atomic_store(pp + 1, sl[g][0] + sl[g][1], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+      if (t == 0) {
+        __hip_atomic_store(pp, smx[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + 1, sl[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       __hip_atomic_store(pp + 2 + t, sred[g][0][t] + sred[g][1][t], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  // the split holding position pos writes the new k / v into the cache
+  // (issued late: an outstanding store would hold up every vmcnt wait above)
+  if (split == nsplit - 1 && lo) {
+    ck[((int64_t)kh * cap + pos) * HD + t] = skn[t];
+    cv[((int64_t)kh * cap + pos) * HD + t] = xv;
   }
   // ---- publish: every partial store has completed before the count moves
   __builtin_amdgcn_s_waitcnt(0);
@@ -583,13 +596,24 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   }
   __syncthreads();
   if (!s_last) return;
-  // ---- merge (last split of this KV head): weights exp(m_s - M) in LDS,
-  // then each thread (head g, dim) sums its dimension over the splits
+  // ---- merge (last split of this KV head), one memory round trip: each
+  // thread (head g, dim) loads its dimension of up to 16 splits while the
+  // splits' (max, sum) go to LDS; then weights exp(m_s - M) and the sums
   const float *pg = part + (int64_t)kh * group * gridDim.x * (HD + 2);
+  const int gt = t / HD, dt = t % HD;  // this thread's (head, dim) while gt < group
+  const float *p0 = pg + (int64_t)(gt < group ? gt : 0) * gridDim.x * (HD + 2) + 2 + dt;
+  float v[16];
+#pragma unroll
+  for (int u = 0; u < 16; u++) {
+    const int s2 = u < nsplit ? u : nsplit - 1;
+    v[u] = __hip_atomic_load(p0 + (int64_t)s2 * (HD + 2), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
   for (int i = t; i < group * nsplit; i += 256) {
     const int g = i / nsplit, s2 = i % nsplit;
-    sw[g][s2] = __hip_atomic_load(pg + ((int64_t)g * gridDim.x + s2) * (HD + 2),
-                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float *pp = pg + ((int64_t)g * gridDim.x + s2) * (HD + 2);
+    sw[g][s2] = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sls[g][s2] = __hip_atomic_load(pp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (t < group) {
@@ -599,30 +623,31 @@ __global__ __launch_bounds__(256) void k_dec_attn(
     for (int s2 = 0; s2 < nsplit; s2++) {
       const float wgt = expf(sw[t][s2] - M);
       sw[t][s2] = wgt;
-      den = fmaf(wgt, __hip_atomic_load(pg + ((int64_t)t * gridDim.x + s2) * (HD + 2) + 1,
-                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 den);
+      den = fmaf(wgt, sls[t][s2], den);
     }
     sden[t] = den;
   }
   __syncthreads();
+  // pairs past the first 256 (group * HD > 256) and splits past the first
+  // 16 (caches longer than 512) load again
   for (int i = t; i < group * HD; i += 256) {
-    const int g = i / HD, dd = i % HD;
-    const float *p0 = pg + (int64_t)g * gridDim.x * (HD + 2) + 2 + dd;
+    const int gi = i / HD, di = i % HD;
+    const float *pi0 = pg + (int64_t)gi * gridDim.x * (HD + 2) + 2 + di;
     float num = 0.0f;
-    for (int s0 = 0; s0 < nsplit; s0 += 8) {
-      float v[8];
+    for (int s0 = 0; s0 < nsplit; s0 += 16) {
+      if (i != t || s0 != 0) {
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int s2 = s0 + u < nsplit ? s0 + u : nsplit - 1;
-        v[u] = __hip_atomic_load(p0 + (int64_t)s2 * (HD + 2), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+        for (int u = 0; u < 16; u++) {
+          const int s2 = s0 + u < nsplit ? s0 + u : nsplit - 1;
+          v[u] = __hip_atomic_load(pi0 + (int64_t)s2 * (HD + 2), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
 #pragma unroll
-      for (int u = 0; u < 8; u++)
-        if (s0 + u < nsplit) num = fmaf(sw[g][s0 + u], v[u], num);
+      for (int u = 0; u < 16; u++)
+        if (s0 + u < nsplit) num = fmaf(sw[gi][s0 + u], v[u], num);
     }
-    out[(kh * group + g) * HD + dd] = num / sden[g];
+    out[(kh * group + gi) * HD + di] = num / sden[gi];
   }
   if (t == 0) __hip_atomic_store(&counters[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
