@@ -179,6 +179,93 @@ int mmnb_dynamic_matmul_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
                             int32_t *d_a_zero_point, int32_t *d_acc,
                             float *d_y);
 
+/* ---- QLinearMatMul, ConvInteger, QLinearConv ----------------------------
+ * The integer products run on the MatMulInteger kernels (exact int32);
+ * 8-bit outputs are int8 when *_is_signed, else uint8.  The reference
+ * returns these as Tensor.int64 (the Dart binding widens). */
+
+/* QLinearMatMul: acc = MatMulInteger(A, B, a_zp, b_zp) with B from
+ * mmnb_pack_integer (its zero point is b_zp); mult = fl32(fl32(a_scale *
+ * b_scale) / y_scale); y = clamp(roundEven(fl32(acc * mult)) + y_zp) to the
+ * output type's range.  Per-tensor scales only (the Dart binding throws
+ * UnsupportedError for others, onnx_qlinear_ops.dart:86-88).  Host buffers, synchronous.
+ * Replaces: opQLinearMatMul (lib/src/onnx_qlinear_ops.dart:83-106),
+ * _dispatch arm 'QLinearMatMul' (lib/src/onnx_graph.dart:1577-1583). */
+int mmnb_qlinear_matmul(mmnb_ctx *ctx, const mmnb_pack *b_pack, const void *a,
+                        int a_is_signed, int64_t a_batch, int64_t m,
+                        const int64_t *a_zero_point, int64_t a_zero_point_len,
+                        float a_scale, float b_scale, float y_scale,
+                        int64_t y_zero_point, int y_is_signed, void *y);
+/* Device-buffer form (d_a_zero_point: device int32, length 0, 1 or m). */
+int mmnb_qlinear_matmul_dev(mmnb_ctx *ctx, const mmnb_pack *b_pack,
+                            const void *d_a, int a_is_signed, int64_t a_batch,
+                            int64_t m, const int32_t *d_a_zero_point,
+                            int64_t a_zero_point_len, float a_scale,
+                            float b_scale, float y_scale, int64_t y_zero_point,
+                            int y_is_signed, void *d_y);
+
+/* 2-D convolution geometry: strides [sh, sw], pads [top, left, bottom,
+ * right], dilations [dh, dw] (ONNX attribute order).  A 1-D convolution is
+ * the 2-D one with height 1 (the reference's reshape, onnx_qlinear_ops.dart:238-252). */
+typedef struct mmnb_conv_params {
+  int64_t strides[2];
+  int64_t pads[4];
+  int64_t dilations[2];
+} mmnb_conv_params;
+
+/* Upload a convolution weight w [m, c_per_group, kh, kw] (int8 when
+ * w_is_signed, else uint8) with its zero point: NULL/0, scalar or per output
+ * channel (length m); other lengths are MMNB_ERR_UNSUPPORTED
+ * (onnx_qlinear_ops.dart:254-257).
+ * Replaces: the weight side of opConvInteger / opQLinearConv; the Dart
+ * binding caches the pack per `w` Tensor. */
+int mmnb_pack_conv(mmnb_ctx *ctx, const void *w, int w_is_signed, int64_t m,
+                   int64_t c_per_group, int64_t kh, int64_t kw, int64_t group,
+                   const int64_t *w_zero_point, int64_t w_zero_point_len,
+                   mmnb_pack **out);
+
+/* Output height and width for an input [n, c, h, wd] (validates the
+ * geometry: c = c_per_group * group, window within the padded input). */
+int mmnb_conv_output_shape(const mmnb_pack *w, int64_t n, int64_t c, int64_t h,
+                           int64_t wd, const mmnb_conv_params *prm,
+                           int64_t *oh, int64_t *ow);
+
+/* ConvInteger: y[n, m, oh, ow] = sum (x - x_zp)(w - w_zp[m]), exact int32;
+ * x [n, c, h, wd] (int8 when x_is_signed, else uint8), x_zp scalar.  Host
+ * buffers, synchronous.
+ * Replaces: opConvInteger (lib/src/onnx_qlinear_ops.dart:235-267, accumulator :160-220), _dispatch
+ * arm 'ConvInteger' (lib/src/onnx_graph.dart:1568-1576). */
+int mmnb_conv_integer(mmnb_ctx *ctx, const mmnb_pack *w, const void *x,
+                      int x_is_signed, int64_t n, int64_t c, int64_t h, int64_t wd,
+                      int64_t x_zero_point, const mmnb_conv_params *prm,
+                      int32_t *y);
+int mmnb_conv_integer_dev(mmnb_ctx *ctx, const mmnb_pack *w, const void *d_x,
+                          int x_is_signed, int64_t n, int64_t c, int64_t h,
+                          int64_t wd, int64_t x_zero_point,
+                          const mmnb_conv_params *prm, int32_t *d_y);
+
+/* QLinearConv: acc as ConvInteger; per output channel c,
+ * mult = x_scale * w_scale[c] / y_scale and y = clamp(roundEven((acc +
+ * bias[c]) * mult) + y_zp), in double as the reference.  w_scale has 1 or m
+ * values (host), bias m int32 values or NULL (host).
+ * Replaces: opQLinearConv (lib/src/onnx_qlinear_ops.dart:270-308), _dispatch
+ * arm 'QLinearConv' (lib/src/onnx_graph.dart:1597-1609). */
+int mmnb_qlinear_conv(mmnb_ctx *ctx, const mmnb_pack *w, const void *x,
+                      int x_is_signed, int64_t n, int64_t c, int64_t h, int64_t wd,
+                      int64_t x_zero_point, float x_scale, const float *w_scale,
+                      int64_t w_scale_len, float y_scale, int64_t y_zero_point,
+                      int y_is_signed, const int32_t *bias,
+                      const mmnb_conv_params *prm, void *y);
+/* Device form: d_x / d_y device buffers; w_scale and bias stay host arrays
+ * (uploaded per call, so this call is not capturable). */
+int mmnb_qlinear_conv_dev(mmnb_ctx *ctx, const mmnb_pack *w, const void *d_x,
+                          int x_is_signed, int64_t n, int64_t c, int64_t h,
+                          int64_t wd, int64_t x_zero_point, float x_scale,
+                          const float *w_scale, int64_t w_scale_len,
+                          float y_scale, int64_t y_zero_point, int y_is_signed,
+                          const int32_t *bias, const mmnb_conv_params *prm,
+                          void *d_y);
+
 /* ---- decoder ops around MatMulNBits -------------------------------------
  * Device buffers, asynchronous on the context stream (like the _dev entry
  * points above).  fp32 throughout. */

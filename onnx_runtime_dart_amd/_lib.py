@@ -42,6 +42,23 @@ SIGNATURES = {
     "mmnb_matmul_integer_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, _vp]),
     "mmnb_dynamic_matmul_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
                                        _vp, _vp]),
+    "mmnb_qlinear_matmul": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, ctypes.c_float,
+                                   ctypes.c_float, ctypes.c_float, _i64, _int, _vp]),
+    "mmnb_qlinear_matmul_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64,
+                                       ctypes.c_float, ctypes.c_float, ctypes.c_float, _i64,
+                                       _int, _vp]),
+    "mmnb_pack_conv": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+                              _P(_vp)]),
+    "mmnb_conv_output_shape": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _P(_i64), _P(_i64)]),
+    "mmnb_conv_integer": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "mmnb_conv_integer_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _vp,
+                                     _vp]),
+    "mmnb_qlinear_conv": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64,
+                                 ctypes.c_float, _vp, _i64, ctypes.c_float, _i64, _int, _vp, _vp,
+                                 _vp]),
+    "mmnb_qlinear_conv_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64,
+                                     ctypes.c_float, _vp, _i64, ctypes.c_float, _i64, _int, _vp,
+                                     _vp, _vp]),
     "mmnb_pack_free": (_int, [_vp]),
     "mmnb_pack_device_bytes": (_i64, [_vp]),
     "mmnb_device_alloc": (_int, [_vp, _sz, _P(_vp)]),
@@ -86,6 +103,11 @@ class DecoderConfig(ctypes.Structure):
     _fields_ = [("layers", _i64), ("hidden", _i64), ("heads", _i64), ("kv_heads", _i64),
                 ("head_dim", _i64), ("intermediate", _i64), ("vocab", _i64),
                 ("max_len", _i64), ("eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+class ConvParams(ctypes.Structure):
+    """mmnb_conv_params (include/mmnb.h)."""
+    _fields_ = [("strides", _i64 * 2), ("pads", _i64 * 4), ("dilations", _i64 * 2)]
+
 
 _lib = None
 _lock = threading.RLock()

@@ -180,20 +180,22 @@ int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *
 // padded) with its column sums; row sums of A' come from v_dot4 on the
 // operand registers.
 // ---------------------------------------------------------------------------
-__global__ void k_prep_int_b(const uint8_t *__restrict__ src, int b_signed, int64_t batch,
-                             int64_t k, int64_t n, int64_t kpad, int8_t *__restrict__ bt,
-                             int32_t *__restrict__ colsum) {
+__global__ void k_prep_int_b(const uint8_t *__restrict__ src, int b_signed, int b_trans,
+                             int64_t batch, int64_t k, int64_t n, int64_t kpad,
+                             int8_t *__restrict__ bt, int32_t *__restrict__ colsum) {
   // one thread per (batch, column)
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= batch * n) return;
   const int64_t b = idx / n, col = idx % n;
-  const uint8_t *s = src + b * k * n + col;
+  // element (b, kk, col) of B: [batch, k, n] or, transposed, [batch, n, k]
+  const uint8_t *s = b_trans ? src + (b * n + col) * k : src + b * k * n + col;
+  const int64_t ks = b_trans ? 1 : n;
   int8_t *d = bt + (b * n + col) * kpad;
   int32_t sum = 0;
   for (int64_t kk = 0; kk < kpad; kk++) {
     int v = 0;
     if (kk < k) {
-      const uint8_t raw = s[kk * n];
+      const uint8_t raw = s[kk * ks];
       v = b_signed ? (int)(int8_t)raw : (int)raw - 128;
     }
     d[kk] = (int8_t)v;
@@ -202,47 +204,49 @@ __global__ void k_prep_int_b(const uint8_t *__restrict__ src, int b_signed, int6
   colsum[idx] = sum;
 }
 
-__global__ void k_prep_int_e(int b_signed, int64_t n, const int32_t *__restrict__ bzp,
+// e = (uint8 ? 128 : 0) - b_zp for each of `cnt` columns (n, or batch*n
+// when the zero points differ per batch).
+__global__ void k_prep_int_e(int b_signed, int64_t cnt, const int32_t *__restrict__ bzp,
                              int64_t bzp_len, int32_t *__restrict__ ecol) {
   const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (col >= n) return;
+  if (col >= cnt) return;
   int32_t z = 0;
   if (bzp_len == 1) z = bzp[0];
-  else if (bzp_len == n && n != 1) z = bzp[col];
+  else if (bzp_len == cnt && cnt != 1) z = bzp[col];
   ecol[col] = (b_signed ? 0 : 128) - z;
 }
 
-int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int64_t batch,
-                      int64_t k, int64_t n, int64_t kpad, const int32_t *d_bzp,
+int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int b_trans,
+                      int64_t batch, int64_t k, int64_t n, int64_t kpad, const int32_t *d_bzp,
                       int64_t bzp_len, int8_t *d_bt, int32_t *d_colsum, int32_t *d_ecol) {
   const int threads = 256;
   const int64_t tot = batch * n;
   int rc = launch(ctx, kKernPrepIntB, k_prep_int_b, dim3((unsigned)((tot + threads - 1) / threads)),
-                  dim3(threads), 0, d_src, b_signed, batch, k, n, kpad, d_bt, d_colsum);
+                  dim3(threads), 0, d_src, b_signed, b_trans, batch, k, n, kpad, d_bt, d_colsum);
   if (rc) return rc;
-  return launch(ctx, kKernPrepIntB, k_prep_int_e, dim3((unsigned)((n + threads - 1) / threads)),
-                dim3(threads), 0, b_signed, n, d_bzp, bzp_len, d_ecol);
+  const int64_t cnt = (bzp_len == batch * n && batch > 1) ? batch * n : n;
+  return launch(ctx, kKernPrepIntB, k_prep_int_e, dim3((unsigned)((cnt + threads - 1) / threads)),
+                dim3(threads), 0, b_signed, cnt, d_bzp, bzp_len, d_ecol);
 }
 
 typedef int int4v __attribute__((ext_vector_type(4)));
 
 // Epilogue shared by both MatMulInteger kernels: completes the row sums,
-// applies the exact integer zero-point corrections and stores int32 and/or
-// the fused fp32 rescale.  16x16 i32 accumulator layout: lane l holds column
-// l%16 and rows 4*(l/16) + r, r = 0..3.
+// applies the exact integer zero-point corrections and stores what `o` asks
+// for (int32, the fused fp32 rescale, 8-bit requantisation).  16x16 i32
+// accumulator layout: lane l holds column l%16 and rows 4*(l/16) + r.
 __device__ __forceinline__ void mmi_epilogue(
     const int4v (&acc)[2][2], int (&rsum)[2], int a_signed, int64_t bz, int64_t M, int64_t K,
     int64_t N, int64_t m0, int64_t n0, int lane, const int32_t *__restrict__ colsum,
     int64_t cs_bstride, const int32_t *__restrict__ ecol, const int32_t *__restrict__ azp,
-    int64_t azp_len, int32_t *__restrict__ Y, const float *__restrict__ a_scale,
-    const float *__restrict__ b_scale, int64_t b_scale_len, float *__restrict__ Yf) {
+    int64_t azp_len, const MmiEpi &o) {
   const int r16 = lane & 15, q = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 2; t++) {
     rsum[t] += __shfl_xor(rsum[t], 16, 64);
     rsum[t] += __shfl_xor(rsum[t], 32, 64);
   }
-  const float as = Yf ? *a_scale : 0.0f;
+  const float as = o.yf ? *o.a_scale : 0.0f;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     int32_t rs[4], cm[4];
@@ -260,19 +264,36 @@ __device__ __forceinline__ void mmi_epilogue(
     for (int j = 0; j < 2; j++) {
       const int64_t col = n0 + j * 16 + r16;
       if (col >= N) continue;
-      const uint32_t e = (uint32_t)ecol[col];
+      const uint32_t e = (uint32_t)ecol[bz * o.ecol_bstride + col];
       const uint32_t cs = (uint32_t)colsum[bz * cs_bstride + col];
+      const int64_t ch = o.trans ? bz * N + col : col;  // output channel (requant mode 2)
       float sj = 0.0f;
-      if (Yf) sj = as * b_scale[b_scale_len == 1 ? 0 : col];
+      if (o.yf) sj = as * o.b_scale[o.b_scale_len == 1 ? 0 : col];
+      double mch = 0.0, bias = 0.0;
+      if (o.rq_mode == 2) {
+        mch = o.rq_mult_ch[ch];
+        if (o.rq_bias) bias = (double)o.rq_bias[ch];
+      }
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         if (row[r] >= M) continue;
         const uint32_t c = (uint32_t)cm[r];
         const uint32_t v = (uint32_t)acc[i][j][r] + e * (uint32_t)rs[r] + c * cs +
                            (uint32_t)K * c * e;
-        const int64_t o = (bz * M + row[r]) * N + col;
-        if (Y) Y[o] = (int32_t)v;
-        if (Yf) Yf[o] = (float)(int32_t)v * sj;
+        const int64_t oi = o.trans ? (bz * N + col) * M + row[r] : (bz * M + row[r]) * N + col;
+        if (o.y) o.y[oi] = (int32_t)v;
+        if (o.yf) o.yf[oi] = (float)(int32_t)v * sj;
+        if (o.yq) {
+          double x;
+          if (o.rq_mode == 1) {
+            x = (double)(float)((double)(int32_t)v * (double)o.rq_mult);
+          } else {
+            x = ((double)(int32_t)v + bias) * mch;
+          }
+          double t = rint(x) + (double)o.yzp;
+          t = t < (double)o.lo ? (double)o.lo : (t > (double)o.hi ? (double)o.hi : t);
+          o.yq[oi] = (uint8_t)(int32_t)t;
+        }
       }
     }
   }
@@ -285,9 +306,7 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
     const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
-    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, int32_t *__restrict__ Y,
-    const float *__restrict__ a_scale, const float *__restrict__ b_scale,
-    int64_t b_scale_len, float *__restrict__ Yf, int fast) {
+    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o, int fast) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t bz = blockIdx.z;
@@ -359,7 +378,7 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
   }
   mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
-               azp_len, Y, a_scale, b_scale, b_scale_len, Yf);
+               azp_len, o);
 }
 
 
@@ -380,9 +399,8 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
     const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
-    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, int32_t *__restrict__ Y,
-    const float *__restrict__ a_scale, const float *__restrict__ b_scale,
-    int64_t b_scale_len, float *__restrict__ Yf, const uint8_t *__restrict__ pad) {
+    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o,
+    const uint8_t *__restrict__ pad) {
   __shared__ uint4 sA[64 * kMmiPieces];
   __shared__ uint4 sB[64 * kMmiPieces];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -448,16 +466,17 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
     __syncthreads();
   }
   mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
-               azp_len, Y, a_scale, b_scale, b_scale_len, Yf);
+               azp_len, o);
 }
 
 int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, int a_signed,
                           int64_t a_batch, int64_t m, const int32_t *d_azp, int64_t azp_len,
-                          int32_t *d_y, const float *d_a_scale, const float *d_b_scale,
-                          int64_t b_scale_len, float *d_yf) {
+                          const MmiEpi &out) {
   const int64_t batch = a_batch > p->batch ? a_batch : p->batch;
   const int64_t k = p->k, n = p->n;
-  if (!d_y && !d_yf) return fail(MMNB_ERR_ARG, "MatMulInteger: no output");
+  if (!out.y && !out.yf && !out.yq) return fail(MMNB_ERR_ARG, "MatMulInteger: no output");
+  MmiEpi o = out;
+  o.ecol_bstride = p->ecol_bstride;
   const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
   if (fast && ctx->d_pad)
@@ -465,13 +484,13 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
                   a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                   p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad,
                   (const int32_t *)p->d_colsum, p->batch == 1 ? (int64_t)0 : n,
-                  (const int32_t *)p->d_ecol, n, d_azp, azp_len, d_y, d_a_scale, d_b_scale,
-                  b_scale_len, d_yf, (const uint8_t *)ctx->d_pad);
+                  (const int32_t *)p->d_ecol, n, d_azp, azp_len, o,
+                  (const uint8_t *)ctx->d_pad);
   return launch(ctx, kKernMmi, k_mmi_mfma, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
                 a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                 p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, (const int32_t *)p->d_colsum,
-                p->batch == 1 ? (int64_t)0 : n, (const int32_t *)p->d_ecol, n, d_azp, azp_len,
-                d_y, d_a_scale, d_b_scale, b_scale_len, d_yf, fast);
+                p->batch == 1 ? (int64_t)0 : n, (const int32_t *)p->d_ecol, n, d_azp, azp_len, o,
+                fast);
 }
 
 // ---------------------------------------------------------------------------

@@ -39,7 +39,7 @@ constexpr int kSegK = 64;        // k per 32-byte segment
 constexpr int kSegBytes = 32;
 constexpr size_t kTailPad = 1024;  // bytes of slack after every device buffer
 
-enum PackKind { kPackNBits = 1, kPackInteger = 2 };
+enum PackKind { kPackNBits = 1, kPackInteger = 2, kPackConv = 3 };
 
 struct Scratch {
   void *ptr = nullptr;
@@ -59,7 +59,7 @@ struct mmnb_ctx {
   // Device staging/scratch buffers, grown on demand and kept for reuse:
   //  0: activations in (fp32 / uint8), 1: outputs, 2: prepared activations
   //  (fp16 hi/lo), 3: small reductions, 4: misc.
-  mmnb::Scratch scratch[6];
+  mmnb::Scratch scratch[10];
   int live_packs = 0;
   // Kernel timing mode: launches go through hipExtLaunchKernelGGL with a
   // start/stop event pair taken from the dispatch itself.
@@ -99,7 +99,11 @@ struct mmnb_pack {
   int b_signed = 0;
   int8_t *d_bt = nullptr;    // [batch, n, kpad] signed bytes (uint8 B xor 0x80)
   int32_t *d_colsum = nullptr;  // [batch, n] sum_k B'
-  int32_t *d_ecol = nullptr;    // [n]  (uint8 ? 128 : 0) - b_zp[n]
+  int32_t *d_ecol = nullptr;    // [n] or [batch, n]: (uint8 ? 128 : 0) - b_zp
+  int64_t ecol_bstride = 0;     // n when the zero points differ per batch
+  // --- convolution weight (kPackConv): the MatMulInteger fields above hold
+  // w as B^T per group (batch = group, n = m / group, k = c_per_group*kh*kw)
+  int64_t conv_m = 0, conv_cg = 0, conv_kh = 0, conv_kw = 0, conv_group = 0;
 };
 
 namespace mmnb {
@@ -198,15 +202,40 @@ int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
 int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y,
                float *d_scale, int32_t *d_zp);
 
-// MatMulInteger (+ optional fused rescale).  d_azp: device int32 of length
-// azp_len (0, 1 or m).  When d_yf is non-null, y_f32 = fl32(fl32(acc) *
-// fl32(a_scale * b_scale[j])) with a_scale read from d_a_scale.
+// Output stage of the MatMulInteger kernels.  Any of y / yf / yq may be
+// set; the exact accumulator acc feeds each.
+//   y:  int32 acc.
+//   yf: fl32(fl32(acc) * fl32(a_scale * b_scale[j])), a_scale read from the
+//       device (the dynamic-quantisation chain's Cast -> Mul -> Mul).
+//   yq: 8-bit requantisation, clamp(rint(x) + yzp, lo, hi) stored as a byte:
+//       rq_mode 1: x = fl32(acc * rq_mult) (QLinearMatMul's binary32 steps);
+//       rq_mode 2: x = (acc + rq_bias[c]) * rq_mult_ch[c] in double
+//                  (QLinearConv, c = output channel).
+// Output element (batch bz, row, col) goes to (bz*M + row)*N + col, or with
+// trans to (bz*N + col)*M + row (channel-major: a convolution's output with
+// rows = positions, columns = channels of group bz, channel = bz*N + col).
+// ecol_bstride: the pack's zero-point offsets per batch (0 = shared).
+struct MmiEpi {
+  int32_t *y = nullptr;
+  float *yf = nullptr;
+  const float *a_scale = nullptr;
+  const float *b_scale = nullptr;
+  int64_t b_scale_len = 0;
+  uint8_t *yq = nullptr;
+  int rq_mode = 0;
+  float rq_mult = 0.0f;
+  const double *rq_mult_ch = nullptr;
+  const int32_t *rq_bias = nullptr;
+  int32_t yzp = 0, lo = 0, hi = 255;
+  int trans = 0;
+  int64_t ecol_bstride = 0;
+};
+
+// MatMulInteger on the device.  d_azp: device int32 of length azp_len (0, 1
+// or m).
 int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a,
                           int a_signed, int64_t a_batch, int64_t m,
-                          const int32_t *d_azp, int64_t azp_len,
-                          int32_t *d_y, const float *d_a_scale,
-                          const float *d_b_scale, int64_t b_scale_len,
-                          float *d_yf);
+                          const int32_t *d_azp, int64_t azp_len, const MmiEpi &out);
 
 // Platform calibration kernels.
 int launch_probe_empty(mmnb_ctx *ctx, int blocks);
@@ -216,7 +245,11 @@ int launch_probe_read(mmnb_ctx *ctx, const void *d_buf, size_t bytes);
 int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n,
                          int64_t k, int64_t src_col_bytes,
                          int64_t dst_col_bytes, uint8_t *d_dst);
-int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed,
+// B [batch, k, n] row-major, or [batch, n, k] with b_trans (a convolution
+// weight, output channel major).  Zero points: bzp_len 0, 1, n (per column,
+// shared by the batches) or batch*n (per column of each batch; d_ecol then
+// holds batch*n entries).
+int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int b_trans,
                       int64_t batch, int64_t k, int64_t n, int64_t kpad,
                       const int32_t *d_bzp, int64_t bzp_len, int8_t *d_bt,
                       int32_t *d_colsum, int32_t *d_ecol);

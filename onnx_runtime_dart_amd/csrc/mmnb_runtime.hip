@@ -421,7 +421,7 @@ int mmnb_pack_integer(mmnb_ctx *ctx, const void *b, int b_is_signed, int64_t b_b
   if (bzl && (e = hipMemcpyAsync(d_zp, zp.data(), (size_t)bzl * 4, hipMemcpyHostToDevice,
                                  ctx->stream)) != hipSuccess)
     return cleanup(check_hip(e, "hipMemcpyAsync(b_zp)"));
-  if ((rc = prepare_integer_b(ctx, (const uint8_t *)d_raw, p->b_signed, b_batch, k, n,
+  if ((rc = prepare_integer_b(ctx, (const uint8_t *)d_raw, p->b_signed, 0, b_batch, k, n,
                               p->kpad, (const int32_t *)d_zp, bzl, p->d_bt, p->d_colsum,
                               p->d_ecol)))
     return cleanup(rc);
@@ -461,8 +461,10 @@ int mmnb_matmul_integer_dev(mmnb_ctx *ctx, const mmnb_pack *pack, const void *d_
   if (!d_y || (!d_a && pack->k > 0)) return fail(MMNB_ERR_ARG, "MatMulInteger: null buffer");
   CtxLock lk(ctx);
   if ((rc = set_device(ctx))) return rc;
+  MmiEpi o;
+  o.y = d_y;
   return launch_matmul_integer(ctx, pack, d_a, a_is_signed ? 1 : 0, a_batch, m,
-                               d_a_zero_point, azl, d_y, nullptr, nullptr, 0, nullptr);
+                               d_a_zero_point, azl, o);
 }
 
 int mmnb_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *pack, const void *a,
@@ -499,9 +501,10 @@ int mmnb_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *pack, const void *a,
   if (azl)
     MMNB_HIP(hipMemcpyAsync(d_az, az.data(), (size_t)azl * 4, hipMemcpyHostToDevice,
                             ctx->stream));
+  MmiEpi o;
+  o.y = (int32_t *)d_y;
   if ((rc = launch_matmul_integer(ctx, pack, d_a, a_is_signed ? 1 : 0, a_batch, m,
-                                  (const int32_t *)d_az, azl, (int32_t *)d_y, nullptr,
-                                  nullptr, 0, nullptr)))
+                                  (const int32_t *)d_az, azl, o)))
     return rc;
   MMNB_HIP(hipMemcpyAsync(y, d_y, (size_t)(batch * m * n) * 4, hipMemcpyDeviceToHost,
                           ctx->stream));
@@ -527,8 +530,13 @@ int mmnb_dynamic_matmul_dev(mmnb_ctx *ctx, const mmnb_pack *pack, const float *d
   CtxLock lk(ctx);
   if ((rc = set_device(ctx))) return rc;
   if ((rc = launch_dql(ctx, d_x, m * pack->k, d_a_q, d_a_scale, d_a_zero_point))) return rc;
-  return launch_matmul_integer(ctx, pack, d_a_q, 0, 1, m, d_a_zero_point, 1, d_acc,
-                               d_a_scale, d_b_scale, b_scale_len, d_y);
+  MmiEpi o;
+  o.y = d_acc;
+  o.yf = d_y;
+  o.a_scale = d_a_scale;
+  o.b_scale = d_b_scale;
+  o.b_scale_len = b_scale_len;
+  return launch_matmul_integer(ctx, pack, d_a_q, 0, 1, m, d_a_zero_point, 1, o);
 }
 
 // ---------------------------------------------------------------------- packs

@@ -8,8 +8,11 @@ as the Dart functions they replace:
 * ``op_matmul_integer``  <- ``opMatMulInteger`` (lib/src/onnx_qlinear_ops.dart:30-79)
 * ``op_dynamic_quantize_linear`` <- ``opDynamicQuantizeLinear``
   (lib/src/onnx_ops.dart:2556-2583)
-* ``dispatch``           <- the three ``_dispatch`` arms
-  (lib/src/onnx_graph.dart:1561-1567, :1584-1596)
+* ``op_qlinear_matmul``  <- ``opQLinearMatMul`` (lib/src/onnx_qlinear_ops.dart:83-106)
+* ``op_conv_integer``    <- ``opConvInteger`` (lib/src/onnx_qlinear_ops.dart:235-267)
+* ``op_qlinear_conv``    <- ``opQLinearConv`` (lib/src/onnx_qlinear_ops.dart:270-308)
+* ``dispatch``           <- the ``_dispatch`` arms of these operators
+  (lib/src/onnx_graph.dart:1561-1609)
 
 Tensors are numpy arrays (shape + dtype + row-major data, like the Dart
 ``Tensor``).  Exceptions: ``NotImplementedError`` where the reference throws
@@ -212,12 +215,169 @@ def op_matmul_integer(a, b, a_zp, b_zp, ctx=None):
     return y.astype(np.int64).reshape(list(batch_shape) + [m, n])
 
 
+# ------------------------------------------------------------ QLinearMatMul
+
+def _scalar_f(t, what):
+    arr = np.asarray(t, dtype=np.float32).ravel()
+    if arr.size != 1:
+        raise NotImplementedError(f"{what}: only per-tensor scales supported")
+    return float(arr[0])
+
+
+def op_qlinear_matmul(a, a_scale, a_zp, b, b_scale, b_zp, y_scale, y_zp, *, lo, hi, ctx=None):
+    """MatMulInteger + requantisation with ``fl32(fl32(aS*bS)/yS)``, saturating
+    to ``[lo, hi]`` (opQLinearMatMul, onnx_qlinear_ops.dart:83-106).  Returns
+    int64 like the reference."""
+    if (np.asarray(a_scale).size != 1 or np.asarray(b_scale).size != 1
+            or np.asarray(y_scale).size != 1):
+        raise NotImplementedError("QLinearMatMul: only per-tensor scales supported")
+    if (lo, hi) not in ((-128, 127), (0, 255)):
+        raise ValueError("QLinearMatMul: output range must be int8 or uint8")
+    ctx = _ctx(ctx)
+    a = np.ascontiguousarray(a)
+    if a.dtype not in (np.uint8, np.int8):
+        raise NotImplementedError(f"QLinearMatMul: A must be uint8 or int8, got {a.dtype}")
+    b_arr = np.asarray(b)
+    if a.ndim < 2 or b_arr.ndim < 2:
+        raise ValueError("MatMulInteger: operands must have rank >= 2")
+    m, k = a.shape[-2], a.shape[-1]
+    if b_arr.shape[-2] != k:
+        raise ValueError("MatMulInteger inner dim mismatch")
+    n = b_arr.shape[-1]
+    keys = [b] + ([b_zp] if b_zp is not None and not np.isscalar(b_zp) else [])
+    extra = (ctx.device,) + ((int(b_zp),) if b_zp is not None and np.isscalar(b_zp) else ())
+    pack = _CACHE.get(keys, extra, lambda: pack_integer(b, b_zp, ctx))
+    a_batch = a.size // (m * k) if m * k else 1
+    batch = max(a_batch, pack.batch)
+    z = _zp_array(a_zp)
+    yz = 0 if y_zp is None else int(np.asarray(y_zp).ravel()[0])
+    signed = lo < 0
+    y = np.empty(batch * m * n, dtype=np.int8 if signed else np.uint8)
+    if m and n:
+        check(ctx.lib.mmnb_qlinear_matmul(
+            ctx.handle, pack.handle, ptr(a.view(np.uint8)), int(a.dtype == np.int8), a_batch, m,
+            ptr(z), 0 if z is None else z.size, _scalar_f(a_scale, "QLinearMatMul"),
+            _scalar_f(b_scale, "QLinearMatMul"), _scalar_f(y_scale, "QLinearMatMul"), yz,
+            int(signed), ptr(y)))
+    batch_shape = a.shape[:-2] if a_batch >= pack.batch else pack.batch_shape
+    return y.astype(np.int64).reshape(list(batch_shape) + [m, n])
+
+
+# -------------------------------------------------------------- convolutions
+
+def pack_conv(w, w_zp, group, ctx=None):
+    """Upload a convolution weight ``[M, C/group, kh, kw]`` (uint8/int8)."""
+    ctx = _ctx(ctx)
+    w = np.ascontiguousarray(w)
+    if w.dtype not in (np.uint8, np.int8):
+        raise NotImplementedError(f"conv: weight must be uint8 or int8, got {w.dtype}")
+    if w.ndim != 4:
+        raise ValueError("conv: weight must be [M, C/group, kh, kw]")
+    z = _zp_array(w_zp)
+    h = ctypes.c_void_p()
+    check(ctx.lib.mmnb_pack_conv(ctx.handle, ptr(w.view(np.uint8)), int(w.dtype == np.int8),
+                                 *[int(d) for d in w.shape], int(group), ptr(z),
+                                 0 if z is None else z.size, ctypes.byref(h)))
+    return Pack(ctx, h, "conv", m=int(w.shape[0]))
+
+
+def _conv_prep(x, w, w_zp, strides, pads, dilations, group, ctx):
+    """The reference's 1-D -> 2-D reshape (onnx_qlinear_ops.dart:238-252) and
+    defaults; returns (x4, w4, params, squeeze, pack)."""
+    x = np.ascontiguousarray(x)
+    w_arr = np.asarray(w)
+    if x.dtype not in (np.uint8, np.int8):
+        raise NotImplementedError(f"conv: input must be uint8 or int8, got {x.dtype}")
+    squeeze = False
+    if x.ndim == 3:
+        x = x.reshape(x.shape[0], x.shape[1], 1, x.shape[2])
+        if w_arr.ndim == 3:
+            w_arr = w_arr.reshape(w_arr.shape[0], w_arr.shape[1], 1, w_arr.shape[2])
+        strides = [1, (strides[0] if strides else 1)]
+        pads = None if pads is None else [0, pads[0], 0, pads[1]]
+        dilations = [1, (dilations[0] if dilations else 1)]
+        squeeze = True
+    if x.ndim != 4 or w_arr.ndim != 4:
+        raise ValueError("ConvInteger implemented for 1-D/2-D convs")
+    prm = _lib.ConvParams()
+    s = list(strides) if strides else [1, 1]
+    p = list(pads) if pads else [0, 0, 0, 0]
+    d = list(dilations) if dilations else [1, 1]
+    for i in range(2):
+        prm.strides[i] = int(s[i])
+        prm.dilations[i] = int(d[i])
+    for i in range(4):
+        prm.pads[i] = int(p[i])
+    keys = [w] + ([w_zp] if w_zp is not None and not np.isscalar(w_zp) else [])
+    extra = (ctx.device, int(group), "conv") + \
+        ((int(w_zp),) if w_zp is not None and np.isscalar(w_zp) else ())
+    pack = _CACHE.get(keys, extra, lambda: pack_conv(w_arr, w_zp, group, ctx))
+    return x, prm, squeeze, pack
+
+
+def _conv_out_shape(ctx, pack, x, prm):
+    oh, ow = ctypes.c_int64(), ctypes.c_int64()
+    check(ctx.lib.mmnb_conv_output_shape(pack.handle, *[int(v) for v in x.shape],
+                                         ctypes.byref(prm), ctypes.byref(oh), ctypes.byref(ow)))
+    return oh.value, ow.value
+
+
+def op_conv_integer(x, w, x_zp, w_zp, *, strides=None, pads=None, dilations=None, group=1,
+                    ctx=None):
+    """``acc[n, m, oy, ox] = sum (x - xZp)(w - wZp[m])`` exact, int64 out like
+    opConvInteger (onnx_qlinear_ops.dart:235-267); 1-D convs run as 2-D."""
+    ctx = _ctx(ctx)
+    x4, prm, squeeze, pack = _conv_prep(x, w, w_zp, strides, pads, dilations, group, ctx)
+    oh, ow = _conv_out_shape(ctx, pack, x4, prm)
+    xz = 0 if x_zp is None else int(np.asarray(x_zp).ravel()[0])
+    n = x4.shape[0]
+    y = np.empty(n * pack.m * oh * ow, dtype=np.int32)
+    if y.size:
+        check(ctx.lib.mmnb_conv_integer(ctx.handle, pack.handle, ptr(x4.view(np.uint8)),
+                                        int(x4.dtype == np.int8), *[int(v) for v in x4.shape],
+                                        xz, ctypes.byref(prm), ptr(y)))
+    y = y.astype(np.int64).reshape(n, pack.m, oh, ow)
+    return y.reshape(n, pack.m, ow) if squeeze else y
+
+
+def op_qlinear_conv(x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, bias, *, strides=None,
+                    pads=None, dilations=None, group=1, lo, hi, ctx=None):
+    """Integer conv + int32 bias + per-channel requantisation in double
+    (opQLinearConv, onnx_qlinear_ops.dart:270-308); 2-D only."""
+    if np.asarray(x).ndim != 4:
+        raise ValueError("QLinearConv implemented for 2-D convs")
+    if (lo, hi) not in ((-128, 127), (0, 255)):
+        raise ValueError("QLinearConv: output range must be int8 or uint8")
+    ctx = _ctx(ctx)
+    x4, prm, _, pack = _conv_prep(x, w, w_zp, strides, pads, dilations, group, ctx)
+    oh, ow = _conv_out_shape(ctx, pack, x4, prm)
+    xz = 0 if x_zp is None else int(np.asarray(x_zp).ravel()[0])
+    yz = 0 if y_zp is None else int(np.asarray(y_zp).ravel()[0])
+    ws = np.ascontiguousarray(np.asarray(w_scale, dtype=np.float32).ravel())
+    bi = None if bias is None else np.ascontiguousarray(np.asarray(bias).astype(np.int32).ravel())
+    if bi is not None and bi.size != pack.m:
+        raise ValueError("QLinearConv: bias must have M values")
+    signed = lo < 0
+    n = x4.shape[0]
+    y = np.empty(n * pack.m * oh * ow, dtype=np.int8 if signed else np.uint8)
+    if y.size:
+        check(ctx.lib.mmnb_qlinear_conv(
+            ctx.handle, pack.handle, ptr(x4.view(np.uint8)), int(x4.dtype == np.int8),
+            *[int(v) for v in x4.shape], xz, float(np.asarray(x_scale, np.float32).ravel()[0]),
+            ptr(ws), ws.size, float(np.asarray(y_scale, np.float32).ravel()[0]), yz, int(signed),
+            ptr(bi), ctypes.byref(prm), ptr(y)))
+    return y.astype(np.int64).reshape(n, pack.m, oh, ow)
+
+
 # --------------------------------------------------------- dispatch arms
 
 def dispatch(op_type, ins, attrs):
-    """The ``_dispatch`` arms for the three operators
-    (onnx_graph.dart:1561-1567, :1584-1596).  ``ins`` lists the node's
-    positional inputs (None for an empty name); returns the output list."""
+    """The ``_dispatch`` arms for the quantized operators
+    (onnx_graph.dart:1561-1609).  ``ins`` lists the node's positional inputs
+    (None for an empty name); returns the output list.  The output range of
+    QLinearMatMul / QLinearConv follows the y zero point's type (int8 ->
+    [-128, 127], else [0, 255]; the reference reads the initializer's
+    element type, :1578, :1598)."""
     def need(i):
         if i >= len(ins) or ins[i] is None:
             raise ValueError(f"{op_type}: missing input {i}")
@@ -234,6 +394,27 @@ def dispatch(op_type, ins, attrs):
         return [op_matmul_nbits(need(0), need(1), need(2), ins[3] if len(ins) > 3 else None,
                                 k=attrs["K"], n=attrs["N"], bits=attrs.get("bits", 4),
                                 block_size=attrs["block_size"])]
+    def rng8(i):
+        z = ins[i] if len(ins) > i else None
+        return (-128, 127) if z is not None and np.asarray(z).dtype == np.int8 else (0, 255)
+
+    def opt(i):
+        return ins[i] if len(ins) > i else None
+
+    if op_type == "ConvInteger":
+        return [op_conv_integer(need(0), need(1), opt(2), opt(3), strides=attrs.get("strides"),
+                                pads=attrs.get("pads"), dilations=attrs.get("dilations"),
+                                group=attrs.get("group", 1))]
+    if op_type == "QLinearMatMul":
+        lo, hi = rng8(7)
+        return [op_qlinear_matmul(need(0), need(1), opt(2), need(3), need(4), opt(5), need(6),
+                                  opt(7), lo=lo, hi=hi)]
+    if op_type == "QLinearConv":
+        lo, hi = rng8(7)
+        return [op_qlinear_conv(need(0), need(1), opt(2), need(3), need(4), opt(5), need(6),
+                                opt(7), opt(8), strides=attrs.get("strides"),
+                                pads=attrs.get("pads"), dilations=attrs.get("dilations"),
+                                group=attrs.get("group", 1), lo=lo, hi=hi)]
     raise NotImplementedError(f"Unsupported op: {op_type}")
 
 

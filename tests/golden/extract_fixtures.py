@@ -38,6 +38,13 @@ CASES = [
     "gqa_kvcache",
     "gqa_kvcache_rotary",
     "gqa_kvcache_bias",
+    # quantized ops adjacent to the path (QLinearMatMul, ConvInteger 2-D and
+    # 1-D, QLinearConv per-tensor and per-channel with bias)
+    "qlinearmatmul",
+    "convinteger",
+    "convinteger_1d",
+    "qlinearconv_pertensor",
+    "qlinearconv_perchannel_bias",
 ]
 
 # ONNX TensorProto.DataType codes used by these fixtures.
@@ -130,7 +137,7 @@ def decode_tensor(buf):
 
 def decode_attribute(buf):
     """AttributeProto: name=1, f=2, i=3, ints=8, type=20."""
-    name, value = "", None
+    name, value, ints = "", None, None
     for fno, wt, val in fields(buf):
         if fno == 1:
             name = val.decode()
@@ -138,7 +145,10 @@ def decode_attribute(buf):
             value = val - (1 << 64) if val >= (1 << 63) else val
         elif fno == 2:
             value = struct.unpack("<f", val)[0]
-    return name, value
+        elif fno == 8:  # repeated int64, packed or not
+            ints = (ints or []) + [v - (1 << 64) if v >= (1 << 63) else v
+                                   for v in _packed_varints(val, wt)]
+    return name, (ints if ints is not None else value)
 
 
 def decode_node(buf):

@@ -96,4 +96,9 @@ def test_dispatch_rejects_bits_other_than_4_before_any_device_call():
 
 def test_unknown_op_is_unsupported():
     with pytest.raises(NotImplementedError):
+        ops.dispatch("QLinearAdd", [], {})
+
+
+def test_missing_required_input_is_an_argument_error():
+    with pytest.raises(ValueError):
         ops.dispatch("QLinearConv", [], {})
