@@ -108,6 +108,44 @@ int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
 int mmnb_matmul_nbits_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
                           const float *d_a, int64_t m, float *d_y);
 
+/* ---- MatMulNBits beyond the reference's 4-bit form -----------------------
+ * The reference accepts bits = 4, uint8 zero points in its flat layout and
+ * fp32 scales, and throws UnsupportedError for g_idx / bias inputs
+ * (onnx_graph.dart:1585-1588, onnx_qlinear_ops.dart:117-119).  ORT-exported
+ * models also use bits = 8, act-order g_idx, a bias, floating-point zero
+ * points, fp16 scales / bias (widened exactly, as the reference's loader
+ * widens fp16 initializers, onnx_proto_loader.dart:29-47, :217-227) and the
+ * per-column zero-point layout [N, ceil(n_blocks * bits / 8)].  This entry
+ * point packs all of them for mmnb_matmul_nbits / _dev (same semantics:
+ * W[k, n] = (q - zp[n, g]) * scale[n, g], g = g_idx[k] or k / block_size,
+ * y = A W + bias).  No reference counterpart: it extends the drop-in to
+ * what the reference rejects. */
+#define MMNB_DT_F32 1
+#define MMNB_DT_U8 2
+#define MMNB_DT_F16 10
+#define MMNB_ZP_FLAT 0        /* nibble i = n * n_blocks + blk (the reference, :133-137) */
+#define MMNB_ZP_PER_COLUMN 1  /* byte row of ceil(n_blocks / 2) per column (ORT) */
+
+typedef struct mmnb_nbits_desc {
+  int64_t k, n, bits, block_size;      /* bits 4 or 8 */
+  const uint8_t *b_q;                  /* [n, ceil(k/bs), bs*bits/8] */
+  int64_t b_q_len;
+  const void *scales;                  /* [n * ceil(k/bs)] */
+  int64_t scales_len;
+  int scales_type;                     /* MMNB_DT_F32 | MMNB_DT_F16 */
+  const void *zero_points;             /* NULL: 8 (bits 4) / 128 (bits 8) */
+  int64_t zero_points_len;
+  int zero_points_type;                /* MMNB_DT_U8 (packed by bits) | F32 | F16 */
+  int zero_points_layout;              /* MMNB_ZP_FLAT | MMNB_ZP_PER_COLUMN (4-bit U8) */
+  const int32_t *g_idx;                /* NULL or [k]; groups of block_size rows */
+  int64_t g_idx_len;
+  const void *bias;                    /* NULL or [n] */
+  int64_t bias_len;
+  int bias_type;                       /* MMNB_DT_F32 | MMNB_DT_F16 */
+} mmnb_nbits_desc;
+
+int mmnb_pack_nbits_ex(mmnb_ctx *ctx, const mmnb_nbits_desc *desc, mmnb_pack **out);
+
 /* ---- DynamicQuantizeLinear --------------------------------------------- */
 
 /* y = saturate(roundEven(x / scale) + zp), scale = fl32((max(0,x) -

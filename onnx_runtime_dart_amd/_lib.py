@@ -42,6 +42,7 @@ SIGNATURES = {
     "mmnb_matmul_integer_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, _vp]),
     "mmnb_dynamic_matmul_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
                                        _vp, _vp]),
+    "mmnb_pack_nbits_ex": (_int, [_vp, _vp, _P(_vp)]),
     "mmnb_qlinear_matmul": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, ctypes.c_float,
                                    ctypes.c_float, ctypes.c_float, _i64, _int, _vp]),
     "mmnb_qlinear_matmul_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64,
@@ -103,6 +104,21 @@ class DecoderConfig(ctypes.Structure):
     _fields_ = [("layers", _i64), ("hidden", _i64), ("heads", _i64), ("kv_heads", _i64),
                 ("head_dim", _i64), ("intermediate", _i64), ("vocab", _i64),
                 ("max_len", _i64), ("eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+DT_F32, DT_U8, DT_F16 = 1, 2, 10
+ZP_FLAT, ZP_PER_COLUMN = 0, 1
+
+
+class NBitsDesc(ctypes.Structure):
+    """mmnb_nbits_desc (include/mmnb.h)."""
+    _fields_ = [("k", _i64), ("n", _i64), ("bits", _i64), ("block_size", _i64),
+                ("b_q", _vp), ("b_q_len", _i64),
+                ("scales", _vp), ("scales_len", _i64), ("scales_type", _int),
+                ("zero_points", _vp), ("zero_points_len", _i64), ("zero_points_type", _int),
+                ("zero_points_layout", _int),
+                ("g_idx", _vp), ("g_idx_len", _i64),
+                ("bias", _vp), ("bias_len", _i64), ("bias_type", _int)]
+
 
 class ConvParams(ctypes.Structure):
     """mmnb_conv_params (include/mmnb.h)."""

@@ -841,7 +841,7 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
     return fail(MMNB_ERR_UNSUPPORTED,
                 "decoder: needs head_dim <= 128 (a multiple of 32) and hidden, heads*head_dim, "
                 "intermediate multiples of 64 and <= 4096");
-  if (lm_head->kind != kPackNBits || lm_head->k != c.hidden || lm_head->n != c.vocab ||
+  if (lm_head->kind != kPackNBits || lm_head->ext || lm_head->k != c.hidden || lm_head->n != c.vocab ||
       lm_head->ctx != ctx)
     return fail(MMNB_ERR_ARG, "decoder: lm_head pack shape");
   CtxLock lk(ctx);
@@ -917,7 +917,7 @@ int mmnb_decoder_set_layer(mmnb_decoder *d, int64_t layer, const float *ln1, con
   const int64_t H = c.hidden, hd = c.head_dim, nh = c.heads, kvh = c.kv_heads,
                 I = c.intermediate;
   auto ok = [&](const mmnb_pack *p, int64_t k, int64_t n) {
-    return p->kind == kPackNBits && p->ctx == d->ctx && p->k == k && p->n == n;
+    return p->kind == kPackNBits && !p->ext && p->ctx == d->ctx && p->k == k && p->n == n;
   };
   if (!ok(qkv, H, (nh + 2 * kvh) * hd) || !ok(o, nh * hd, H) || !ok(gate_up, H, 2 * I) ||
       !ok(down, I, H))

@@ -93,6 +93,18 @@ struct mmnb_pack {
   float *d_scales = nullptr;
   uint8_t *d_zp = nullptr;  // packed uint4; 0x88 filler when the op has none
   bool has_zp = false;
+  // --- MatMulNBits beyond the reference's 4-bit form (mmnb_pack_nbits_ex):
+  // the kernels run on a 4-bit "virtual" weight of k rows (k, n_blocks, d_w,
+  // d_scales, d_zp above); A is first gathered into [m, k64] when d_asrc is
+  // set, and afterwards y += bias[n] + sum_b corr[b][n] * asum[m][b] with
+  // asum the block sums (block `block`) of the (gathered) A over corr_nb
+  // blocks.
+  bool ext = false;
+  int64_t k_in = 0;           // the operator's K (A's last dimension)
+  int32_t *d_asrc = nullptr;  // [k] column of A feeding each virtual row, -1 = zero
+  float *d_corr = nullptr;    // [corr_nb, n]
+  int64_t corr_nb = 0;
+  float *d_bias = nullptr;    // [n]
   // --- MatMulInteger
   int64_t batch = 0;
   int64_t kpad = 0;          // k padded to a multiple of 64
@@ -192,6 +204,18 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
                     const float *norm_gamma, float eps, int epi, const float *resid,
                     float *d_y, unsigned long long *d_argmax);
 int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n);
+
+// Builds a 4-bit MatMulNBits pack (lock held): b_q [n, ceil(k/bs), bs/2]
+// bytes, scales fp32 [n * ceil(k/bs)], zp packed uint4 with the flat index
+// (or null: every byte zp_fill).
+int pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales,
+                    const uint8_t *zp, int zp_fill, int64_t k, int64_t n, int64_t bs,
+                    mmnb_pack **out);
+
+// MatMulNBits for any pack (plain or extended): gathers A, runs the kernels
+// and the correction pass as the pack requires.  lda = row stride of A.
+int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
+                     int64_t m, float *d_y);
 
 // Kernel launchers (return MMNB_OK or an error code) -------------------------
 // MatMulNBits: y[m, n] = a[m, k] * W;  lda = row stride of a (elements).

@@ -173,6 +173,70 @@ int mmnb_device_info(mmnb_ctx *ctx, char *name, size_t name_len,
 
 // ---------------------------------------------------------------- MatMulNBits
 
+}  // extern "C"
+
+int mmnb::pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales,
+                    const uint8_t *zero_points, int zp_fill, int64_t k, int64_t n,
+                    int64_t block_size, mmnb_pack **out) {
+  const int64_t nb = (k + block_size - 1) / block_size;
+  const int64_t src_col = nb * (block_size / 2);
+  const int64_t zp_need = (n * nb + 1) / 2;
+  int rc;
+  mmnb_pack *p = new (std::nothrow) mmnb_pack();
+  if (!p) return fail(MMNB_ERR_OOM, "out of host memory");
+  p->ctx = ctx;
+  p->kind = kPackNBits;
+  p->k = k;
+  p->n = n;
+  p->block = block_size;
+  p->n_blocks = nb;
+  int64_t kp = nb * block_size;
+  p->k64 = (kp + kSegK - 1) / kSegK * kSegK;
+  p->col_bytes = p->k64 / 2;
+  auto cleanup = [&](int code) {
+    if (p->d_w) (void)hipFree(p->d_w);
+    if (p->d_scales) (void)hipFree(p->d_scales);
+    if (p->d_zp) (void)hipFree(p->d_zp);
+    delete p;
+    return code;
+  };
+  const size_t wbytes = (size_t)(n * p->col_bytes);
+  if ((rc = device_alloc(wbytes, (void **)&p->d_w))) return cleanup(rc);
+  if ((rc = device_alloc((size_t)(n * nb) * 4, (void **)&p->d_scales))) return cleanup(rc);
+  p->has_zp = zero_points != nullptr || zp_fill != 0x88;
+  if ((rc = device_alloc((size_t)zp_need, (void **)&p->d_zp))) return cleanup(rc);
+  // Upload the raw B into scratch, repack on the device.
+  void *d_raw = nullptr;
+  if ((rc = scratch_get(ctx, 4, (size_t)(n * src_col), &d_raw))) return cleanup(rc);
+  hipError_t e;
+  if ((e = hipMemcpyAsync(d_raw, b_q, (size_t)(n * src_col), hipMemcpyHostToDevice,
+                          ctx->stream)) != hipSuccess)
+    return cleanup(check_hip(e, "hipMemcpyAsync(B)"));
+  if ((rc = repack_nbits_weights(ctx, (const uint8_t *)d_raw, n, k, src_col, p->col_bytes,
+                                 p->d_w)))
+    return cleanup(rc);
+  if ((e = hipMemcpyAsync(p->d_scales, scales, (size_t)(n * nb) * 4,
+                          hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+    return cleanup(check_hip(e, "hipMemcpyAsync(scales)"));
+  if (zero_points) {
+    if ((e = hipMemcpyAsync(p->d_zp, zero_points, (size_t)zp_need, hipMemcpyHostToDevice,
+                            ctx->stream)) != hipSuccess)
+      return cleanup(check_hip(e, "hipMemcpyAsync(zero_points)"));
+  } else if ((e = hipMemsetAsync(p->d_zp, zp_fill, (size_t)zp_need, ctx->stream)) !=
+             hipSuccess) {
+    return cleanup(check_hip(e, "hipMemsetAsync(zero_points)"));
+  }
+  if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
+    return cleanup(check_hip(e, "hipStreamSynchronize(pack)"));
+  p->bytes = (int64_t)wbytes + n * nb * 4 + zp_need;
+  p->k_in = k;
+  ctx->live_packs++;
+  *out = p;
+  return MMNB_OK;
+}
+
+extern "C" {
+
 int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
                     const float *scales, int64_t scales_len,
                     const uint8_t *zero_points, int64_t zero_points_len,
@@ -207,55 +271,7 @@ int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
   CtxLock lk(ctx);
   int rc = set_device(ctx);
   if (rc) return rc;
-  mmnb_pack *p = new (std::nothrow) mmnb_pack();
-  if (!p) return fail(MMNB_ERR_OOM, "out of host memory");
-  p->ctx = ctx;
-  p->kind = kPackNBits;
-  p->k = k;
-  p->n = n;
-  p->block = block_size;
-  p->n_blocks = nb;
-  int64_t kp = nb * block_size;
-  p->k64 = (kp + kSegK - 1) / kSegK * kSegK;
-  p->col_bytes = p->k64 / 2;
-  auto cleanup = [&](int code) {
-    if (p->d_w) (void)hipFree(p->d_w);
-    if (p->d_scales) (void)hipFree(p->d_scales);
-    if (p->d_zp) (void)hipFree(p->d_zp);
-    delete p;
-    return code;
-  };
-  const size_t wbytes = (size_t)(n * p->col_bytes);
-  if ((rc = device_alloc(wbytes, (void **)&p->d_w))) return cleanup(rc);
-  if ((rc = device_alloc((size_t)(n * nb) * 4, (void **)&p->d_scales))) return cleanup(rc);
-  p->has_zp = zero_points != nullptr;
-  if ((rc = device_alloc((size_t)zp_need, (void **)&p->d_zp))) return cleanup(rc);
-  // Upload the raw B into scratch, repack on the device.
-  void *d_raw = nullptr;
-  if ((rc = scratch_get(ctx, 4, (size_t)(n * src_col), &d_raw))) return cleanup(rc);
-  hipError_t e;
-  if ((e = hipMemcpyAsync(d_raw, b_q, (size_t)(n * src_col), hipMemcpyHostToDevice,
-                          ctx->stream)) != hipSuccess)
-    return cleanup(check_hip(e, "hipMemcpyAsync(B)"));
-  if ((rc = repack_nbits_weights(ctx, (const uint8_t *)d_raw, n, k, src_col, p->col_bytes,
-                                 p->d_w)))
-    return cleanup(rc);
-  if ((e = hipMemcpyAsync(p->d_scales, scales, (size_t)(n * nb) * 4,
-                          hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
-    return cleanup(check_hip(e, "hipMemcpyAsync(scales)"));
-  if (zero_points) {
-    if ((e = hipMemcpyAsync(p->d_zp, zero_points, (size_t)zp_need, hipMemcpyHostToDevice,
-                            ctx->stream)) != hipSuccess)
-      return cleanup(check_hip(e, "hipMemcpyAsync(zero_points)"));
-  } else if ((e = hipMemsetAsync(p->d_zp, 0x88, (size_t)zp_need, ctx->stream)) != hipSuccess) {
-    return cleanup(check_hip(e, "hipMemsetAsync(zero_points)"));
-  }
-  if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
-    return cleanup(check_hip(e, "hipStreamSynchronize(pack)"));
-  p->bytes = (int64_t)wbytes + n * nb * 4 + zp_need;
-  ctx->live_packs++;
-  *out = p;
-  return MMNB_OK;
+  return pack_nbits_core(ctx, b_q, scales, zero_points, 0x88, k, n, block_size, out);
 }
 
 static int check_nbits_pack(const mmnb_ctx *ctx, const mmnb_pack *p) {
@@ -275,7 +291,7 @@ int mmnb_matmul_nbits_dev(mmnb_ctx *ctx, const mmnb_pack *pack, const float *d_a
   if (!d_a || !d_y) return fail(MMNB_ERR_ARG, "MatMulNBits: null buffer");
   CtxLock lk(ctx);
   if ((rc = set_device(ctx))) return rc;
-  return launch_matmul_nbits(ctx, pack, d_a, pack->k, m, d_y);
+  return run_matmul_nbits(ctx, pack, d_a, pack->k_in, m, d_y);
 }
 
 int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
@@ -289,10 +305,10 @@ int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
   if (!a || !y) return fail(MMNB_ERR_ARG, "MatMulNBits: null buffer");
   CtxLock lk(ctx);
   if ((rc = set_device(ctx))) return rc;
-  const int64_t k = pack->k, n = pack->n;
+  const int64_t k = pack->k_in, n = pack->n;
   // Stage A with rows padded to k64 (zero tail) so the kernels take their
-  // aligned full-segment path.
-  const int64_t lda = pack->k64;
+  // aligned full-segment path (an extended pack gathers A itself).
+  const int64_t lda = pack->ext ? k : pack->k64;
   void *d_a = nullptr, *d_y = nullptr;
   if ((rc = scratch_get(ctx, 0, (size_t)(m * lda) * 4, &d_a))) return rc;
   if ((rc = scratch_get(ctx, 1, (size_t)(m * n) * 4, &d_y))) return rc;
@@ -304,7 +320,7 @@ int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
     MMNB_HIP(hipMemcpyAsync(d_a, a, (size_t)(m * k) * 4, hipMemcpyHostToDevice,
                             ctx->stream));
   }
-  if ((rc = launch_matmul_nbits(ctx, pack, (const float *)d_a, lda, m, (float *)d_y)))
+  if ((rc = run_matmul_nbits(ctx, pack, (const float *)d_a, lda, m, (float *)d_y)))
     return rc;
   MMNB_HIP(hipMemcpyAsync(y, d_y, (size_t)(m * n) * 4, hipMemcpyDeviceToHost,
                           ctx->stream));
@@ -554,6 +570,9 @@ int mmnb_pack_free(mmnb_pack *p) {
     if (p->d_bt) (void)hipFree(p->d_bt);
     if (p->d_colsum) (void)hipFree(p->d_colsum);
     if (p->d_ecol) (void)hipFree(p->d_ecol);
+    if (p->d_asrc) (void)hipFree(p->d_asrc);
+    if (p->d_corr) (void)hipFree(p->d_corr);
+    if (p->d_bias) (void)hipFree(p->d_bias);
     ctx->live_packs--;
   }
   delete p;

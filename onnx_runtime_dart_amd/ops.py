@@ -145,6 +145,80 @@ def op_matmul_nbits(a, b_q, scales, zero_points, *, k, n, bits, block_size, ctx=
     return y.reshape(list(af.shape[:-1]) + [n])
 
 
+# ----------------------------------- MatMulNBits as ORT-exported models use it
+
+_FLOAT_TYPES = {np.dtype(np.float32): _lib.DT_F32, np.dtype(np.float16): _lib.DT_F16}
+
+
+def _float_arg(x, what):
+    arr = np.ascontiguousarray(x)
+    if arr.dtype not in _FLOAT_TYPES:
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+    return arr, _FLOAT_TYPES[arr.dtype]
+
+
+def pack_nbits_ex(b_q, scales, zero_points=None, g_idx=None, bias=None, *, k, n, bits,
+                  block_size, ctx=None):
+    """Upload a MatMulNBits weight with the inputs and types ORT exports use
+    and the reference rejects (onnx_graph.dart:1585-1588): bits 4 or 8,
+    uint8 zero points in the flat layout (1-D) or per column ([N, bytes] 2-D),
+    float / fp16 zero points, fp16 scales, g_idx [K] and bias [N]."""
+    ctx = _ctx(ctx)
+    b = np.ascontiguousarray(b_q)
+    if b.dtype != np.uint8:
+        b = np.ascontiguousarray(np.asarray(b, dtype=np.int64).astype(np.uint8))
+    s, st = _float_arg(scales, "scales")
+    d = _lib.NBitsDesc()
+    d.k, d.n, d.bits, d.block_size = int(k), int(n), int(bits), int(block_size)
+    d.b_q, d.b_q_len = ptr(b), b.size
+    d.scales, d.scales_len, d.scales_type = ptr(s), s.size, st
+    keep = [b, s]
+    if zero_points is not None:
+        z = np.ascontiguousarray(zero_points)
+        if z.dtype == np.uint8:
+            d.zero_points_type = _lib.DT_U8
+            d.zero_points_layout = _lib.ZP_PER_COLUMN if z.ndim == 2 else _lib.ZP_FLAT
+        else:
+            z, d.zero_points_type = _float_arg(z, "zero_points")
+        d.zero_points, d.zero_points_len = ptr(z), z.size
+        keep.append(z)
+    if g_idx is not None:
+        gi = np.ascontiguousarray(np.asarray(g_idx).astype(np.int32).ravel())
+        d.g_idx, d.g_idx_len = ptr(gi), gi.size
+        keep.append(gi)
+    if bias is not None:
+        bb, d.bias_type = _float_arg(np.asarray(bias).ravel(), "bias")
+        d.bias, d.bias_len = ptr(bb), bb.size
+        keep.append(bb)
+    h = ctypes.c_void_p()
+    check(ctx.lib.mmnb_pack_nbits_ex(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
+    return Pack(ctx, h, "nbits", k=int(k), n=int(n), block=int(block_size))
+
+
+def op_matmul_nbits_ex(a, b_q, scales, zero_points=None, g_idx=None, bias=None, *, k, n,
+                       bits, block_size, ctx=None):
+    """MatMulNBits with ORT's full input list (A, B, scales, zero_points,
+    g_idx, bias): ``W[k, n] = (q - zp[n, g]) * scale[n, g]`` with
+    ``g = g_idx[k]`` (or ``k / block_size``), ``y = A W + bias``."""
+    if bits not in (4, 8):
+        raise NotImplementedError(f"MatMulNBits: bits must be 4 or 8, got {bits}")
+    ctx = _ctx(ctx)
+    keys = [b_q, scales] + [t for t in (zero_points, g_idx, bias) if t is not None]
+    extra = (k, n, bits, block_size, ctx.device, "ex",
+             zero_points is not None, g_idx is not None, bias is not None)
+    pack = _CACHE.get(keys, extra,
+                      lambda: pack_nbits_ex(b_q, scales, zero_points, g_idx, bias, k=k, n=n,
+                                            bits=bits, block_size=block_size, ctx=ctx))
+    af = np.ascontiguousarray(a, dtype=np.float32)
+    if af.ndim == 0 or af.shape[-1] != k:
+        raise ValueError(f"MatMulNBits: A's last dimension must be K={k}, got {af.shape}")
+    m = af.size // k
+    y = np.empty(m * n, dtype=np.float32)
+    if m:
+        check(ctx.lib.mmnb_matmul_nbits(ctx.handle, pack.handle, ptr(af), m, ptr(y)))
+    return y.reshape(list(af.shape[:-1]) + [n])
+
+
 # ---------------------------------------------------- DynamicQuantizeLinear
 
 def op_dynamic_quantize_linear(x, ctx=None):
@@ -371,13 +445,17 @@ def op_qlinear_conv(x, x_scale, x_zp, w, w_scale, w_zp, y_scale, y_zp, bias, *, 
 
 # --------------------------------------------------------- dispatch arms
 
-def dispatch(op_type, ins, attrs):
+def dispatch(op_type, ins, attrs, ort_semantics=False):
     """The ``_dispatch`` arms for the quantized operators
     (onnx_graph.dart:1561-1609).  ``ins`` lists the node's positional inputs
     (None for an empty name); returns the output list.  The output range of
     QLinearMatMul / QLinearConv follows the y zero point's type (int8 ->
     [-128, 127], else [0, 255]; the reference reads the initializer's
-    element type, :1578, :1598)."""
+    element type, :1578, :1598).
+
+    ``ort_semantics=True`` lifts the reference's MatMulNBits restrictions:
+    g_idx / bias inputs, bits = 8, float zero points and fp16 scales go to
+    ``op_matmul_nbits_ex``; the default keeps the reference's behaviour."""
     def need(i):
         if i >= len(ins) or ins[i] is None:
             raise ValueError(f"{op_type}: missing input {i}")
@@ -388,6 +466,11 @@ def dispatch(op_type, ins, attrs):
     if op_type == "MatMulInteger":
         return [op_matmul_integer(need(0), need(1), ins[2] if len(ins) > 2 else None,
                                   ins[3] if len(ins) > 3 else None)]
+    if op_type == "MatMulNBits" and ort_semantics:
+        opt_in = [ins[i] if len(ins) > i else None for i in range(3, 6)]
+        return [op_matmul_nbits_ex(need(0), need(1), need(2), *opt_in, k=attrs["K"],
+                                   n=attrs["N"], bits=attrs.get("bits", 4),
+                                   block_size=attrs["block_size"])]
     if op_type == "MatMulNBits":
         if len(ins) > 4:
             raise NotImplementedError("MatMulNBits: g_idx/bias inputs not supported")
