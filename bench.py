@@ -26,6 +26,7 @@ Also reported (extra keys on the same line):
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -206,6 +207,131 @@ def bench_int8(ctx, lib, ops, synth, steps, warmup):
         bf.free()
     pack.free()
     return res
+
+
+def _kernel_us_per_call(kt, reps):
+    """{kernel: µs per call} and the sum, from a timing read over `reps` calls."""
+    per = {name: v[1] / reps * 1e3 for name, v in kt.items()}
+    return per, sum(per.values())
+
+
+def bench_qlinear(ctx, lib, ops, reps=200):
+    """QLinearMatMul at the int8 chain's shape ([512,1024] u8 x [1024,3072]
+    i8 -> u8) and a ResNet-50 layer-1 3x3 convolution (1x64x56x56 u8,
+    64x64x3x3 i8, pad 1) as ConvInteger (int32 out) and QLinearConv
+    (per-channel scales, bias, u8 out).  Kernel times from dispatch events."""
+    out = {}
+    rng = np.random.default_rng(7)
+    m, k, n = 512, 1024, 3072
+    a = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    pack = ops.pack_integer(b, np.int8(0), ctx)
+    da, dz, dq = ctx.to_device(a), ctx.to_device(np.array([128], np.int32)), ctx.alloc(m * n)
+
+    def qmm():
+        lib.check(ctx.lib.mmnb_qlinear_matmul_dev(ctx.handle, pack.handle, da.ptr, 0, 1, m,
+                                                  dz.ptr, 1, 0.02, 0.01, 0.5, 3, 0, dq.ptr))
+    for _ in range(10):
+        qmm()
+    ctx.kernel_timing(True, max_launches=2 * reps)
+    for _ in range(reps):
+        qmm()
+    per, tot = _kernel_us_per_call(ctx.kernel_timing_read(), reps)
+    ctx.kernel_timing(False)
+    nbytes = m * k + k * n + m * n
+    out["qlinear_matmul"] = {
+        "m": m, "k": k, "n": n, "kernels_us": per, "us_per_call": tot,
+        "gbs": nbytes / (tot * 1e-6) / 1e9, "hbm_frac": nbytes / (tot * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "tops": 2.0 * m * k * n / (tot * 1e-6) / 1e12}
+    for bf in (da, dz, dq):
+        bf.free()
+    pack.free()
+    # convolution, ResNet-50 layer 1 (3x3, 64 -> 64, 56x56, pad 1)
+    c, h, w, mo = 64, 56, 56, 64
+    x = rng.integers(0, 256, (1, c, h, w)).astype(np.uint8)
+    wt = rng.integers(-127, 128, (mo, c, 3, 3)).astype(np.int8)
+    cp = ops.pack_conv(wt, np.zeros(mo, np.int8), 1, ctx)
+    prm = lib.ConvParams()
+    prm.strides[0] = prm.strides[1] = 1
+    prm.dilations[0] = prm.dilations[1] = 1
+    for i in range(4):
+        prm.pads[i] = 1
+    dx, dy32, dy8 = ctx.to_device(x), ctx.alloc(mo * h * w * 4), ctx.alloc(mo * h * w)
+    ws = rng.uniform(0.001, 0.01, mo).astype(np.float32)
+    bias = rng.integers(-1000, 1000, mo).astype(np.int32)
+
+    def conv():
+        lib.check(ctx.lib.mmnb_conv_integer_dev(ctx.handle, cp.handle, dx.ptr, 0, 1, c, h, w, 128,
+                                                ctypes.byref(prm), dy32.ptr))
+
+    def qconv():
+        lib.check(ctx.lib.mmnb_qlinear_conv_dev(
+            ctx.handle, cp.handle, dx.ptr, 0, 1, c, h, w, 128, 0.02, ws.ctypes.data, mo, 0.05,
+            128, 0, bias.ctypes.data, ctypes.byref(prm), dy8.ptr))
+    ops_ = 2.0 * mo * h * w * c * 9
+    for name, fn, obytes in (("conv_integer", conv, 4), ("qlinear_conv", qconv, 1)):
+        for _ in range(5):
+            fn()
+        ctx.kernel_timing(True, max_launches=4 * reps)
+        for _ in range(reps):
+            fn()
+        per, tot = _kernel_us_per_call(ctx.kernel_timing_read(), reps)
+        ctx.kernel_timing(False)
+        nbytes = c * h * w + mo * c * 9 + mo * h * w * obytes
+        out[name] = {"shape": "x 1x64x56x56 u8, w 64x64x3x3 i8, pad 1", "kernels_us": per,
+                     "us_per_call": tot, "tops": ops_ / (tot * 1e-6) / 1e12,
+                     "gbs": nbytes / (tot * 1e-6) / 1e9}
+    for bf in (dx, dy32, dy8):
+        bf.free()
+    cp.free()
+    return out
+
+
+def bench_nbits_ex(ctx, lib, ops, reps=300):
+    """MatMulNBits with the inputs the reference rejects, at the headline
+    decode shape M=1, K=N=4096, block 128: bits 8 (uint8 zero points),
+    float zero points, act-order g_idx, bias.  Per-call kernel time (the
+    4-bit kernels plus the gather / block-sum / correction launches) and
+    GB/s over the operator's own bytes."""
+    out = {}
+    rng = np.random.default_rng(9)
+    k = n = 4096
+    bs, m = 128, 1
+    nb = k // bs
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    da, dy = ctx.to_device(a), ctx.alloc(m * n * 4)
+    cases = {
+        "bits8_u8zp": dict(bits=8, z=rng.integers(0, 256, n * nb).astype(np.uint8)),
+        "bits4_float_zp": dict(bits=4, z=rng.uniform(0, 15, (n, nb)).astype(np.float32)),
+        "bits4_g_idx": dict(bits=4, g=rng.permutation(np.repeat(np.arange(nb), bs))),
+        "bits4_bias": dict(bits=4, bias=rng.standard_normal(n).astype(np.float32)),
+    }
+    for name, cfg in cases.items():
+        bits = cfg["bits"]
+        bq = rng.integers(0, 256, (n, nb, bs * bits // 8)).astype(np.uint8)
+        sc = rng.uniform(0.002, 0.02, n * nb).astype(np.float32)
+        pack = ops.pack_nbits_ex(bq, sc, cfg.get("z"), cfg.get("g"), cfg.get("bias"), k=k, n=n,
+                                 bits=bits, block_size=bs, ctx=ctx)
+
+        def call():
+            lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, pack.handle, da.ptr, m, dy.ptr))
+        for _ in range(10):
+            call()
+        ctx.kernel_timing(True, max_launches=5 * reps)
+        for _ in range(reps):
+            call()
+        per, tot = _kernel_us_per_call(ctx.kernel_timing_read(), reps)
+        ctx.kernel_timing(False)
+        z = cfg.get("z")
+        nbytes = (bq.nbytes + sc.nbytes + (0 if z is None else z.nbytes) + a.nbytes + m * n * 4
+                  + (0 if cfg.get("g") is None else k * 4)
+                  + (0 if cfg.get("bias") is None else n * 4))
+        out[name] = {"m": m, "k": k, "n": n, "block": bs, "bits": bits, "kernels_us": per,
+                     "us_per_call": tot, "bytes": nbytes, "gbs": nbytes / (tot * 1e-6) / 1e9}
+        pack.free()
+    da.free()
+    dy.free()
+    return out
 
 
 def bench_decoder(ctx, lib, runs=3):
@@ -483,6 +609,10 @@ def main():
                                                        "kernel_ms", "bytes_per_call")})
             out["decode_sweep"] = sweep
             print("# decode sweep done", file=sys.stderr, flush=True)
+            out["qlinear"] = bench_qlinear(ctx, lib, ops)
+            print(f"# qlinear: {json.dumps(out['qlinear'])[:300]}", file=sys.stderr, flush=True)
+            out["nbits_ex"] = bench_nbits_ex(ctx, lib, ops)
+            print(f"# nbits_ex: {json.dumps(out['nbits_ex'])[:300]}", file=sys.stderr, flush=True)
             out["decoder"] = bench_decoder(ctx, lib)
             print(f"# decoder: decode {out['decoder']['decode_tok_s']:.0f} tok/s, prefill "
                   f"{out['decoder']['prefill_tok_s']:.0f} tok/s", file=sys.stderr, flush=True)

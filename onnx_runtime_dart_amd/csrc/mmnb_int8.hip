@@ -256,7 +256,7 @@ __device__ __forceinline__ void mmi_epilogue(
       rs[r] = __shfl(rsum[i], q * 4 + r, 64);  // lane holding that row's sum
       row[r] = m0 + i * 16 + q * 4 + r;
       int32_t z = 0;
-      if (azp_len == 1) z = azp[0];
+      if (azp_len == 1) z = o.azp_is_const ? o.azp_const : azp[0];
       else if (azp_len > 1 && row[r] < M) z = azp[row[r]];
       cm[r] = (a_signed ? 0 : 128) - z;
     }

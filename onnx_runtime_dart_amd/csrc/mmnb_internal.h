@@ -58,7 +58,10 @@ struct mmnb_ctx {
   int lds_max = 65536;
   // Device staging/scratch buffers, grown on demand and kept for reuse:
   //  0: activations in (fp32 / uint8), 1: outputs, 2: prepared activations
-  //  (fp16 hi/lo), 3: small reductions, 4: misc.
+  //  (fp16 hi/lo), 3: small reductions, 4: raw weights while packing,
+  //  5: small uploads (zero points), 6: convolution im2col rows, 7: block
+  //  sums / the convolution's input zero point, 8: QLinearConv per-channel
+  //  parameters, 9: gathered activations of an extended MatMulNBits pack.
   mmnb::Scratch scratch[10];
   int live_packs = 0;
   // Kernel timing mode: launches go through hipExtLaunchKernelGGL with a
@@ -147,7 +150,9 @@ enum KernelId {
   kKernDecGemvRes = 13,  // decode MatMulNBits + residual (o, down)
   kKernDecGemvGlu = 14,  // decode MatMulNBits, RMSNorm + SwiGLU (gate/up)
   kKernDecGemvLm = 15,   // decode MatMulNBits, RMSNorm + argmax (lm_head)
-  kKernCount = 16
+  kKernIm2col = 16,      // convolution input rows for the MatMulInteger kernels
+  kKernNbitsEx = 17,     // extended MatMulNBits: A gather, block sums, correction
+  kKernCount = 18
 };
 
 // Launch `kern` on the context stream; in timing mode the dispatch records
@@ -253,6 +258,9 @@ struct MmiEpi {
   int32_t yzp = 0, lo = 0, hi = 255;
   int trans = 0;
   int64_t ecol_bstride = 0;
+  // A's zero point as a constant (azp_len must be 1; the pointer is unused)
+  int azp_is_const = 0;
+  int32_t azp_const = 0;
 };
 
 // MatMulInteger on the device.  d_azp: device int32 of length azp_len (0, 1

@@ -78,6 +78,36 @@ __global__ __launch_bounds__(256) void k_nbits_correct(float *__restrict__ Y, in
   Y[m * N + n] += v;
 }
 
+// The same correction for few rows, with the block sums of row m formed in
+// LDS by the workgroup itself (one launch instead of two; every column
+// workgroup re-reads its row, which is cheap for M <= 8).
+constexpr int kFusedMaxBlocks = 8192;
+
+__global__ __launch_bounds__(256) void k_nbits_correct_rows(
+    float *__restrict__ Y, int64_t N, const float *__restrict__ bias,
+    const float *__restrict__ corr, int64_t nb, const float *__restrict__ A, int64_t lda,
+    int64_t ka, int64_t bs) {
+  __shared__ float sas[kFusedMaxBlocks];
+  const int64_t m = blockIdx.y;
+  const int w = threadIdx.x >> 6, ln = threadIdx.x & 63;
+  if (corr) {
+    for (int64_t b = w; b < nb; b += 4) {
+      const int64_t k0 = b * bs, k1 = std::min(ka, k0 + bs);
+      float s = 0.0f;
+      for (int64_t kk = k0 + ln; kk < k1; kk += 64) s += A[m * lda + kk];
+      for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+      if (ln == 0) sas[b] = s;
+    }
+    __syncthreads();
+  }
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float v = bias ? bias[n] : 0.0f;
+  if (corr)
+    for (int64_t b = 0; b < nb; b++) v = fmaf(corr[b * N + n], sas[b], v);
+  Y[m * N + n] += v;
+}
+
 int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                      int64_t m, float *d_y) {
   if (!p->ext) return launch_matmul_nbits(ctx, p, d_a, lda, m, d_y);
@@ -89,7 +119,7 @@ int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_
     if ((rc = scratch_get(ctx, 9, (size_t)(m * p->k64) * 4, &buf))) return rc;
     int64_t blocks = (m * p->k64 + 255) / 256;
     blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, 16384));
-    if ((rc = launch(ctx, kKernPrep, k_gather_a, dim3((unsigned)blocks), dim3(256), 0, d_a, lda,
+    if ((rc = launch(ctx, kKernNbitsEx, k_gather_a, dim3((unsigned)blocks), dim3(256), 0, d_a, lda,
                      m, (const int32_t *)p->d_asrc, p->k, p->k64, (float *)buf)))
       return rc;
     a2 = (const float *)buf;
@@ -97,16 +127,21 @@ int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_
     ka = p->k;
   }
   if ((rc = launch_matmul_nbits(ctx, p, a2, lda2, m, d_y))) return rc;
+  if (m <= 8 && p->corr_nb <= kFusedMaxBlocks)
+    return launch(ctx, kKernNbitsEx, k_nbits_correct_rows,
+                  dim3((unsigned)((p->n + 255) / 256), (unsigned)m), dim3(256), 0, d_y, p->n,
+                  (const float *)p->d_bias, (const float *)p->d_corr, p->corr_nb, a2, lda2, ka,
+                  p->block);
   const float *d_asum = nullptr;
   if (p->d_corr) {
     void *buf = nullptr;
     if ((rc = scratch_get(ctx, 7, (size_t)(m * p->corr_nb) * 4, &buf))) return rc;
-    if ((rc = launch(ctx, kKernPrep, k_block_sums, dim3((unsigned)p->corr_nb, (unsigned)m),
+    if ((rc = launch(ctx, kKernNbitsEx, k_block_sums, dim3((unsigned)p->corr_nb, (unsigned)m),
                      dim3(64), 0, a2, lda2, ka, p->block, p->corr_nb, (float *)buf)))
       return rc;
     d_asum = (const float *)buf;
   }
-  return launch(ctx, kKernPrep, k_nbits_correct,
+  return launch(ctx, kKernNbitsEx, k_nbits_correct,
                 dim3((unsigned)((p->n + 255) / 256), (unsigned)m), dim3(256), 0, d_y, p->n,
                 (const float *)p->d_bias, (const float *)p->d_corr, p->corr_nb, d_asum);
 }

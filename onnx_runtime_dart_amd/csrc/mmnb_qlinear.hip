@@ -20,29 +20,27 @@ using namespace mmnb;
 
 namespace mmnb {
 
-// One image: x [C][H][W] bytes -> out [groups][oh*ow][cg*kh*kw].  Grid-stride
-// over output bytes; the source index is clamped so every load is in bounds.
-__global__ __launch_bounds__(256) void k_im2col(const uint8_t *__restrict__ x, int64_t H,
-                                                int64_t W, int64_t cg, int64_t kh, int64_t kw,
-                                                int64_t oh, int64_t ow, int sh, int sw, int ph,
-                                                int pw, int dh, int dw, uint32_t zp,
-                                                int64_t groups, uint8_t *__restrict__ out) {
-  const int64_t kcn = cg * kh * kw, P = oh * ow;
-  const int64_t total = groups * P * kcn;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t kc = i % kcn, t = i / kcn;
-    const int64_t p = t % P, g = t / P;
-    const int64_t kx = kc % kw, ky = (kc / kw) % kh, c = kc / (kw * kh);
-    const int64_t oy = p / ow, ox = p % ow;
-    const int64_t iy = oy * sh - ph + ky * dh, ix = ox * sw - pw + kx * dw;
-    const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W;
-    const uint8_t v = x[((g * cg + c) * H + (in ? iy : 0)) * W + (in ? ix : 0)];
-    out[i] = in ? v : (uint8_t)zp;
-  }
+// One image: x [C][H][W] bytes -> out [groups][oh*ow][cg*kh*kw].  Grid
+// (output positions, 256-wide chunks of a row, groups); 32-bit index
+// arithmetic (the host checks the sizes); the source index is clamped so
+// every load is in bounds.
+__global__ __launch_bounds__(256) void k_im2col(const uint8_t *__restrict__ x, int H, int W,
+                                                int cg, int kh, int kw, int ow, int sh, int sw,
+                                                int ph, int pw, int dh, int dw, uint32_t zp,
+                                                uint8_t *__restrict__ out) {
+  const int kcn = cg * kh * kw;
+  const int kc = blockIdx.y * blockDim.x + threadIdx.x;
+  if (kc >= kcn) return;
+  const int p = blockIdx.x, g = blockIdx.z;
+  const int khw = kh * kw;
+  const int c = kc / khw, r = kc - c * khw;
+  const int ky = r / kw, kx = r - ky * kw;
+  const int oy = p / ow, ox = p - oy * ow;
+  const int iy = oy * sh - ph + ky * dh, ix = ox * sw - pw + kx * dw;
+  const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W;
+  const uint8_t v = x[((size_t)(g * cg + c) * H + (in ? iy : 0)) * W + (in ? ix : 0)];
+  out[((size_t)g * gridDim.x + p) * kcn + kc] = in ? v : (uint8_t)zp;
 }
-
-__global__ void k_set_i32(int32_t *p, int32_t v) { *p = v; }
 
 }  // namespace mmnb
 
@@ -94,35 +92,34 @@ int check_zp(int64_t v, int is_signed, const char *what) {
 // Device side of a convolution: per image, im2col then the MatMulInteger
 // kernel with a channel-major epilogue.  `o` carries the output pointers of
 // image 0; each image's output follows the previous one's m*oh*ow values.
-// Scratch: slot 6 = im2col, slot 7 = x_zp (int32).
+// Scratch: slot 6 = im2col.
 int conv_run(mmnb_ctx *ctx, const mmnb_pack *p, const uint8_t *d_x, int x_signed,
              const ConvShape &s, int64_t x_zp, MmiEpi o) {
   const int64_t P = s.oh * s.ow, kcn = p->k, g = p->conv_group, m = p->conv_m;
   if (s.n == 0 || P == 0) return MMNB_OK;
-  void *d_col = nullptr, *d_zp = nullptr;
+  if (kcn > 65535 * 256 || g > 65535 || g * P * kcn > INT32_MAX ||
+      s.c * s.h * s.w > INT32_MAX)
+    return fail(MMNB_ERR_UNSUPPORTED, "conv: image too large for one launch");
+  void *d_col = nullptr;
   int rc;
   if ((rc = scratch_get(ctx, 6, (size_t)(g * P * kcn) + 256, &d_col))) return rc;
-  if ((rc = scratch_get(ctx, 7, 64, &d_zp))) return rc;
-  const int32_t zp32 = (int32_t)x_zp;
-  if ((rc = launch(ctx, kKernPrepIntB, k_set_i32, dim3(1), dim3(1), 0, (int32_t *)d_zp, zp32)))
-    return rc;
-  const uint32_t zbyte = (uint32_t)(zp32 & 0xFF);
-  const int64_t total = g * P * kcn;
-  int64_t blocks = (total + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  if (blocks < 1) blocks = 1;
+  o.azp_is_const = 1;
+  o.azp_const = (int32_t)x_zp;
+  const uint32_t zbyte = (uint32_t)(x_zp & 0xFF);
+  const dim3 grid((unsigned)P, (unsigned)((kcn + 255) / 256), (unsigned)g);
   for (int64_t b = 0; b < s.n; b++) {
     const uint8_t *xb = d_x + b * s.c * s.h * s.w;
-    if ((rc = launch(ctx, kKernPrepIntB, k_im2col, dim3((unsigned)blocks), dim3(256), 0, xb,
-                     s.h, s.w, p->conv_cg, p->conv_kh, p->conv_kw, s.oh, s.ow, s.sh, s.sw, s.ph,
-                     s.pw, s.dh, s.dw, zbyte, g, (uint8_t *)d_col)))
+    if ((rc = launch(ctx, kKernIm2col, k_im2col, grid, dim3(256), 0, xb, (int)s.h, (int)s.w,
+                     (int)p->conv_cg, (int)p->conv_kh, (int)p->conv_kw, (int)s.ow, s.sh, s.sw,
+                     s.ph, s.pw, s.dh, s.dw, zbyte, (uint8_t *)d_col)))
       return rc;
     MmiEpi ob = o;
     ob.trans = 1;
     const int64_t off = b * m * P;
     if (o.y) ob.y = o.y + off;
     if (o.yq) ob.yq = o.yq + off;
-    if ((rc = launch_matmul_integer(ctx, p, d_col, x_signed, g, P, (const int32_t *)d_zp, 1, ob)))
+    if ((rc = launch_matmul_integer(ctx, p, d_col, x_signed, g, P, (const int32_t *)ctx->d_pad,
+                                    1, ob)))
       return rc;
   }
   return MMNB_OK;

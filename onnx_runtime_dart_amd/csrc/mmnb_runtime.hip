@@ -679,7 +679,7 @@ static const char *kKernelNames[kKernCount] = {
     "k_gemv_valu", "k_prep_a", "k_gemm_mfma", "k_dql_minmax",
     "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b", "k_probe_empty",
     "k_probe_read", "k_dec_gemv", "k_dec_attn", "k_dec_ops", "k_dec_gemv_res",
-    "k_dec_gemv_glu", "k_dec_gemv_lm"};
+    "k_dec_gemv_glu", "k_dec_gemv_lm", "k_im2col", "k_nbits_ex"};
 
 const char *mmnb_kernel_name(int kernel_id) {
   if (kernel_id < 0 || kernel_id >= kKernCount) return nullptr;
