@@ -304,6 +304,38 @@ int mmnb_qlinear_conv_dev(mmnb_ctx *ctx, const mmnb_pack *w, const void *d_x,
                           const int32_t *bias, const mmnb_conv_params *prm,
                           void *d_y);
 
+/* ---- weight-pack loader -------------------------------------------------
+ * Loads the quantized weights of an ONNX model file into resident packs:
+ * every MatMulNBits (any input form mmnb_pack_nbits_ex accepts),
+ * MatMulInteger / QLinearMatMul (constant B) and ConvInteger / QLinearConv
+ * (constant W) node whose weight inputs are initializers.  Bytes go from the
+ * file to the device: inline raw_data is read in place from the
+ * memory-mapped model, external data (location / offset / length, relative
+ * to the model's directory) from the memory-mapped companion file, so a
+ * multi-GB weight file is never read into host memory whole.  Packs stay
+ * resident until mmnb_model_free.
+ * Replaces: loadOnnxModel (lib/onnx_runtime_dart_io.dart:19-42) and the
+ * weight decoding of tensorFromProto (lib/src/onnx_proto_loader.dart:80-243)
+ * for these nodes' weights; the Dart binding looks packs up by node name
+ * instead of packing host tensors on first use. */
+typedef struct mmnb_model mmnb_model;
+int mmnb_model_load(mmnb_ctx *ctx, const char *path, mmnb_model **out);
+int64_t mmnb_model_pack_count(const mmnb_model *model);
+/* i-th packed node: op type, node name (its first output when unnamed) and
+ * pack; the strings live as long as the model. */
+int mmnb_model_pack_info(const mmnb_model *model, int64_t i, const char **op_type,
+                         const char **node_name, const mmnb_pack **pack);
+int mmnb_model_find(const mmnb_model *model, const char *node_name,
+                    const mmnb_pack **pack);
+int mmnb_model_free(mmnb_model *model);
+
+/* The external-data guard: location a plain relative path inside the model's
+ * directory (no "..", no absolute path, no drive), [offset, offset+length)
+ * within the file's file_len bytes; MMNB_OK or MMNB_ERR_ARG.
+ * Replaces: checkExternalRef (lib/onnx_runtime_dart_io.dart:44-69). */
+int mmnb_check_external_ref(const char *location, int64_t offset, int64_t length,
+                            int64_t file_len);
+
 /* ---- decoder ops around MatMulNBits -------------------------------------
  * Device buffers, asynchronous on the context stream (like the _dev entry
  * points above).  fp32 throughout. */
@@ -402,6 +434,11 @@ int mmnb_pack_free(mmnb_pack *pack);
 
 /* Device bytes held by a pack. */
 int64_t mmnb_pack_device_bytes(const mmnb_pack *pack);
+
+/* The operator shape a pack serves: k = A's last dimension (MatMulNBits,
+ * MatMulInteger) or c_per_group*kh*kw (convolution), n = output columns or
+ * channels, batch = B's batch (MatMulInteger) or the group count (conv). */
+int mmnb_pack_dims(const mmnb_pack *pack, int64_t *k, int64_t *n, int64_t *batch);
 
 /* ---- device memory and timing (harness utilities; no reference
  *      counterpart: the reference has no device) ------------------------- */

@@ -43,6 +43,13 @@ SIGNATURES = {
     "mmnb_dynamic_matmul_dev": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
                                        _vp, _vp]),
     "mmnb_pack_nbits_ex": (_int, [_vp, _vp, _P(_vp)]),
+    "mmnb_model_load": (_int, [_vp, ctypes.c_char_p, _P(_vp)]),
+    "mmnb_model_pack_count": (_i64, [_vp]),
+    "mmnb_model_pack_info": (_int, [_vp, _i64, _P(ctypes.c_char_p), _P(ctypes.c_char_p),
+                                    _P(_vp)]),
+    "mmnb_model_find": (_int, [_vp, ctypes.c_char_p, _P(_vp)]),
+    "mmnb_model_free": (_int, [_vp]),
+    "mmnb_check_external_ref": (_int, [ctypes.c_char_p, _i64, _i64, _i64]),
     "mmnb_qlinear_matmul": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, ctypes.c_float,
                                    ctypes.c_float, ctypes.c_float, _i64, _int, _vp]),
     "mmnb_qlinear_matmul_dev": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64,
@@ -62,6 +69,7 @@ SIGNATURES = {
                                      _vp, _vp]),
     "mmnb_pack_free": (_int, [_vp]),
     "mmnb_pack_device_bytes": (_i64, [_vp]),
+    "mmnb_pack_dims": (_int, [_vp, _P(_i64), _P(_i64), _P(_i64)]),
     "mmnb_device_alloc": (_int, [_vp, _sz, _P(_vp)]),
     "mmnb_device_free": (_int, [_vp, _vp]),
     "mmnb_memcpy_h2d": (_int, [_vp, _vp, _vp, _sz]),

@@ -16,7 +16,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libmmnb.so"
 SOURCES = ["mmnb_runtime.hip", "mmnb_nbits.hip", "mmnb_int8.hip", "mmnb_decoder.hip",
-           "mmnb_qlinear.hip", "mmnb_nbits_ex.hip"]
+           "mmnb_qlinear.hip", "mmnb_nbits_ex.hip", "mmnb_model.hip"]
 ARCH = "gfx950"
 
 

@@ -557,6 +557,14 @@ int mmnb_dynamic_matmul_dev(mmnb_ctx *ctx, const mmnb_pack *pack, const float *d
 
 // ---------------------------------------------------------------------- packs
 
+int mmnb_pack_dims(const mmnb_pack *p, int64_t *k, int64_t *n, int64_t *batch) {
+  if (!p) return fail(MMNB_ERR_ARG, "null pack");
+  if (k) *k = p->kind == kPackNBits ? p->k_in : p->k;
+  if (n) *n = p->kind == kPackConv ? p->conv_m : p->n;
+  if (batch) *batch = p->kind == kPackNBits ? 1 : p->batch;
+  return MMNB_OK;
+}
+
 int mmnb_pack_free(mmnb_pack *p) {
   if (!p) return MMNB_OK;
   mmnb_ctx *ctx = p->ctx;

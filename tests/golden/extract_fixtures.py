@@ -8,7 +8,8 @@ path, and the six that pin the decoder ops around it (RMSNorm chain,
 ``RotaryEmbedding``, ``GroupQueryAttention`` with and without KV cache,
 rotary and bias), decodes the initializers and node attributes out of ``model.onnx`` with
 a minimal protobuf wire-format reader (no ``onnx`` package needed), and writes
-``tests/golden/<case>.json``.  The fixtures are data: the inputs the
+``tests/golden/<case>.json`` (and, for the loader tests, copies a few
+``model.onnx`` files to ``tests/golden/onnx/<case>.onnx``).  The fixtures are data: the inputs the
 reference's ORT-oracle fixture test feeds (``test/fixture_parity_test.dart``)
 and the outputs native onnxruntime produced for them
 (``tool/gen_fixtures.py:59-102``, ``:690-693``, ``:713-735``, ``:892-925``).
@@ -46,6 +47,12 @@ CASES = [
     "qlinearconv_pertensor",
     "qlinearconv_perchannel_bias",
 ]
+
+# Fixtures whose model.onnx is also kept (tests/golden/onnx/), as real
+# exporter output for the weight-pack loader.
+ONNX_FILES = {"matmulnbits_basic", "matmulnbits_zeropoints", "matmulnbits_partial_block",
+              "matmulinteger_u8i8", "matmulinteger_percol_bzp", "qlinearmatmul",
+              "convinteger", "convinteger_1d", "qlinearconv_perchannel_bias"}
 
 # ONNX TensorProto.DataType codes used by these fixtures.
 DTYPES = {1: ("float32", "<f", 4), 2: ("uint8", "<B", 1), 3: ("int8", "<b", 1),
@@ -211,6 +218,9 @@ def main():
         if len(nodes) > 1:  # a multi-node pattern (the RMSNorm chain)
             out["nodes"] = nodes
         (dst / f"{case}.json").write_text(json.dumps(out, indent=None) + "\n")
+        if case in ONNX_FILES:  # the model file itself, for the weight loader
+            (dst / "onnx").mkdir(exist_ok=True)
+            (dst / "onnx" / f"{case}.onnx").write_bytes((d / "model.onnx").read_bytes())
         print(case, nodes[0]["op_type"], nodes[0]["attrs"],
               {k: v["shape"] for k, v in inits.items()})
 
