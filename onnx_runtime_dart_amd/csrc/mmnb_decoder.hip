@@ -25,6 +25,7 @@
 #include <new>
 #include <vector>
 
+#include "mmnb_device.h"
 #include "mmnb_internal.h"
 
 namespace mmnb {
@@ -393,27 +394,39 @@ constexpr int kDecMaxGroup = 4;     // query heads per KV head
 constexpr int kDecMaxLen = 8192;    // cache length (merge weights kept in LDS)
 constexpr int kDecMaxSplits = kDecMaxLen / kDecKS;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_add_dec(float v) {
-  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
-                                                false);
-  return v + __builtin_bit_cast(float, moved);
-}
-
 // Sum over each aligned group of 8 lanes (DPP within a row).
 __device__ __forceinline__ float lane8_sum(float v) {
-  v = dpp_add_dec<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = dpp_add_dec<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = dpp_add_dec<0x141>(v);  // row_half_mirror: lanes 0-7 <-> 7-0 of each half row
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror: lanes 0-7 <-> 7-0 of each half row
   return v;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void k_dec_attn(
-    const DecState *__restrict__ st, const float *__restrict__ qkv, int nh, int kvh,
-    const float *__restrict__ qn, const float *__restrict__ kn, float eps,
-    const float *__restrict__ cos, const float *__restrict__ sin, float *ck, float *cv,
-    int64_t cap, float scale, float *part, int *counters, float *__restrict__ out) {
+// Operands of one layer's decode attention.  Partials live at
+// part[((kh*group + g) * nsmax + split) * (HD + 2)]: max, sum, o[HD].
+struct DecAttnArgs {
+  const float *qkv;
+  int nh, kvh;
+  const float *qn, *kn;
+  float eps;
+  const float *cos, *sin;
+  float *ck, *cv;
+  int64_t cap;
+  float scale;
+  float *part;
+  int nsmax;
+  float *out;
+};
+
+// One split of kDecKS keys of KV head kh at position pos: the group's q
+// heads and the new k (per-head RMSNorm, rotary at pos), scores (8 lanes per
+// key, DPP reduction), a split-local softmax, o = sum p v, and the partial
+// (max, sum, o) of every query head of the group.  The split holding pos also
+// writes the new k / v into the cache.  COH: qkv was written in the same
+// launch and the cache row is read by other workgroups of the same launch
+// (coherent loads / stores, see ld_act).  Whole workgroup, 256 threads.
+template <int HD, bool COH>
+__device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int kh) {
   constexpr int kDpk = HD / 8;  // dims per K lane (a multiple of 4)
   constexpr int kHr = HD / 2;
   __shared__ __align__(16) float sq[kDecMaxGroup][HD];
@@ -425,21 +438,15 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   __shared__ float sred[kDecMaxGroup][2][kAttnMaxHd];
   __shared__ __align__(16) float sp[kDecMaxGroup][kDecKS];
   __shared__ float smx[kDecMaxGroup], sl[kDecMaxGroup];
-  __shared__ float sw[kDecMaxGroup][kDecMaxSplits], sls[kDecMaxGroup][kDecMaxSplits];
-  __shared__ float sden[kDecMaxGroup];
-  __shared__ int s_last;
-  const int split = blockIdx.x, kh = blockIdx.y;
-  const int group = nh / kvh;
+  const int nh = a.nh, kvh = a.kvh, group = nh / kvh;
   const int t = threadIdx.x, w = t >> 6, ln = t & 63;
   const int d = t & (kAttnMaxHd - 1), half = t >> 7;  // V layout: dim, key half
   const int jk = t >> 3, p8 = t & 7;                  // K layout: key, dim slice
-  const int pos = st->pos;
   const int L = pos + 1;
   const int nsplit = (L + kDecKS - 1) / kDecKS;
-  if (split >= nsplit) return;  // whole workgroup
   const int j0 = split * kDecKS;
-  const float *Kb = ck + (int64_t)kh * cap * HD;
-  const float *Vb = cv + (int64_t)kh * cap * HD;
+  const float *Kb = a.ck + (int64_t)kh * a.cap * HD;
+  const float *Vb = a.cv + (int64_t)kh * a.cap * HD;
   const bool lo = t < HD;
   const int dc = lo ? t : HD - 1;
   // ---- loads (rows >= pos are read from row 0 and replaced or dropped)
@@ -466,13 +473,13 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   float xq[kDecMaxGroup];
 #pragma unroll
   for (int g = 0; g < kDecMaxGroup; g++)
-    xq[g] = qkv[(kh * group + (g < group ? g : 0)) * HD + dc];
-  const float xk = qkv[(nh + kh) * HD + dc];
-  const float xv = qkv[(nh + kvh + kh) * HD + dc];
-  const float gq = qn[dc], gk = kn[dc];
+    xq[g] = ld_act<COH>(a.qkv + (kh * group + (g < group ? g : 0)) * HD + dc);
+  const float xk = ld_act<COH>(a.qkv + (nh + kh) * HD + dc);
+  const float xv = ld_act<COH>(a.qkv + (nh + kvh + kh) * HD + dc);
+  const float gq = a.qn[dc], gk = a.kn[dc];
   const int pi = dc < kHr ? dc : dc - kHr;
-  const double cs = (double)cos[(int64_t)pos * kHr + pi];
-  const double sn = (double)sin[(int64_t)pos * kHr + pi];
+  const double cs = (double)a.cos[(int64_t)pos * kHr + pi];
+  const double sn = (double)a.sin[(int64_t)pos * kHr + pi];
   // ---- per-head RMSNorm of the group's q heads and of k (double sums,
   // one block reduction for all of them), then rotary at pos
   {
@@ -495,7 +502,7 @@ __global__ __launch_bounds__(256) void k_dec_attn(
 #pragma unroll
     for (int g = 0; g <= kDecMaxGroup; g++) {
       const double tot = shd[g][0] + shd[g][1] + shd[g][2] + shd[g][3];
-      const double inv = 1.0 / sqrt(tot / (double)HD + (double)eps);
+      const double inv = 1.0 / sqrt(tot / (double)HD + (double)a.eps);
       const float x = g < kDecMaxGroup ? xq[g] : xk;
       const float gam = g < kDecMaxGroup ? gq : gk;
       if (lo) shx[g][t] = (float)((double)x * inv * (double)gam);
@@ -526,7 +533,7 @@ __global__ __launch_bounds__(256) void k_dec_attn(
 #pragma unroll
         for (int e = 0; e < kDpk; e++) dot = fmaf(sq[g][p8 * kDpk + e], kreg[e], dot);
         dot = lane8_sum(dot);
-        if (p8 == 0) ssc[g][jk] = j < L ? dot * scale : -INFINITY;
+        if (p8 == 0) ssc[g][jk] = j < L ? dot * a.scale : -INFINITY;
       }
     }
   }
@@ -571,49 +578,46 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   __syncthreads();
   if (lo) {
     for (int g = 0; g < group; g++) {
-      float *pp = part + ((int64_t)(kh * group + g) * gridDim.x + split) * (HD + 2);
+      float *pp = a.part + ((int64_t)(kh * group + g) * a.nsmax + split) * (HD + 2);
       if (t == 0) {
-        __hip_atomic_store(pp, smx[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pp + 1, sl[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_act<true>(pp, smx[g]);
+        st_act<true>(pp + 1, sl[g]);
       }
-      __hip_atomic_store(pp + 2 + t, sred[g][0][t] + sred[g][1][t], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      st_act<true>(pp + 2 + t, sred[g][0][t] + sred[g][1][t]);
     }
   }
   // the split holding position pos writes the new k / v into the cache
   // (issued late: an outstanding store would hold up every vmcnt wait above)
   if (split == nsplit - 1 && lo) {
-    ck[((int64_t)kh * cap + pos) * HD + t] = skn[t];
-    cv[((int64_t)kh * cap + pos) * HD + t] = xv;
+    st_act<COH>(a.ck + ((int64_t)kh * a.cap + pos) * HD + t, skn[t]);
+    st_act<COH>(a.cv + ((int64_t)kh * a.cap + pos) * HD + t, xv);
   }
-  // ---- publish: every partial store has completed before the count moves
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (t == 0) {
-    const int prev =
-        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == nsplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // ---- merge (last split of this KV head), one memory round trip: each
-  // thread (head g, dim) loads its dimension of up to 16 splits while the
-  // splits' (max, sum) go to LDS; then weights exp(m_s - M) and the sums
-  const float *pg = part + (int64_t)kh * group * gridDim.x * (HD + 2);
+}
+
+// Merges the nsplit partials of KV head kh into out (every query head of the
+// group), one memory round trip for up to 16 splits: each thread (head g,
+// dim) loads its dimension of the splits while the splits' (max, sum) go to
+// LDS; then the weights exp(m_s - M) and the sums.  Whole workgroup.
+template <int HD, bool COH>
+__device__ void dec_attn_merge(const DecAttnArgs &a, int pos, int kh) {
+  __shared__ float sw[kDecMaxGroup][kDecMaxSplits], sls[kDecMaxGroup][kDecMaxSplits];
+  __shared__ float sden[kDecMaxGroup];
+  const int group = a.nh / a.kvh, t = threadIdx.x;
+  const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
+  const float *pg = a.part + (int64_t)kh * group * a.nsmax * (HD + 2);
   const int gt = t / HD, dt = t % HD;  // this thread's (head, dim) while gt < group
-  const float *p0 = pg + (int64_t)(gt < group ? gt : 0) * gridDim.x * (HD + 2) + 2 + dt;
+  const float *p0 = pg + (int64_t)(gt < group ? gt : 0) * a.nsmax * (HD + 2) + 2 + dt;
   float v[16];
 #pragma unroll
   for (int u = 0; u < 16; u++) {
     const int s2 = u < nsplit ? u : nsplit - 1;
-    v[u] = __hip_atomic_load(p0 + (int64_t)s2 * (HD + 2), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    v[u] = ld_act<true>(p0 + (int64_t)s2 * (HD + 2));
   }
   for (int i = t; i < group * nsplit; i += 256) {
     const int g = i / nsplit, s2 = i % nsplit;
-    const float *pp = pg + ((int64_t)g * gridDim.x + s2) * (HD + 2);
-    sw[g][s2] = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sls[g][s2] = __hip_atomic_load(pp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float *pp = pg + ((int64_t)g * a.nsmax + s2) * (HD + 2);
+    sw[g][s2] = ld_act<true>(pp);
+    sls[g][s2] = ld_act<true>(pp + 1);
   }
   __syncthreads();
   if (t < group) {
@@ -632,24 +636,49 @@ __global__ __launch_bounds__(256) void k_dec_attn(
   // 16 (caches longer than 512) load again
   for (int i = t; i < group * HD; i += 256) {
     const int gi = i / HD, di = i % HD;
-    const float *pi0 = pg + (int64_t)gi * gridDim.x * (HD + 2) + 2 + di;
+    const float *pi0 = pg + (int64_t)gi * a.nsmax * (HD + 2) + 2 + di;
     float num = 0.0f;
     for (int s0 = 0; s0 < nsplit; s0 += 16) {
       if (i != t || s0 != 0) {
 #pragma unroll
         for (int u = 0; u < 16; u++) {
           const int s2 = s0 + u < nsplit ? s0 + u : nsplit - 1;
-          v[u] = __hip_atomic_load(pi0 + (int64_t)s2 * (HD + 2), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+          v[u] = ld_act<true>(pi0 + (int64_t)s2 * (HD + 2));
         }
       }
 #pragma unroll
       for (int u = 0; u < 16; u++)
         if (s0 + u < nsplit) num = fmaf(sw[gi][s0 + u], v[u], num);
     }
-    out[(kh * group + gi) * HD + di] = num / sden[gi];
+    st_act<COH>(a.out + (kh * group + gi) * HD + di, num / sden[gi]);
   }
-  if (t == 0) __hip_atomic_store(&counters[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();  // the LDS above may be reused by the caller's next item
+}
+
+// Launch form: grid (splits, KV heads); the last split of a KV head to
+// finish (counter, reset by it) merges.
+template <int HD>
+__global__ __launch_bounds__(256) void k_dec_attn(const DecState *__restrict__ st,
+                                                  DecAttnArgs a, int *counters) {
+  __shared__ int s_last;
+  const int split = blockIdx.x, kh = blockIdx.y;
+  const int pos = st->pos;
+  const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
+  if (split >= nsplit) return;  // whole workgroup
+  dec_attn_partial<HD, false>(a, pos, split, kh);
+  // ---- publish: every partial store has completed before the count moves
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev =
+        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == nsplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  dec_attn_merge<HD, false>(a, pos, kh);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&counters[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -1045,11 +1074,12 @@ static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float 
   const mmnb_decoder_config &c = d->cfg;
   const dim3 grid((unsigned)((c.max_len + kDecKS - 1) / kDecKS), (unsigned)c.kv_heads);
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
+  DecAttnArgs args{(const float *)d->qkv, (int)c.heads, (int)c.kv_heads, (const float *)L.qn,
+                   (const float *)L.kn, c.eps, (const float *)d->cos, (const float *)d->sin,
+                   ck, cv, c.max_len, scale, d->part, (int)grid.x, d->attn};
 #define MMNB_DEC_ATTN(HD)                                                                      \
   launch(ctx, kKernDecAttn, k_dec_attn<HD>, grid, dim3(256), 0, (const DecState *)d->state,   \
-         (const float *)d->qkv, (int)c.heads, (int)c.kv_heads, (const float *)L.qn,            \
-         (const float *)L.kn, c.eps, (const float *)d->cos, (const float *)d->sin, ck, cv,     \
-         c.max_len, scale, d->part, d->counters, d->attn)
+         args, d->counters)
   switch (c.head_dim) {
     case 32: return MMNB_DEC_ATTN(32);
     case 64: return MMNB_DEC_ATTN(64);

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdint>
 
+#include "mmnb_device.h"
 #include "mmnb_internal.h"
 
 namespace mmnb {
@@ -138,23 +139,6 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) 
 // The 32 lanes of a column half-wave reduce with DPP/swizzle, the waves
 // through LDS.
 // ---------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
-                                                false);
-  return v + __builtin_bit_cast(float, moved);
-}
-
-// Sum over each group of 32 lanes; every lane of the group gets the sum.
-__device__ __forceinline__ float half_wave_sum(float v) {
-  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = dpp_add<0x141>(v);  // row_half_mirror
-  v = dpp_add<0x140>(v);  // row_mirror
-  // xor 16 inside each 32-lane group (ds_swizzle bit mode, xor_mask = 16)
-  const int o = __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F);
-  return v + __builtin_bit_cast(float, o);
-}
 
 constexpr int kGemvMaxWaves = 4;
 
@@ -367,11 +351,6 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
 // Lane layout and arithmetic follow k_gemv_valu with M = 1 and one
 // quantisation block per chunk; K is at most 4096 (one chunk per lane).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ unsigned long long argmax_key(float v, int col) {
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)col);
-}
 
 template <int R, bool NORM, int EPI>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
