@@ -80,6 +80,8 @@ struct mmnb_ctx {
   int gemv_cg = 0;
   // Prefill GEMM LDS stages (2 or 3; MMNB_GEMM_STAGES tuning override).
   int gemm_stages = 2;
+  // Prefill GEMM 128-column blocks per tile (MMNB_GEMM_CB: 1 or 2; 0 = auto).
+  int gemm_cb = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
 };

@@ -1022,15 +1022,17 @@ constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 // bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-template <int NBPS, int NST, int GROUPS>
+template <int NBPS, int NST, int GROUPS, int CB>
 __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs, int segsp,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S,
     const uint8_t *__restrict__ Z, int nb, int bs_log2, int M, int N, int grid_x, int grid_y,
     float *__restrict__ Y) {
-  constexpr int kSz = 128 * NBPS;                 // scale (and zero-point) dwords per stage
-  constexpr int kStageU4 = 1024 + 256 + kSz / 2;  // uint4 per stage: A, W, scales + zp
-  constexpr int kL = 5 + NBPS;                    // DMA loads per thread per stage
+  constexpr int kBN = kGemmBN * CB;                    // columns per workgroup tile
+  constexpr int kSz = kBN * NBPS;                       // scale (and zero-point) dwords per stage
+  constexpr int kStageU4 = 1024 + 256 * CB + kSz / 2;   // uint4 per stage: A, W, scales + zp
+  constexpr int kL = 4 + CB + CB * NBPS;                // DMA loads per thread per stage
+  constexpr int kSOff = 1024 + 256 * CB;                // scales / zero points in a stage
   extern __shared__ uint4 smem_all[];
   // wave-uniform indices in scalar registers
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1055,7 +1057,7 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
   const int ty = first_y + (L % per_group) % rows_in_group;
   const int tx = (L % per_group) / rows_in_group;
   const int rb0 = ty * 2;
-  const int n0 = tx * kGemmBN;
+  const int n0 = tx * kBN;
 
   // DMA sources.  Activations: thread's unit pieces idx = tid + 256 i
   // (unit idx/64 = row block (idx/64)/8, step*2+part (idx/64)%8); the
@@ -1068,15 +1070,19 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     const int u = idx >> 6;
     a_off[i] = ((u >> 3) * segsp * 8 + (u & 7)) * 64 + (idx & 63);
   }
-  const int wcol = min(n0 + (tid >> 1), N - 1);
-  const uint8_t *w_base = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
+  const uint8_t *w_base[CB];
+#pragma unroll
+  for (int i = 0; i < CB; i++) {
+    const int wcol = min(n0 + 128 * i + (tid >> 1), N - 1);
+    w_base[i] = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
+  }
   // scale / zero-point slots of this thread: slot = tid + 256 i, i < NBPS;
   // slots [0, kSz) are scales, [kSz, 2 kSz) zero-point dwords, each indexed
   // (column c, block q) as c * NBPS + q.
-  int sz_col[NBPS], sz_q[NBPS];
-  bool sz_isz[NBPS];
+  int sz_col[CB * NBPS], sz_q[CB * NBPS];
+  bool sz_isz[CB * NBPS];
 #pragma unroll
-  for (int i = 0; i < NBPS; i++) {
+  for (int i = 0; i < CB * NBPS; i++) {
     int slot = tid + 256 * i;
     sz_isz[i] = slot >= kSz;
     if (sz_isz[i]) slot -= kSz;
@@ -1084,11 +1090,16 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     sz_q[i] = slot % NBPS;
   }
 
-  // this lane's output column
-  const int ccol = n0 + wave * 32 + cl;
-  const bool colok = ccol < N;
-  const int col = colok ? ccol : N - 1;
-  const int my_slot = (wave * 32 + cl) * NBPS;
+  // this lane's output columns (CB 32-column blocks of the wave)
+  int col[CB], my_slot[CB];
+  bool colok[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; cb++) {
+    const int ccol = n0 + (wave * CB + cb) * 32 + cl;
+    colok[cb] = ccol < N;
+    col[cb] = colok[cb] ? ccol : N - 1;
+    my_slot[cb] = ((wave * CB + cb) * 32 + cl) * NBPS;
+  }
 
   auto issue = [&](int seg, int buf) {
     const int sa_ = min(seg, segsp - 1);
@@ -1098,10 +1109,14 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     for (int i = 0; i < 4; i++)
       __builtin_amdgcn_global_load_lds(a_base + a_off[i] + sa_ * 512, st + 256 * i + 64 * wave,
                                        16, 0, 0);
-    __builtin_amdgcn_global_load_lds(w_base + sg * kSegBytes, st + 1024 + 64 * wave, 16, 0, 0);
-    uint32_t *sz = (uint32_t *)(st + 1280);
 #pragma unroll
-    for (int i = 0; i < NBPS; i++) {
+    for (int i = 0; i < CB; i++) {
+      const uint8_t *wsrc = w_base[i] + sg * kSegBytes;
+      __builtin_amdgcn_global_load_lds(wsrc, st + 1024 + 256 * i + 64 * wave, 16, 0, 0);
+    }
+    uint32_t *sz = (uint32_t *)(st + kSOff);
+#pragma unroll
+    for (int i = 0; i < CB * NBPS; i++) {
       const int blk = (sa_ * kSegK + sz_q[i] * (kSegK / NBPS)) >> bs_log2;
       const int b2 = blk < nb ? blk : nb - 1;
       const int zi = sz_col[i] * nb + b2;
@@ -1112,16 +1127,18 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
   };
 
   constexpr int kDSets = NBPS > 1 ? 2 : 1;
-  float16_t acc[2], D[kDSets][2];
+  float16_t acc[2][CB], D[kDSets][2][CB];
   const float16_t zero16 = {};
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      acc[t][r] = 0.0f;
+    for (int cb = 0; cb < CB; cb++)
 #pragma unroll
-      for (int ds = 0; ds < kDSets; ds++) D[ds][t][r] = 0.0f;
-    }
+      for (int r = 0; r < 16; r++) {
+        acc[t][cb][r] = 0.0f;
+#pragma unroll
+        for (int ds = 0; ds < kDSets; ds++) D[ds][t][cb][r] = 0.0f;
+      }
 
 #pragma unroll
   for (int p = 0; p < NST - 1; p++) issue(sbeg + p, p);
@@ -1135,33 +1152,42 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     issue(seg + NST - 1, buf == 0 ? NST - 1 : buf - 1);
     const uint4 *st = smem + buf * kStageU4;
     const u4vec *sAv = (const u4vec *)st;
-    const uint32_t *sS = (const uint32_t *)(st + 1280);
-    const u4vec wv = ((const u4vec *)(st + 1024))[(wave * 32 + cl) * 2 + g];
-    int zpv[NBPS];
-    float scv[NBPS];
+    const uint32_t *sS = (const uint32_t *)(st + kSOff);
+    u4vec wv[CB];
+    int zpv[CB][NBPS];
+    float scv[CB][NBPS];
 #pragma unroll
-    for (int q = 0; q < NBPS; q++) {
-      const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
-      const int b2 = blk < nb ? blk : nb - 1;
-      const int zi = col * nb + b2;
-      const uint32_t zd = sS[kSz + my_slot + q];
-      const float sv = __builtin_bit_cast(float, sS[my_slot + q]);
-      zpv[q] = (int)((zd >> (8 * ((zi >> 1) & 3) + 4 * (zi & 1))) & 0xF);
-      scv[q] = blk < nb ? sv : 0.0f;
+    for (int cb = 0; cb < CB; cb++) {
+      wv[cb] = ((const u4vec *)(st + 1024))[((wave * CB + cb) * 32 + cl) * 2 + g];
+#pragma unroll
+      for (int q = 0; q < NBPS; q++) {
+        const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
+        const int b2 = blk < nb ? blk : nb - 1;
+        const int zi = col[cb] * nb + b2;
+        const uint32_t zd = sS[kSz + my_slot[cb] + q];
+        const float sv = __builtin_bit_cast(float, sS[my_slot[cb] + q]);
+        zpv[cb][q] = (int)((zd >> (8 * ((zi >> 1) & 3) + 4 * (zi & 1))) & 0xF);
+        scv[cb][q] = blk < nb ? sv : 0.0f;
+      }
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int q = j / (4 / NBPS);
       const int ds = (NBPS > 1) ? (q & 1) : 0;
-      const half8_t b = dequant8(wv[j], zpv[q], magic);
+      half8_t b[CB];
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++) b[cb] = dequant8(wv[cb][j], zpv[cb][q], magic);
       const bool fresh = (NBPS > 1) && ((j % (4 / NBPS)) == 0);
 #pragma unroll
       for (int rb = 0; rb < 2; rb++) {
         const half8_t ah = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + 0) * 64 + lane]);
         const half8_t al = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + 1) * 64 + lane]);
-        D[ds][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, fresh ? zero16 : D[ds][rb],
-                                                           0, 0, 0);
-        D[ds][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, D[ds][rb], 0, 0, 0);
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) {
+          D[ds][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              ah, b[cb], fresh ? zero16 : D[ds][rb][cb], 0, 0, 0);
+          D[ds][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b[cb], D[ds][rb][cb], 0, 0, 0);
+        }
       }
       const bool boundary = (NBPS > 1)
                                 ? (((j + 1) % (4 / NBPS)) == 0)
@@ -1170,10 +1196,12 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-          for (int r = 0; r < 16; r++) {
-            acc[rb][r] = fmaf(scv[q], D[ds][rb][r], acc[rb][r]);
-            if (NBPS == 1) D[ds][rb][r] = 0.0f;
-          }
+          for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              acc[rb][cb][r] = fmaf(scv[cb][q], D[ds][rb][cb][r], acc[rb][cb][r]);
+              if (NBPS == 1) D[ds][rb][cb][r] = 0.0f;
+            }
       }
     }
     if (++buf == NST) buf = 0;
@@ -1184,13 +1212,15 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
   if constexpr (GROUPS > 1) {
     // partial tiles of groups 1.. -> LDS, summed by group 0
     __syncthreads();
-    float *red = (float *)smem_all;  // (GROUPS-1) x 32 x 256 floats
+    float *red = (float *)smem_all;  // (GROUPS-1) x 32*CB x 256 floats
     if (grp > 0) {
 #pragma unroll
       for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-          red[((grp - 1) * 32 + rb * 16 + r) * 256 + tid] = acc[rb][r];
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            red[((grp - 1) * 32 * CB + (rb * CB + cb) * 16 + r) * 256 + tid] = acc[rb][cb][r];
     }
     __syncthreads();
     if (grp > 0) return;
@@ -1198,18 +1228,22 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
 #pragma unroll
       for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-          acc[rb][r] += red[((gg - 1) * 32 + rb * 16 + r) * 256 + tid];
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            acc[rb][cb][r] += red[((gg - 1) * 32 * CB + (rb * CB + cb) * 16 + r) * 256 + tid];
   }
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
-  if (colok) {
+#pragma unroll
+  for (int cb = 0; cb < CB; cb++) {
+    if (!colok[cb]) continue;
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int row = (rb0 + rb) * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-        if (row < M) Y[(size_t)row * N + col] = ldexpf(acc[rb][r], -row_exp[row]);
+        if (row < M) Y[(size_t)row * N + col[cb]] = ldexpf(acc[rb][cb][r], -row_exp[row]);
       }
     }
   }
@@ -1219,17 +1253,24 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
                        int64_t m, float *d_y) {
   const int64_t segs = p->k64 / kSegK;
   const int64_t mpad = (m + kGemmBM - 1) / kGemmBM * kGemmBM;
-  const int gx = (int)((p->n + kGemmBN - 1) / kGemmBN), gy = (int)(mpad / kGemmBM);
+  const int gy = (int)(mpad / kGemmBM);
+  // 256-column tiles (each wave two 32-column blocks, so every A fragment
+  // read from LDS feeds twice the MFMAs and A streams half as often) when
+  // there are at least 1.5 such tiles per CU (measured: 448 tiles on 256 CUs
+  // gain 8%, 256 tiles lose 3%); 128 otherwise.
+  int cb = ((p->n + 2 * kGemmBN - 1) / (2 * kGemmBN)) * gy >= 3 * ctx->cu_count / 2 ? 2 : 1;
+  if (ctx->gemm_cb) cb = ctx->gemm_cb;
+  const int gx = (int)((p->n + cb * kGemmBN - 1) / (cb * kGemmBN));
   const int nbps = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
   // K split over two wave groups when the tiles alone leave CUs with one
   // wave per SIMD; each group's range covers whole quantisation blocks.
   const int groups = ((int64_t)gx * gy < 2 * (int64_t)ctx->cu_count && segs >= 16) ? 2 : 1;
-  const int nst = ctx->gemm_stages;
+  const int nst = cb == 2 ? 2 : ctx->gemm_stages;
   const int64_t align = groups * std::max<int64_t>(1, p->block / kSegK);
   const int64_t segsp = (segs + align - 1) / align * align;
   const int64_t rblocks = mpad / 32;
   const size_t ap_bytes = (size_t)(rblocks * segsp * 4 * 2 * 64) * 16;
-  const size_t shmem = (size_t)groups * nst * (1024 + 256 + 64 * nbps) * 16;
+  const size_t shmem = (size_t)groups * nst * (1024 + 256 * cb + 64 * cb * nbps) * 16;
   if (shmem > (size_t)ctx->lds_max)
     return fail(MMNB_ERR_UNSUPPORTED, "GEMM: LDS stages exceed the device limit");
   void *d_ap = nullptr, *d_exp = nullptr;
@@ -1241,9 +1282,9 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
     return rc;
   const int bs_log2 = ilog2(p->block);
   const dim3 grid((unsigned)(gx * gy));
-#define MMNB_GEMM_LAUNCH(Q, NS, GR)                                                          \
+#define MMNB_GEMM_LAUNCH(Q, NS, GR, CB)                                                      \
   {                                                                                          \
-    auto kern = k_gemm_mfma<Q, NS, GR>;                                                      \
+    auto kern = k_gemm_mfma<Q, NS, GR, CB>;                                                  \
     if (shmem > 65536) {                                                                     \
       hipError_t e_ = hipFuncSetAttribute(                                                   \
           (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);       \
@@ -1254,18 +1295,22 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
                   p->d_scales, p->d_zp, (int)p->n_blocks, bs_log2, (int)m, (int)p->n, gx,   \
                   gy, d_y);                                                                  \
   }
-#define MMNB_GEMM_NB(NS, GR)                     \
-  {                                              \
-    if (nbps == 1) MMNB_GEMM_LAUNCH(1, NS, GR);  \
-    if (nbps == 2) MMNB_GEMM_LAUNCH(2, NS, GR);  \
-    MMNB_GEMM_LAUNCH(4, NS, GR);                 \
+#define MMNB_GEMM_NB(NS, GR, CB)                     \
+  {                                                  \
+    if (nbps == 1) MMNB_GEMM_LAUNCH(1, NS, GR, CB);  \
+    if (nbps == 2) MMNB_GEMM_LAUNCH(2, NS, GR, CB);  \
+    MMNB_GEMM_LAUNCH(4, NS, GR, CB);                 \
+  }
+  if (cb == 2) {
+    if (groups == 2) MMNB_GEMM_NB(2, 2, 2);
+    MMNB_GEMM_NB(2, 1, 2);
   }
   if (groups == 2) {
-    if (nst == 3) MMNB_GEMM_NB(3, 2);
-    MMNB_GEMM_NB(2, 2);
+    if (nst == 3) MMNB_GEMM_NB(3, 2, 1);
+    MMNB_GEMM_NB(2, 2, 1);
   }
-  if (nst == 3) MMNB_GEMM_NB(3, 1);
-  MMNB_GEMM_NB(2, 1);
+  if (nst == 3) MMNB_GEMM_NB(3, 1, 1);
+  MMNB_GEMM_NB(2, 1, 1);
 #undef MMNB_GEMM_NB
 #undef MMNB_GEMM_LAUNCH
 }

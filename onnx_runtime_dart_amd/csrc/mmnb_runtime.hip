@@ -109,6 +109,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v == 2 || v == 3) ctx->gemm_stages = v;
   }
+  if (const char *r = std::getenv("MMNB_GEMM_CB")) {
+    const int v = std::atoi(r);
+    if (v == 1 || v == 2) ctx->gemm_cb = v;
+  }
   if (const char *r = std::getenv("MMNB_GEMV_CG")) {
     const int v = std::atoi(r);
     if (v >= 1 && v <= 8) ctx->gemv_cg = v;
