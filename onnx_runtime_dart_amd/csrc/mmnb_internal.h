@@ -97,6 +97,11 @@ struct mmnb_pack {
   uint8_t *d_w = nullptr;
   float *d_scales = nullptr;
   uint8_t *d_zp = nullptr;  // packed uint4; 0x88 filler when the op has none
+  // block-major copies for the prefill GEMM: scales [nb][ldsz], zero points
+  // [nb][ldsz], ldsz = n rounded up to 4 (padding zero)
+  float *d_st = nullptr;
+  uint32_t *d_zt = nullptr;
+  int64_t ldsz = 0;
   bool has_zp = false;
   // --- MatMulNBits beyond the reference's 4-bit form (mmnb_pack_nbits_ex):
   // the kernels run on a 4-bit "virtual" weight of k rows (k, n_blocks, d_w,
@@ -276,6 +281,8 @@ int launch_probe_empty(mmnb_ctx *ctx, int blocks);
 int launch_probe_read(mmnb_ctx *ctx, const void *d_buf, size_t bytes);
 
 // Pack construction helpers (device-side repack kernels).
+// Allocates and fills p->d_st / p->d_zt from p->d_scales / p->d_zp.
+int build_gemm_sz(mmnb_ctx *ctx, mmnb_pack *p);
 int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n,
                          int64_t k, int64_t src_col_bytes,
                          int64_t dst_col_bytes, uint8_t *d_dst);

@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "mmnb_device.h"
 #include "mmnb_internal.h"
@@ -87,6 +88,41 @@ int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n, int64_t
                 d_src, n, src_col, dst_col, k, d_dst);
 }
 
+// ---------------------------------------------------------------------------
+// Block-major copies of the scales and zero points for the prefill GEMM:
+// st[b][c] = scales[c][b], zt[b][c] = zero-point nibble (c, b) as a dword, so
+// the columns of one quantisation block that a GEMM tile stages are
+// contiguous (coalesced DMA) instead of nb apart.  One thread per (b, c).
+// ---------------------------------------------------------------------------
+__global__ void k_sz_block_major(const float *__restrict__ S, const uint8_t *__restrict__ Z,
+                                 int64_t n, int64_t nb, int64_t ld, float *__restrict__ st,
+                                 uint32_t *__restrict__ zt) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= ld * nb) return;
+  const int64_t b = idx / ld, c = idx % ld;
+  if (c >= n) {  // row padding
+    st[idx] = 0.0f;
+    zt[idx] = 0u;
+    return;
+  }
+  const int64_t zi = c * nb + b;
+  st[idx] = S[zi];
+  zt[idx] = (uint32_t)(Z[zi >> 1] >> (4 * (zi & 1))) & 0xFu;
+}
+
+int build_gemm_sz(mmnb_ctx *ctx, mmnb_pack *p) {
+  p->ldsz = (p->n + 3) / 4 * 4;
+  const int64_t total = p->ldsz * p->n_blocks;
+  int rc;
+  if ((rc = device_alloc((size_t)total * 4, (void **)&p->d_st))) return rc;
+  if ((rc = device_alloc((size_t)total * 4, (void **)&p->d_zt))) return rc;
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  return launch(ctx, kKernRepack, k_sz_block_major, dim3((unsigned)blocks), dim3(threads), 0,
+                (const float *)p->d_scales, (const uint8_t *)p->d_zp, p->n, p->n_blocks,
+                p->ldsz, p->d_st, p->d_zt);
+}
+
 // (a & mask) | orv in one VALU op.  gfx9 VOP3 takes no literal, so the
 // compiler splits this into v_and + v_or; with the mask in an SGPR and the
 // magic in a VGPR it is one v_and_or_b32.
@@ -108,10 +144,9 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) 
   const uint32_t w8 = w >> 8;
   const uint32_t t2 = and_or(w8, 0x000F000Fu, magic);
   const uint32_t t3 = and_or(w8, 0x00F000F0u, magic);
-  const _Float16 z1024 = (_Float16)(1024 + zp);
-  const _Float16 z64 = (_Float16)(64 + zp);
-  const half2_t zz = {z1024, z1024};
-  const half2_t zs = {z64, z64};
+  // 1024 + zp and 64 + zp (zp <= 15) as fp16 bits: ulp 1 at 1024, 1/16 at 64
+  const half2_t zz = __builtin_bit_cast(half2_t, (uint32_t)(0x6400 + zp) * 0x10001u);
+  const half2_t zs = __builtin_bit_cast(half2_t, (uint32_t)(0x5400 + (zp << 4)) * 0x10001u);
   const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
   const half2_t h0 = __builtin_bit_cast(half2_t, t0) - zz;
   const half2_t h1 = __builtin_bit_cast(half2_t, t1) * sixteenth - zs;
@@ -993,26 +1028,27 @@ __global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int
 // ---------------------------------------------------------------------------
 // Prefill GEMM, fed by direct global->LDS DMA.
 //
-// Workgroup tile 64 (M) x 128 (N).  A group of 4 waves in 1 x 4 owns the
-// tile over a range of K: wave tile 64 x 32 (both 32-row A blocks, one
-// 32-column weight block, so every weight is dequantised once per group).
-// GROUPS = 2 splits K between two such groups (8 waves, two per SIMD, so one
-// wave's MFMAs overlap the other's vector work) when the tiles alone leave a
-// single wave per SIMD; the partial tiles are summed through LDS at the end.
+// Workgroup tile 64 (M) x 128*CB (N).  A group of 4 waves in 1 x 4 owns the
+// tile over a range of K: wave tile 64 x 32*CB (both 32-row A blocks, CB
+// 32-column weight blocks, so every weight is dequantised once per group and
+// every A fragment read from LDS feeds CB column blocks).  GROUPS = 2 splits
+// K between two such groups (8 waves, two per SIMD) when the tiles alone
+// leave a single wave per SIMD; the partial tiles are summed through LDS at
+// the end.
 //
 // Every operand of a 64-k segment -- the prepared activations (16 KB), the
-// packed weights (128 columns x 32 B), the tile's scales and the dwords that
-// hold its zero points (128 x NBPS each) -- is copied by global_load_lds into
-// one of NST LDS stages, so NST-1 segments are in flight without a register
-// round trip.  Every thread issues the same number of DMA loads per stage
-// (kL), so "stage s has landed" is vmcnt <= (NST-2)*kL once the next stages
-// are issued; a barrier then publishes the stage to all waves.
+// packed weights (128*CB columns x 32 B), the tile's scales and zero points
+// (from block-major copies, so one block's columns are contiguous and move
+// as 16 B per lane) -- is copied by global_load_lds into one of NST LDS
+// stages, so NST-1 segments are in flight without a register round trip.
+// Every thread issues the same number of DMA loads per stage (kL), so "stage
+// s has landed" is vmcnt <= (NST-2)*kL once the next stages are issued; a
+// barrier then publishes the stage to all waves.
 //
-// Each 16-k step issues 2 (row blocks) x 2 (hi, lo) v_mfma_f32_32x32x16_f16
-// into per-block partials D; at each quantisation block boundary
-// acc += scale[n, blk] * D.  Blocks that end inside a segment (block 16, 32)
-// start with a zero accumulator input and alternate between two partial
-// sets, so one block's epilogue can overlap the next block's MFMAs.
+// Each 16-k step issues 2 (row blocks) x CB x 2 (hi, lo)
+// v_mfma_f32_32x32x16_f16 into the partial set of its quantisation block
+// (zero accumulator input at the block's first step); acc += scale[n, blk]
+// * partials is applied while the next block's MFMAs run (two sets).
 // ---------------------------------------------------------------------------
 constexpr int kGemmBM = 64;   // two 32-row blocks
 constexpr int kGemmBN = 128;  // four 32-column blocks
@@ -1023,15 +1059,16 @@ constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 template <int NBPS, int NST, int GROUPS, int CB>
-__global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
+__global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_mfma(
     const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs, int segsp,
-    const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S,
-    const uint8_t *__restrict__ Z, int nb, int bs_log2, int M, int N, int grid_x, int grid_y,
-    float *__restrict__ Y) {
+    const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ ST,
+    const uint32_t *__restrict__ ZT, int ldsz, int nb, int bs_log2, int M, int N, int grid_x,
+    int grid_y, float *__restrict__ Y) {
   constexpr int kBN = kGemmBN * CB;                    // columns per workgroup tile
   constexpr int kSz = kBN * NBPS;                       // scale (and zero-point) dwords per stage
   constexpr int kStageU4 = 1024 + 256 * CB + kSz / 2;   // uint4 per stage: A, W, scales + zp
-  constexpr int kL = 4 + CB + CB * NBPS;                // DMA loads per thread per stage
+  constexpr int kSzI = CB * NBPS / 4 > 0 ? CB * NBPS / 4 : 1;  // 1 KB scale/zp loads per wave
+  constexpr int kL = 4 + CB + kSzI;                     // DMA loads per thread per stage
   constexpr int kSOff = 1024 + 256 * CB;                // scales / zero points in a stage
   extern __shared__ uint4 smem_all[];
   // wave-uniform indices in scalar registers
@@ -1076,29 +1113,34 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     const int wcol = min(n0 + 128 * i + (tid >> 1), N - 1);
     w_base[i] = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
   }
-  // scale / zero-point slots of this thread: slot = tid + 256 i, i < NBPS;
-  // slots [0, kSz) are scales, [kSz, 2 kSz) zero-point dwords, each indexed
-  // (column c, block q) as c * NBPS + q.
-  int sz_col[CB * NBPS], sz_q[CB * NBPS];
-  bool sz_isz[CB * NBPS];
+  // Scale / zero-point dword slots of a stage: [0, kSz) scales, [kSz, 2 kSz)
+  // zero points, each indexed (block q, column c) as q * kBN + c.  They move
+  // in 1 KB chunks (256 slots, 4 consecutive columns per lane, 16 B loads
+  // from the block-major copies, whose rows are ldsz = N rounded up to 4
+  // apart): wave w loads chunks w, w + 4, ... of the 2 kSz / 256; with fewer
+  // chunks than waves the extra waves repeat one (same data, same place).
+  constexpr int kSzChunks = 2 * kSz / 256;
+  int sz_col[kSzI], sz_q[kSzI], sz_chunk[kSzI];
+  bool sz_isz[kSzI];
 #pragma unroll
-  for (int i = 0; i < CB * NBPS; i++) {
-    int slot = tid + 256 * i;
+  for (int i = 0; i < kSzI; i++) {
+    sz_chunk[i] = (wave + 4 * i) % kSzChunks;
+    int slot = sz_chunk[i] * 256 + 4 * lane;
     sz_isz[i] = slot >= kSz;
     if (sz_isz[i]) slot -= kSz;
-    sz_col[i] = min(n0 + slot / NBPS, N - 1);
-    sz_q[i] = slot % NBPS;
+    sz_col[i] = min(n0 + slot % kBN, ldsz - 4);
+    sz_q[i] = slot / kBN;
   }
 
   // this lane's output columns (CB 32-column blocks of the wave)
-  int col[CB], my_slot[CB];
+  int col[CB], my_c[CB];
   bool colok[CB];
 #pragma unroll
   for (int cb = 0; cb < CB; cb++) {
     const int ccol = n0 + (wave * CB + cb) * 32 + cl;
     colok[cb] = ccol < N;
     col[cb] = colok[cb] ? ccol : N - 1;
-    my_slot[cb] = ((wave * CB + cb) * 32 + cl) * NBPS;
+    my_c[cb] = (wave * CB + cb) * 32 + cl;
   }
 
   auto issue = [&](int seg, int buf) {
@@ -1116,34 +1158,43 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
     }
     uint32_t *sz = (uint32_t *)(st + kSOff);
 #pragma unroll
-    for (int i = 0; i < CB * NBPS; i++) {
+    for (int i = 0; i < kSzI; i++) {
       const int blk = (sa_ * kSegK + sz_q[i] * (kSegK / NBPS)) >> bs_log2;
       const int b2 = blk < nb ? blk : nb - 1;
-      const int zi = sz_col[i] * nb + b2;
-      const void *src = sz_isz[i] ? (const void *)(Z + ((zi >> 1) & ~3))
-                                  : (const void *)(S + zi);
-      __builtin_amdgcn_global_load_lds(src, sz + 256 * i + 64 * wave, 4, 0, 0);
+      const size_t zi = (size_t)b2 * ldsz + sz_col[i];
+      const void *src = sz_isz[i] ? (const void *)(ZT + zi) : (const void *)(ST + zi);
+      uint32_t *dst = sz + 256 * sz_chunk[i];
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
     }
   };
 
-  constexpr int kDSets = NBPS > 1 ? 2 : 1;
-  float16_t acc[2][CB], D[kDSets][2][CB];
+  // Two partial sets D[0], D[1].  A quantisation block's MFMAs accumulate
+  // into one set while the previous block's partials (the other set) are
+  // scaled into acc, so the epilogue FMAs overlap MFMAs instead of waiting
+  // for them.  With NBPS blocks per stage the sets alternate by block; with
+  // one block or less per stage (NBPS == 1) every stage is its own partial,
+  // scaled by its block's scale, and the sets alternate by stage parity.
+  float16_t acc[2][CB], D[2][2][CB];
+  float pend[CB];  // scale of the set awaiting its epilogue (0 before the first)
   const float16_t zero16 = {};
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++)
+    for (int cb = 0; cb < CB; cb++) {
+      pend[cb] = 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         acc[t][cb][r] = 0.0f;
-#pragma unroll
-        for (int ds = 0; ds < kDSets; ds++) D[ds][t][cb][r] = 0.0f;
+        D[0][t][cb][r] = 0.0f;
+        D[1][t][cb][r] = 0.0f;
       }
+    }
 
 #pragma unroll
   for (int p = 0; p < NST - 1; p++) issue(sbeg + p, p);
   int buf = 0;
-  for (int seg = sbeg; seg < sbeg + nseg; seg++) {
+  auto stage = [&](const int seg, auto parity) __attribute__((always_inline)) {
+    constexpr int P = decltype(parity)::value;
     // this thread's DMA for stage `seg` has landed; the barrier (without a
     // fence, which would wait for every outstanding load) makes all of it
     // visible, and frees the stage computed in the previous iteration
@@ -1162,50 +1213,86 @@ __global__ __launch_bounds__(256 * GROUPS) void k_gemm_mfma(
 #pragma unroll
       for (int q = 0; q < NBPS; q++) {
         const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
-        const int b2 = blk < nb ? blk : nb - 1;
-        const int zi = col[cb] * nb + b2;
-        const uint32_t zd = sS[kSz + my_slot[cb] + q];
-        const float sv = __builtin_bit_cast(float, sS[my_slot[cb] + q]);
-        zpv[cb][q] = (int)((zd >> (8 * ((zi >> 1) & 3) + 4 * (zi & 1))) & 0xF);
+        const float sv = __builtin_bit_cast(float, sS[q * kBN + my_c[cb]]);
+        zpv[cb][q] = (int)sS[kSz + q * kBN + my_c[cb]];
         scv[cb][q] = blk < nb ? sv : 0.0f;
       }
     }
+    // with one column block per wave every A fragment of the stage is read
+    // up front (16 x 16 B per lane), so the MFMAs wait on in-order LDS
+    // returns instead of one read each; two blocks read them per k step
+    constexpr int kPre = CB == 1 ? 4 : 1;
+    half8_t af[kPre][2][2];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int q = j / (4 / NBPS);
-      const int ds = (NBPS > 1) ? (q & 1) : 0;
+      if (CB == 1 ? j == 0 : true) {
+#pragma unroll
+        for (int jj = 0; jj < kPre; jj++)
+#pragma unroll
+          for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+              af[jj][rb][h] = __builtin_bit_cast(
+                  half8_t, sAv[(rb * 8 + (j + jj) * 2 + h) * 64 + lane]);
+      }
+      const int jf = CB == 1 ? j : 0;
+      constexpr int kJB = 4 / NBPS;  // k steps per block (NBPS > 1)
+      const int q = j / kJB;
+      const bool first = (j % kJB) == 0;
       half8_t b[CB];
 #pragma unroll
       for (int cb = 0; cb < CB; cb++) b[cb] = dequant8(wv[cb][j], zpv[cb][q], magic);
-      const bool fresh = (NBPS > 1) && ((j % (4 / NBPS)) == 0);
-#pragma unroll
-      for (int rb = 0; rb < 2; rb++) {
-        const half8_t ah = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + 0) * 64 + lane]);
-        const half8_t al = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + 1) * 64 + lane]);
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) {
-          D[ds][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              ah, b[cb], fresh ? zero16 : D[ds][rb][cb], 0, 0, 0);
-          D[ds][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b[cb], D[ds][rb][cb], 0, 0, 0);
-        }
-      }
-      const bool boundary = (NBPS > 1)
-                                ? (((j + 1) % (4 / NBPS)) == 0)
-                                : (j == 3 && (((seg + 1) * kSegK) & ((1 << bs_log2) - 1)) == 0);
-      if (boundary) {
+      // set S takes this block; the other set holds the block before it
+      auto mma = [&](auto set) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-          for (int cb = 0; cb < CB; cb++)
+          for (int cb = 0; cb < CB; cb++) {
+            D[S][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                af[jf][rb][0], b[cb], first ? zero16 : D[S][rb][cb], 0, 0, 0);
+            D[S][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[jf][rb][1], b[cb],
+                                                                  D[S][rb][cb], 0, 0, 0);
+          }
+        if (first) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-              acc[rb][cb][r] = fmaf(scv[cb][q], D[ds][rb][cb][r], acc[rb][cb][r]);
-              if (NBPS == 1) D[ds][rb][cb][r] = 0.0f;
-            }
+          for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+              for (int r = 0; r < 16; r++)
+                acc[rb][cb][r] = fmaf(pend[cb], D[1 - S][rb][cb][r], acc[rb][cb][r]);
+        }
+      };
+      if (NBPS > 1 ? (q & 1) : P)
+        mma(std::integral_constant<int, 1>());
+      else
+        mma(std::integral_constant<int, 0>());
+      if ((j + 1) % kJB == 0) {
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) pend[cb] = scv[cb][q];
       }
     }
     if (++buf == NST) buf = 0;
+  };
+  if constexpr (NBPS > 1) {
+    for (int seg = sbeg; seg < sbeg + nseg; seg++) stage(seg, std::integral_constant<int, 0>());
+  } else {
+    for (int seg = sbeg; seg < sbeg + nseg; seg += 2) {
+      stage(seg, std::integral_constant<int, 0>());
+      if (seg + 1 < sbeg + nseg) stage(seg + 1, std::integral_constant<int, 1>());
+    }
   }
+  // the last block's partials: set 1 unless NBPS == 1 and the stage count is odd
+  const bool last1 = NBPS > 1 || (nseg & 1) == 0;
+#pragma unroll
+  for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+    for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        acc[rb][cb][r] = fmaf(pend[cb], last1 ? D[1][rb][cb][r] : D[0][rb][cb][r],
+                              acc[rb][cb][r]);
   // drain the DMA still in flight (clamped stages past the end) before the
   // LDS is reused or the workgroup exits
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -1256,9 +1343,9 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   const int gy = (int)(mpad / kGemmBM);
   // 256-column tiles (each wave two 32-column blocks, so every A fragment
   // read from LDS feeds twice the MFMAs and A streams half as often) when
-  // there are at least 1.5 such tiles per CU (measured: 448 tiles on 256 CUs
-  // gain 8%, 256 tiles lose 3%); 128 otherwise.
-  int cb = ((p->n + 2 * kGemmBN - 1) / (2 * kGemmBN)) * gy >= 3 * ctx->cu_count / 2 ? 2 : 1;
+  // there is at least one such tile per CU (measured on 256 CUs: 256 tiles
+  // gain 7%, 448 tiles 8%; 128 tiles lose 40%); 128 otherwise.
+  int cb = ((p->n + 2 * kGemmBN - 1) / (2 * kGemmBN)) * gy >= ctx->cu_count ? 2 : 1;
   if (ctx->gemm_cb) cb = ctx->gemm_cb;
   const int gx = (int)((p->n + cb * kGemmBN - 1) / (cb * kGemmBN));
   const int nbps = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
@@ -1292,7 +1379,8 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
     }                                                                                        \
     return launch(ctx, kKernGemm, kern, grid, dim3(256 * GR), shmem, (const uint4 *)d_ap,   \
                   (const int *)d_exp, (int)segs, (int)segsp, p->d_w, p->col_bytes,          \
-                  p->d_scales, p->d_zp, (int)p->n_blocks, bs_log2, (int)m, (int)p->n, gx,   \
+                  p->d_st, p->d_zt, (int)p->ldsz, (int)p->n_blocks, bs_log2, (int)m,        \
+                  (int)p->n, gx,                                                             \
                   gy, d_y);                                                                  \
   }
 #define MMNB_GEMM_NB(NS, GR, CB)                     \

@@ -201,6 +201,8 @@ int mmnb::pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales
     if (p->d_w) (void)hipFree(p->d_w);
     if (p->d_scales) (void)hipFree(p->d_scales);
     if (p->d_zp) (void)hipFree(p->d_zp);
+    if (p->d_st) (void)hipFree(p->d_st);
+    if (p->d_zt) (void)hipFree(p->d_zt);
     delete p;
     return code;
   };
@@ -230,9 +232,10 @@ int mmnb::pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales
              hipSuccess) {
     return cleanup(check_hip(e, "hipMemsetAsync(zero_points)"));
   }
+  if ((rc = build_gemm_sz(ctx, p))) return cleanup(rc);
   if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
     return cleanup(check_hip(e, "hipStreamSynchronize(pack)"));
-  p->bytes = (int64_t)wbytes + n * nb * 4 + zp_need;
+  p->bytes = (int64_t)wbytes + n * nb * 4 + zp_need + p->ldsz * nb * 8;
   p->k_in = k;
   ctx->live_packs++;
   *out = p;
@@ -579,6 +582,8 @@ int mmnb_pack_free(mmnb_pack *p) {
     if (p->d_w) (void)hipFree(p->d_w);
     if (p->d_scales) (void)hipFree(p->d_scales);
     if (p->d_zp) (void)hipFree(p->d_zp);
+    if (p->d_st) (void)hipFree(p->d_st);
+    if (p->d_zt) (void)hipFree(p->d_zt);
     if (p->d_bt) (void)hipFree(p->d_bt);
     if (p->d_colsum) (void)hipFree(p->d_colsum);
     if (p->d_ecol) (void)hipFree(p->d_ecol);
