@@ -1070,6 +1070,7 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int kSzI = CB * NBPS / 4 > 0 ? CB * NBPS / 4 : 1;  // 1 KB scale/zp loads per wave
   constexpr int kL = 4 + CB + kSzI;                     // DMA loads per thread per stage
   constexpr int kSOff = 1024 + 256 * CB;                // scales / zero points in a stage
+  constexpr bool kPingPong = GROUPS == 2 && CB == 1;
   extern __shared__ uint4 smem_all[];
   // wave-uniform indices in scalar registers
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1168,131 +1169,278 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     }
   };
 
-  // Two partial sets D[0], D[1].  A quantisation block's MFMAs accumulate
-  // into one set while the previous block's partials (the other set) are
-  // scaled into acc, so the epilogue FMAs overlap MFMAs instead of waiting
-  // for them.  With NBPS blocks per stage the sets alternate by block; with
-  // one block or less per stage (NBPS == 1) every stage is its own partial,
-  // scaled by its block's scale, and the sets alternate by stage parity.
-  float16_t acc[2][CB], D[2][2][CB];
-  float pend[CB];  // scale of the set awaiting its epilogue (0 before the first)
+  float16_t acc[2][CB];
   const float16_t zero16 = {};
 #pragma unroll
   for (int t = 0; t < 2; t++)
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) {
-      pend[cb] = 0.0f;
+    for (int cb = 0; cb < CB; cb++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        acc[t][cb][r] = 0.0f;
-        D[0][t][cb][r] = 0.0f;
-        D[1][t][cb][r] = 0.0f;
-      }
-    }
+      for (int r = 0; r < 16; r++) acc[t][cb][r] = 0.0f;
+  // the DMA ring slot of stage seg + NST - 1 (the one computed before seg)
+  auto next_buf = [](int b) { return b == 0 ? NST - 1 : b - 1; };
 
+  if constexpr (kPingPong) {
+    // Ping-pong: each stage is a vector phase (scale / zero-point reads,
+    // dequantisation of the stage's weights, the previous stage's block
+    // epilogues) and a matrix phase (A fragment reads and the MFMAs).  The
+    // two K groups run them half a stage apart, separated by workgroup
+    // barriers, so on every SIMD one group's wave issues MFMAs while the
+    // other group's wave runs its vector phase:
+    //   group 0: wait(s)  B  issue(s+1) V(s)  B  M(s)
+    //   group 1:          B  M(s-1) wait(s)  B  issue(s+1) V(s)
+    // Both run the same number of barriers (two per stage and one after the
+    // loop).  A stage slot is refilled only after the barrier that follows
+    // the group's last read of it; a stage is read only after the barrier
+    // that follows every wave's wait for its own DMA of it.
+    constexpr int kJB = 4 / NBPS;   // k steps per quantisation block
+    float16_t P[NBPS][2][CB];       // partials of the stage's blocks
+    float psc[CB][NBPS];            // their scales (0 before the first stage)
+    half8_t bq[4][CB];              // the stage's dequantised weights
 #pragma unroll
-  for (int p = 0; p < NST - 1; p++) issue(sbeg + p, p);
-  int buf = 0;
-  auto stage = [&](const int seg, auto parity) __attribute__((always_inline)) {
-    constexpr int P = decltype(parity)::value;
-    // this thread's DMA for stage `seg` has landed; the barrier (without a
-    // fence, which would wait for every outstanding load) makes all of it
-    // visible, and frees the stage computed in the previous iteration
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kL));
-    __builtin_amdgcn_s_barrier();
-    issue(seg + NST - 1, buf == 0 ? NST - 1 : buf - 1);
-    const uint4 *st = smem + buf * kStageU4;
-    const u4vec *sAv = (const u4vec *)st;
-    const uint32_t *sS = (const uint32_t *)(st + kSOff);
-    u4vec wv[CB];
-    int zpv[CB][NBPS];
-    float scv[CB][NBPS];
+    for (int q = 0; q < NBPS; q++)
 #pragma unroll
-    for (int cb = 0; cb < CB; cb++) {
-      wv[cb] = ((const u4vec *)(st + 1024))[((wave * CB + cb) * 32 + cl) * 2 + g];
+      for (int cb = 0; cb < CB; cb++) {
+        psc[cb][q] = 0.0f;
 #pragma unroll
-      for (int q = 0; q < NBPS; q++) {
-        const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
-        const float sv = __builtin_bit_cast(float, sS[q * kBN + my_c[cb]]);
-        zpv[cb][q] = (int)sS[kSz + q * kBN + my_c[cb]];
-        scv[cb][q] = blk < nb ? sv : 0.0f;
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) P[q][t][cb][r] = 0.0f;
       }
-    }
-    // with one column block per wave every A fragment of the stage is read
-    // up front (16 x 16 B per lane), so the MFMAs wait on in-order LDS
-    // returns instead of one read each; two blocks read them per k step
-    constexpr int kPre = CB == 1 ? 4 : 1;
-    half8_t af[kPre][2][2];
+    auto vphase = [&](const int seg, const int b) __attribute__((always_inline)) {
+      const uint4 *st = smem + b * kStageU4;
+      const uint32_t *sS = (const uint32_t *)(st + kSOff);
+      u4vec wv[CB];
+      int zpv[CB][NBPS];
+      float scv[CB][NBPS];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      if (CB == 1 ? j == 0 : true) {
+      for (int cb = 0; cb < CB; cb++) {
+        wv[cb] = ((const u4vec *)(st + 1024))[((wave * CB + cb) * 32 + cl) * 2 + g];
 #pragma unroll
-        for (int jj = 0; jj < kPre; jj++)
-#pragma unroll
-          for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-              af[jj][rb][h] = __builtin_bit_cast(
-                  half8_t, sAv[(rb * 8 + (j + jj) * 2 + h) * 64 + lane]);
+        for (int q = 0; q < NBPS; q++) {
+          const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
+          const float sv = __builtin_bit_cast(float, sS[q * kBN + my_c[cb]]);
+          zpv[cb][q] = (int)sS[kSz + q * kBN + my_c[cb]];
+          scv[cb][q] = blk < nb ? sv : 0.0f;
+        }
       }
-      const int jf = CB == 1 ? j : 0;
-      constexpr int kJB = 4 / NBPS;  // k steps per block (NBPS > 1)
-      const int q = j / kJB;
-      const bool first = (j % kJB) == 0;
-      half8_t b[CB];
 #pragma unroll
-      for (int cb = 0; cb < CB; cb++) b[cb] = dequant8(wv[cb][j], zpv[cb][q], magic);
-      // set S takes this block; the other set holds the block before it
-      auto mma = [&](auto set) __attribute__((always_inline)) {
-        constexpr int S = decltype(set)::value;
+      for (int q = 0; q < NBPS; q++)
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+          for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+              acc[rb][cb][r] = fmaf(psc[cb][q], P[q][rb][cb][r], acc[rb][cb][r]);
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for (int q = 0; q < NBPS; q++) psc[cb][q] = scv[cb][q];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) bq[j][cb] = dequant8(wv[cb][j], zpv[cb][j / kJB], magic);
+    };
+    auto mphase = [&](const int b) __attribute__((always_inline)) {
+      const u4vec *sAv = (const u4vec *)(smem + b * kStageU4);
+      half8_t af[4][2][2];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+            af[j][rb][h] = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + h) * 64 + lane]);
+      // all 16 reads are issued before the first MFMA (one wait, then the
+      // MFMAs back to back) instead of the scheduler's read-wait-MFMA pairs
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int q = j / kJB;
+        const bool first = (j % kJB) == 0;
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
           for (int cb = 0; cb < CB; cb++) {
-            D[S][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                af[jf][rb][0], b[cb], first ? zero16 : D[S][rb][cb], 0, 0, 0);
-            D[S][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[jf][rb][1], b[cb],
-                                                                  D[S][rb][cb], 0, 0, 0);
+            P[q][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                af[j][rb][0], bq[j][cb], first ? zero16 : P[q][rb][cb], 0, 0, 0);
+            P[q][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j][rb][1], bq[j][cb],
+                                                                  P[q][rb][cb], 0, 0, 0);
           }
-        if (first) {
+      }
+    };
+    // the scheduler may not move any instruction across a phase boundary
+    // (s_barrier alone orders only memory operations)
+    auto phase_barrier = []() __attribute__((always_inline)) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int p = 0; p < NST - 1; p++) issue(sbeg + p, p);
+    int buf = 0;
+    if (grp == 0) {
+      for (int seg = sbeg; seg < sbeg + nseg; seg++) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kL));
+        phase_barrier();
+        issue(seg + NST - 1, next_buf(buf));
+        vphase(seg, buf);
+        phase_barrier();
+        mphase(buf);
+        if (++buf == NST) buf = 0;
+      }
+      phase_barrier();
+    } else {
+      int prev = 0;
+      for (int seg = sbeg; seg < sbeg + nseg; seg++) {
+        __builtin_amdgcn_s_barrier();
+        if (seg > sbeg) mphase(prev);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kL));
+        __builtin_amdgcn_s_barrier();
+        issue(seg + NST - 1, next_buf(buf));
+        vphase(seg, buf);
+        prev = buf;
+        if (++buf == NST) buf = 0;
+      }
+      __builtin_amdgcn_s_barrier();
+      mphase(prev);
+    }
+    // the last stage's blocks
+#pragma unroll
+    for (int q = 0; q < NBPS; q++)
+#pragma unroll
+      for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            acc[rb][cb][r] = fmaf(psc[cb][q], P[q][rb][cb][r], acc[rb][cb][r]);
+  } else {
+    // Two partial sets D[0], D[1].  A quantisation block's MFMAs accumulate
+    // into one set while the previous block's partials (the other set) are
+    // scaled into acc, so the epilogue FMAs overlap MFMAs instead of waiting
+    // for them.  With NBPS blocks per stage the sets alternate by block; with
+    // one block or less per stage (NBPS == 1) every stage is its own partial,
+    // scaled by its block's scale, and the sets alternate by stage parity.
+    float16_t D[2][2][CB];
+    float pend[CB];  // scale of the set awaiting its epilogue (0 before the first)
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++) {
+        pend[cb] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          D[0][t][cb][r] = 0.0f;
+          D[1][t][cb][r] = 0.0f;
+        }
+      }
+
+#pragma unroll
+    for (int p = 0; p < NST - 1; p++) issue(sbeg + p, p);
+    int buf = 0;
+    auto stage = [&](const int seg, auto parity) __attribute__((always_inline)) {
+      constexpr int P = decltype(parity)::value;
+      // this thread's DMA for stage `seg` has landed; the barrier (without a
+      // fence, which would wait for every outstanding load) makes all of it
+      // visible, and frees the stage computed in the previous iteration
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * kL));
+      __builtin_amdgcn_s_barrier();
+      issue(seg + NST - 1, buf == 0 ? NST - 1 : buf - 1);
+      const uint4 *st = smem + buf * kStageU4;
+      const u4vec *sAv = (const u4vec *)st;
+      const uint32_t *sS = (const uint32_t *)(st + kSOff);
+      u4vec wv[CB];
+      int zpv[CB][NBPS];
+      float scv[CB][NBPS];
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++) {
+        wv[cb] = ((const u4vec *)(st + 1024))[((wave * CB + cb) * 32 + cl) * 2 + g];
+#pragma unroll
+        for (int q = 0; q < NBPS; q++) {
+          const int blk = (seg * kSegK + q * (kSegK / NBPS)) >> bs_log2;
+          const float sv = __builtin_bit_cast(float, sS[q * kBN + my_c[cb]]);
+          zpv[cb][q] = (int)sS[kSz + q * kBN + my_c[cb]];
+          scv[cb][q] = blk < nb ? sv : 0.0f;
+        }
+      }
+      // with one column block per wave every A fragment of the stage is read
+      // up front (16 x 16 B per lane), so the MFMAs wait on in-order LDS
+      // returns instead of one read each; two blocks read them per k step
+      constexpr int kPre = CB == 1 ? 4 : 1;
+      half8_t af[kPre][2][2];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if (CB == 1 ? j == 0 : true) {
+#pragma unroll
+          for (int jj = 0; jj < kPre; jj++)
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+              for (int h = 0; h < 2; h++)
+                af[jj][rb][h] = __builtin_bit_cast(
+                    half8_t, sAv[(rb * 8 + (j + jj) * 2 + h) * 64 + lane]);
+        }
+        const int jf = CB == 1 ? j : 0;
+        constexpr int kJB = 4 / NBPS;  // k steps per block (NBPS > 1)
+        const int q = j / kJB;
+        const bool first = (j % kJB) == 0;
+        half8_t b[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; cb++) b[cb] = dequant8(wv[cb][j], zpv[cb][q], magic);
+        // set S takes this block; the other set holds the block before it
+        auto mma = [&](auto set) __attribute__((always_inline)) {
+          constexpr int S = decltype(set)::value;
 #pragma unroll
           for (int rb = 0; rb < 2; rb++)
 #pragma unroll
-            for (int cb = 0; cb < CB; cb++)
+            for (int cb = 0; cb < CB; cb++) {
+              D[S][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                  af[jf][rb][0], b[cb], first ? zero16 : D[S][rb][cb], 0, 0, 0);
+              D[S][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[jf][rb][1], b[cb],
+                                                                    D[S][rb][cb], 0, 0, 0);
+            }
+          if (first) {
 #pragma unroll
-              for (int r = 0; r < 16; r++)
-                acc[rb][cb][r] = fmaf(pend[cb], D[1 - S][rb][cb][r], acc[rb][cb][r]);
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+              for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                  acc[rb][cb][r] = fmaf(pend[cb], D[1 - S][rb][cb][r], acc[rb][cb][r]);
+          }
+        };
+        if (NBPS > 1 ? (q & 1) : P)
+          mma(std::integral_constant<int, 1>());
+        else
+          mma(std::integral_constant<int, 0>());
+        if ((j + 1) % kJB == 0) {
+#pragma unroll
+          for (int cb = 0; cb < CB; cb++) pend[cb] = scv[cb][q];
         }
-      };
-      if (NBPS > 1 ? (q & 1) : P)
-        mma(std::integral_constant<int, 1>());
-      else
-        mma(std::integral_constant<int, 0>());
-      if ((j + 1) % kJB == 0) {
-#pragma unroll
-        for (int cb = 0; cb < CB; cb++) pend[cb] = scv[cb][q];
+      }
+      if (++buf == NST) buf = 0;
+    };
+    if constexpr (NBPS > 1) {
+      for (int seg = sbeg; seg < sbeg + nseg; seg++) stage(seg, std::integral_constant<int, 0>());
+    } else {
+      for (int seg = sbeg; seg < sbeg + nseg; seg += 2) {
+        stage(seg, std::integral_constant<int, 0>());
+        if (seg + 1 < sbeg + nseg) stage(seg + 1, std::integral_constant<int, 1>());
       }
     }
-    if (++buf == NST) buf = 0;
-  };
-  if constexpr (NBPS > 1) {
-    for (int seg = sbeg; seg < sbeg + nseg; seg++) stage(seg, std::integral_constant<int, 0>());
-  } else {
-    for (int seg = sbeg; seg < sbeg + nseg; seg += 2) {
-      stage(seg, std::integral_constant<int, 0>());
-      if (seg + 1 < sbeg + nseg) stage(seg + 1, std::integral_constant<int, 1>());
-    }
+    // the last block's partials: set 1 unless NBPS == 1 and the stage count is odd
+    const bool last1 = NBPS > 1 || (nseg & 1) == 0;
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+      for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          acc[rb][cb][r] = fmaf(pend[cb], last1 ? D[1][rb][cb][r] : D[0][rb][cb][r],
+                                acc[rb][cb][r]);
   }
-  // the last block's partials: set 1 unless NBPS == 1 and the stage count is odd
-  const bool last1 = NBPS > 1 || (nseg & 1) == 0;
-#pragma unroll
-  for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-    for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-      for (int r = 0; r < 16; r++)
-        acc[rb][cb][r] = fmaf(pend[cb], last1 ? D[1][rb][cb][r] : D[0][rb][cb][r],
-                              acc[rb][cb][r]);
   // drain the DMA still in flight (clamped stages past the end) before the
   // LDS is reused or the workgroup exits
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
