@@ -38,6 +38,7 @@ namespace mmnb {
 constexpr int kSegK = 64;        // k per 32-byte segment
 constexpr int kSegBytes = 32;
 constexpr size_t kTailPad = 1024;  // bytes of slack after every device buffer
+constexpr int kGemmMaxSplitTiles = 1024;  // tiles of a K-sliced prefill GEMM
 
 enum PackKind { kPackNBits = 1, kPackInteger = 2, kPackConv = 3 };
 
@@ -61,8 +62,9 @@ struct mmnb_ctx {
   //  (fp16 hi/lo), 3: small reductions, 4: raw weights while packing,
   //  5: small uploads (zero points), 6: convolution im2col rows, 7: block
   //  sums / the convolution's input zero point, 8: QLinearConv per-channel
-  //  parameters, 9: gathered activations of an extended MatMulNBits pack.
-  mmnb::Scratch scratch[10];
+  //  parameters, 9: gathered activations of an extended MatMulNBits pack,
+  //  10: the prefill GEMM's K-slice partial tiles.
+  mmnb::Scratch scratch[11];
   int live_packs = 0;
   // Kernel timing mode: launches go through hipExtLaunchKernelGGL with a
   // start/stop event pair taken from the dispatch itself.
@@ -73,6 +75,9 @@ struct mmnb_ctx {
   // 4 KB device page: 1 KB of 0x00 and 1 KB of 0x80 (int8 padding), then a
   // 2 KB sink for the calibration kernels.
   void *d_pad = nullptr;
+  // Per-tile arrival counters of the prefill GEMM's K slices (kGemmMaxSplitTiles
+  // ints, zero at rest: the last slice of a tile resets its counter).
+  int *d_gemm_cnt = nullptr;
   // Tuning override of the GEMV columns-per-lane R (MMNB_GEMV_R; 0 = auto).
   int gemv_r = 0;
   // Tuning override of the multi-row GEMV column groups per workgroup
@@ -82,6 +87,8 @@ struct mmnb_ctx {
   int gemm_stages = 2;
   // Prefill GEMM 128-column blocks per tile (MMNB_GEMM_CB: 1 or 2; 0 = auto).
   int gemm_cb = 0;
+  // Prefill GEMM K slices per tile (MMNB_GEMM_KSPLIT: 1, 2, 4 or 8; 0 = auto).
+  int gemm_ksplit = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
 };

@@ -1063,7 +1063,8 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     const uint4 *__restrict__ Ap, const int *__restrict__ row_exp, int segs, int segsp,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ ST,
     const uint32_t *__restrict__ ZT, int ldsz, int nb, int bs_log2, int M, int N, int grid_x,
-    int grid_y, float *__restrict__ Y) {
+    int grid_y, float *__restrict__ Y, int ksplit, float *__restrict__ part,
+    int *__restrict__ tile_cnt) {
   constexpr int kBN = kGemmBN * CB;                    // columns per workgroup tile
   constexpr int kSz = kBN * NBPS;                       // scale (and zero-point) dwords per stage
   constexpr int kStageU4 = 1024 + 256 * CB + kSz / 2;   // uint4 per stage: A, W, scales + zp
@@ -1079,16 +1080,20 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   const int cl = lane & 31, g = lane >> 5;
   const uint32_t magic = 0x64006400u;
   uint4 *smem = smem_all + grp * NST * kStageU4;
-  // this group's contiguous segment range [sbeg, sbeg + nseg)
-  const int nseg = segsp / GROUPS;
-  const int sbeg = grp * nseg;
 
   // XCD-aware tile order: consecutive workgroup ids go to different XCDs
   // (round robin), so regroup them into contiguous chunks per XCD, then walk
-  // the chunk kGemmGroup row bands at a time.
-  const int Gt = grid_x * grid_y;
+  // the chunk kGemmGroup row bands at a time.  With ksplit > 1 the ksplit
+  // consecutive ids of a chunk are one tile's K slices.
+  const int Gt = grid_x * grid_y * ksplit;
   int L = blockIdx.x;
   if ((Gt & 7) == 0) L = (L & 7) * (Gt >> 3) + (L >> 3);
+  const int split = L % ksplit;
+  L /= ksplit;
+  const int tile = L;
+  // this group's contiguous segment range [sbeg, sbeg + nseg) of the slice
+  const int nseg = segsp / (GROUPS * ksplit);
+  const int sbeg = (split * GROUPS + grp) * nseg;
   const int per_group = kGemmGroup * grid_x;
   const int first_y = (L / per_group) * kGemmGroup;
   const int rows_in_group = min(grid_y - first_y, kGemmGroup);
@@ -1458,16 +1463,69 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
             red[((grp - 1) * 32 * CB + (rb * CB + cb) * 16 + r) * 256 + tid] = acc[rb][cb][r];
     }
     __syncthreads();
-    if (grp > 0) return;
-    for (int gg = 1; gg < GROUPS; gg++)
+    if (grp == 0) {
+      for (int gg = 1; gg < GROUPS; gg++)
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+          for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+              acc[rb][cb][r] += red[((gg - 1) * 32 * CB + (rb * CB + cb) * 16 + r) * 256 + tid];
+    }
+  }
+  if (ksplit > 1) {
+    // K slices: every slice stores its tile partial (agent scope, so the
+    // last slice reads it from any XCD), then counts in; the last one to
+    // arrive sums the ksplit partials in slice order (the same bits whatever
+    // the arrival order), resets the counter and stores the tile.  Every
+    // wave takes part in the barriers.
+    __shared__ int s_last;
+    constexpr int kPart = 32 * CB * 256;  // floats per tile partial
+    float *pt = part + (size_t)tile * ksplit * kPart;
+    if (grp == 0) {
 #pragma unroll
       for (int rb = 0; rb < 2; rb++)
 #pragma unroll
         for (int cb = 0; cb < CB; cb++)
 #pragma unroll
           for (int r = 0; r < 16; r++)
-            acc[rb][cb][r] += red[((gg - 1) * 32 * CB + (rb * CB + cb) * 16 + r) * 256 + tid];
+            st_act<true>(pt + (size_t)split * kPart + ((rb * CB + cb) * 16 + r) * 256 + tid,
+                         acc[rb][cb][r]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev =
+          __hip_atomic_fetch_add(&tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == ksplit - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;  // whole workgroup
+    if (grp == 0) {
+      // one round trip per slice: all of a slice's values, then the adds
+      for (int sl = 0; sl < ksplit; sl++) {
+        float t[2][CB][16];
+        const float *q = pt + (size_t)sl * kPart + tid;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+          for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) t[rb][cb][r] = ld_act<true>(q + ((rb * CB + cb) * 16 + r) * 256);
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+          for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+              acc[rb][cb][r] = sl == 0 ? t[rb][cb][r] : acc[rb][cb][r] + t[rb][cb][r];
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&tile_cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (grp > 0) return;
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
 #pragma unroll
@@ -1501,22 +1559,45 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   // wave per SIMD; each group's range covers whole quantisation blocks.
   const int groups = ((int64_t)gx * gy < 2 * (int64_t)ctx->cu_count && segs >= 16) ? 2 : 1;
   const int nst = cb == 2 ? 2 : ctx->gemm_stages;
-  const int64_t align = groups * std::max<int64_t>(1, p->block / kSegK);
+  // K slices across workgroups when the tiles (with the K groups) still
+  // leave CUs idle: the largest power of two <= 8 that fits the CUs, keeps
+  // at least 4 stages per group and splits K without padding; each slice
+  // covers whole quantisation blocks.
+  const int64_t bstages = std::max<int64_t>(1, p->block / kSegK);
+  const int64_t tiles = (int64_t)gx * gy;
+  int ksplit = 1;
+  if (tiles <= kGemmMaxSplitTiles) {
+    if (ctx->gemm_ksplit) {
+      ksplit = ctx->gemm_ksplit;
+    } else {
+      for (int ks = 8; ks > 1; ks >>= 1) {
+        const int64_t unit = groups * ks * bstages;
+        if (tiles * ks <= ctx->cu_count && segs % unit == 0 && segs / (groups * ks) >= 4) {
+          ksplit = ks;
+          break;
+        }
+      }
+    }
+  }
+  const int64_t align = groups * ksplit * bstages;
   const int64_t segsp = (segs + align - 1) / align * align;
   const int64_t rblocks = mpad / 32;
   const size_t ap_bytes = (size_t)(rblocks * segsp * 4 * 2 * 64) * 16;
   const size_t shmem = (size_t)groups * nst * (1024 + 256 * cb + 64 * cb * nbps) * 16;
   if (shmem > (size_t)ctx->lds_max)
     return fail(MMNB_ERR_UNSUPPORTED, "GEMM: LDS stages exceed the device limit");
-  void *d_ap = nullptr, *d_exp = nullptr;
+  void *d_ap = nullptr, *d_exp = nullptr, *d_part = nullptr;
   int rc;
   if ((rc = scratch_get(ctx, 2, ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)mpad * 4, &d_exp))) return rc;
+  if (ksplit > 1 &&
+      (rc = scratch_get(ctx, 10, (size_t)tiles * ksplit * 32 * cb * 256 * 4, &d_part)))
+    return rc;
   if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(mpad / kPrepRows)), dim3(256), 0,
                     d_a, lda, m, p->k, segsp, (int *)d_exp, (uint4 *)d_ap)))
     return rc;
   const int bs_log2 = ilog2(p->block);
-  const dim3 grid((unsigned)(gx * gy));
+  const dim3 grid((unsigned)(gx * gy * ksplit));
 #define MMNB_GEMM_LAUNCH(Q, NS, GR, CB)                                                      \
   {                                                                                          \
     auto kern = k_gemm_mfma<Q, NS, GR, CB>;                                                  \
@@ -1528,8 +1609,7 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
     return launch(ctx, kKernGemm, kern, grid, dim3(256 * GR), shmem, (const uint4 *)d_ap,   \
                   (const int *)d_exp, (int)segs, (int)segsp, p->d_w, p->col_bytes,          \
                   p->d_st, p->d_zt, (int)p->ldsz, (int)p->n_blocks, bs_log2, (int)m,        \
-                  (int)p->n, gx,                                                             \
-                  gy, d_y);                                                                  \
+                  (int)p->n, gx, gy, d_y, ksplit, (float *)d_part, ctx->d_gemm_cnt);        \
   }
 #define MMNB_GEMM_NB(NS, GR, CB)                     \
   {                                                  \

@@ -113,6 +113,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v == 1 || v == 2) ctx->gemm_cb = v;
   }
+  if (const char *r = std::getenv("MMNB_GEMM_KSPLIT")) {
+    const int v = std::atoi(r);
+    if (v == 1 || v == 2 || v == 4 || v == 8) ctx->gemm_ksplit = v;
+  }
   if (const char *r = std::getenv("MMNB_GEMV_CG")) {
     const int v = std::atoi(r);
     if (v >= 1 && v <= 8) ctx->gemv_cg = v;
@@ -133,9 +137,14 @@ int mmnb_init(int device, mmnb_ctx **out) {
   if (e == hipSuccess) e = hipMemset(ctx->d_pad, 0, 1024);
   if (e == hipSuccess) e = hipMemset((char *)ctx->d_pad + 1024, 0x80, 1024);
   if (e == hipSuccess) e = hipMemset((char *)ctx->d_pad + 2048, 0, 2048);
+  if (e == hipSuccess) e = hipMalloc((void **)&ctx->d_gemm_cnt, kGemmMaxSplitTiles * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(ctx->d_gemm_cnt, 0, kGemmMaxSplitTiles * sizeof(int));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
+    if (ctx->d_pad) (void)hipFree(ctx->d_pad);
+    if (ctx->d_gemm_cnt) (void)hipFree(ctx->d_gemm_cnt);
     delete ctx;
-    return check_hip(e, "hipMalloc(pad page)");
+    return check_hip(e, "hipMalloc(pad page, GEMM counters)");
   }
   *out = ctx;
   return MMNB_OK;
@@ -153,6 +162,7 @@ int mmnb_shutdown(mmnb_ctx *ctx) {
     for (auto &s : ctx->scratch)
       if (s.ptr) (void)hipFree(s.ptr);
     if (ctx->d_pad) (void)hipFree(ctx->d_pad);
+    if (ctx->d_gemm_cnt) (void)hipFree(ctx->d_gemm_cnt);
     for (auto &ev : ctx->events)
       if (ev) (void)hipEventDestroy(ev);
     for (auto &ev : ctx->tev) (void)hipEventDestroy(ev);

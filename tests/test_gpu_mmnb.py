@@ -141,6 +141,23 @@ def test_edge_shapes(ctx, m, k, n, block, zp):
     check_bound(p, y)
 
 
+@pytest.mark.parametrize("m,k,n,block,zp", [
+    (100, 4096, 512, 32, True),    # 8 tiles: 8 K slices
+    (64, 3072, 1024, 128, False),  # 4 slices (8 would pad K)
+    (256, 2048, 1024, 128, True),  # decoder o projection shape: 4 slices
+    (256, 1024, 4096, 128, True),  # decoder q|k|v shape: 2 slices
+    (64, 2000, 100, 16, True),     # block 16, K not a multiple of 64
+])
+def test_gemm_k_slices(ctx, m, k, n, block, zp):
+    # Few tiles: K is split across workgroups and the last slice of each tile
+    # sums the partials in slice order, so repeated calls give the same bits.
+    p = synth.mmnb_problem(m, k, n, block, zp, seed=21 + m + k)
+    y = run_gpu(ctx, p)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+    np.testing.assert_array_equal(run_gpu(ctx, p), y)
+
+
 def test_batched_activation_shape(ctx):
     p = synth.mmnb_problem(6, 256, 48, 32, True, seed=5)
     a3 = p.a.reshape(2, 3, 256)
