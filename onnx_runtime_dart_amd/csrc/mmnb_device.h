@@ -7,6 +7,10 @@
 
 namespace mmnb {
 
+// s_waitcnt immediate that waits for vmcnt <= n (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // v + (v moved by the DPP control CTRL), every lane.
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {

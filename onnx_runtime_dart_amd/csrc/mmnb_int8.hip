@@ -4,6 +4,7 @@
 
 #include <cstdint>
 
+#include "mmnb_device.h"
 #include "mmnb_internal.h"
 
 namespace mmnb {
@@ -384,16 +385,20 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 
 // MatMulInteger with LDS staging by direct global->LDS DMA
 // (global_load_lds_dwordx4, 16 B per lane, no VGPR round trip).  Same tile
-// and arithmetic as k_mmi_mfma; the K range is staged in chunks of kMmiKc
-// bytes: the workgroup issues the whole chunk of A (64 rows) and B (64
-// columns) at once, waits, then runs the MFMAs from LDS.  LDS rows hold
-// kMmiKc/16 16-byte pieces; piece c of row r is stored at slot c ^ (r & 15)
+// and arithmetic as k_mmi_mfma.  K moves in chunks of kMmiKc bytes through a
+// two-slot ring: the next chunk is in flight while the current one is
+// multiplied (every thread issues the same kMmiLoads DMA loads per chunk, so
+// "chunk c has landed" is vmcnt <= kMmiLoads while chunk c+1 is pending; a
+// barrier then publishes it, another frees its slot).  LDS rows hold
+// kMmiPieces 16-byte pieces; piece c of row r is stored at slot c ^ (r & 15)
 // so the 16 rows an MFMA operand read touches land in 16 different bank
 // groups.  Pieces past K (or rows past M) are read from a constant page whose
 // bytes become zero after the int8 offset.  Requires K % 16 == 0 and a
 // 16-byte aligned A.
-constexpr int kMmiKc = 512;
-constexpr int kMmiPieces = kMmiKc / 16;  // per row
+constexpr int kMmiKc = 256;
+constexpr int kMmiPieces = kMmiKc / 16;                   // per row
+constexpr int kMmiSlotU4 = 64 * kMmiPieces;               // uint4 per operand per slot
+constexpr int kMmiLoads = 2 * (kMmiSlotU4 / 64) / 4;      // DMA loads per thread per chunk
 
 __global__ __launch_bounds__(256) void k_mmi_lds(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
@@ -401,9 +406,10 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
     int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o,
     const uint8_t *__restrict__ pad) {
-  __shared__ uint4 sA[64 * kMmiPieces];
-  __shared__ uint4 sB[64 * kMmiPieces];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ uint4 sA[2][kMmiSlotU4];
+  __shared__ uint4 sB[2][kMmiSlotU4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t bz = blockIdx.z;
   const uint8_t *Ab = A + bz * a_bstride;
@@ -414,6 +420,30 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
   const int r16 = lane & 15, q = lane >> 4;
   const uint32_t flip = a_signed ? 0u : 0x80808080u;
   const uint8_t *apad = pad + (a_signed ? 0 : 1024);
+  const int nchunks = (int)((kpad + kMmiKc - 1) / kMmiKc);
+
+  // DMA of chunk c into slot s: instruction i of a wave fills LDS slots
+  // [64 i, 64 i + 64) of each operand.
+  auto issue = [&](int c, int s) {
+    const int64_t k0 = (int64_t)c * kMmiKc;
+#pragma unroll
+    for (int u = 0; u < kMmiSlotU4 / 64 / 4; u++) {
+      const int i = wave + 4 * u;
+      const int slot = i * 64 + lane;
+      const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
+      const int pc = cs_ ^ (r & 15);
+      const int64_t kk = k0 + (int64_t)pc * 16;
+      const int64_t arow = mt0 + r;
+      const uint8_t *ga = (arow < M && kk < K) ? Ab + arow * K + kk : apad;
+      int64_t bcol = nt0 + r;
+      if (bcol >= N) bcol = N - 1;
+      const int8_t *gb = kk < kpad ? Bb + bcol * kpad + kk : (const int8_t *)pad;
+      uint4 *da = &sA[s][i * 64];
+      uint4 *db = &sB[s][i * 64];
+      __builtin_amdgcn_global_load_lds(ga, da, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gb, db, 16, 0, 0);
+    }
+  };
 
   int4v acc[2][2];
 #pragma unroll
@@ -422,39 +452,30 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
     for (int j = 0; j < 2; j++) acc[i][j] = (int4v){0, 0, 0, 0};
   int rsum[2] = {0, 0};
 
-  for (int64_t k0 = 0; k0 < kpad; k0 += kMmiKc) {
-    const int64_t kc = kpad - k0 < kMmiKc ? kpad - k0 : kMmiKc;  // multiple of 64
-    // ---- DMA: 64 rows x kMmiPieces pieces each for A and B; instruction i of
-    // a wave fills LDS slots [64 i, 64 i + 64).
-    constexpr int kInstr = 64 * kMmiPieces / 64;  // per operand
-    for (int i = wave; i < kInstr; i += 4) {
-      const int slot = i * 64 + lane;
-      const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
-      const int c = cs_ ^ (r & 15);
-      const int64_t kk = k0 + (int64_t)c * 16;
-      const int64_t arow = mt0 + r;
-      const uint8_t *ga = (arow < M && kk < K) ? Ab + arow * K + kk : apad;
-      int64_t bcol = nt0 + r;
-      if (bcol >= N) bcol = N - 1;
-      const int8_t *gb = kk < kpad ? Bb + bcol * kpad + kk : (const int8_t *)pad;
-      __builtin_amdgcn_global_load_lds(ga, sA + i * 64, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(gb, sB + i * 64, 16, 0, 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  issue(0, 0);
+  if (nchunks > 1) issue(1, 1);
+  for (int c = 0; c < nchunks; c++) {
+    const int s = c & 1;
+    if (c + 1 < nchunks)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kMmiLoads));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_barrier();
+    const int64_t kc = kpad - (int64_t)c * kMmiKc < kMmiKc ? kpad - (int64_t)c * kMmiKc
+                                                            : kMmiKc;  // multiple of 64
     for (int st = 0; st < kc / 64; st++) {
       int4v av[2], bv[2];
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const int ra = wm * 32 + t * 16 + r16;
-        const uint4 x = sA[ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
+        const uint4 x = sA[s][ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
         uint32_t w[4] = {x.x ^ flip, x.y ^ flip, x.z ^ flip, x.w ^ flip};
 #pragma unroll
         for (int d = 0; d < 4; d++)
           rsum[t] = __builtin_amdgcn_sdot4((int)w[d], 0x01010101, rsum[t], false);
         av[t] = (int4v){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
         const int rb = wn * 32 + t * 16 + r16;
-        const uint4 y = sB[rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
+        const uint4 y = sB[s][rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
         bv[t] = (int4v){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
       }
 #pragma unroll
@@ -463,7 +484,10 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
         for (int j = 0; j < 2; j++)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-    __syncthreads();
+    if (c + 2 < nchunks) {
+      __builtin_amdgcn_s_barrier();  // every wave is done with slot s
+      issue(c + 2, s);
+    }
   }
   mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
                azp_len, o);

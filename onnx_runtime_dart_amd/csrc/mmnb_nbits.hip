@@ -1054,9 +1054,6 @@ constexpr int kGemmBM = 64;   // two 32-row blocks
 constexpr int kGemmBN = 128;  // four 32-column blocks
 constexpr int kGemmGroup = 2; // row bands per tile group (L2 reuse of A)
 
-// s_waitcnt immediate that waits for vmcnt <= n (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 template <int NBPS, int NST, int GROUPS, int CB>
 __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_mfma(
