@@ -152,7 +152,9 @@ def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
                         "mfma_passes": 2,
                         "mfma_utilisation": 2 * achieved / MFMA_FP16_PEAK_TFLOPS,
                         "vs_fp32_mfma_peak": achieved / MFMA_FP32_PEAK_TFLOPS,
-                        "traffic": None}}
+                        "traffic": (measured_traffic("gemm_m512_k4096_n4096_bs32_zp")
+                                    if (m, k, n, bs, zp) == (512, 4096, 4096, 32, True)
+                                    else None)}}
     da.free()
     dy.free()
     pack.free()
