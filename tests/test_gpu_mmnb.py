@@ -89,6 +89,17 @@ def test_headline_gemv_4096(ctx, block, zp):
     check_bound(p, y)
 
 
+@pytest.mark.parametrize("k,n,block,zp", [(16384, 16384, 128, False), (11008, 4096, 32, True),
+                                          (8192, 14336, 64, True), (14336, 4096, 128, False)])
+def test_gemv_long_k(ctx, k, n, block, zp):
+    # Decode GEMV at full size with K > 4096 (2..4 chunks per lane)
+    p = synth.mmnb_problem(1, k, n, block, zp, seed=5 + k // 1024)
+    y = run_gpu(ctx, p)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+    np.testing.assert_array_equal(run_gpu(ctx, p), y)
+
+
 @pytest.mark.parametrize("m,n,block", [(128, 4096, 32), (128, 4096, 128)])
 def test_prefill_full_oracle(ctx, m, n, block):
     p = synth.mmnb_problem(m, 4096, n, block, True, seed=2, outlier_frac=0.01)
@@ -120,6 +131,12 @@ def test_prefill_full_size_row_sample(ctx, m, n, block):
     (65, 1000, 130, 128, True),  # GEMM path, K not a multiple of 64
     (8, 3000, 17, 64, False),
     (1, 4096, 1, 128, True),    # single column
+    # M = 1 with K > 4096: several chunks per lane, the next chunk's loads
+    # in flight during the current one's arithmetic
+    (1, 9000, 33, 128, True),
+    (1, 5000, 70, 16, True),    # block 16, K not a multiple of 64
+    (1, 12288, 200, 32, False),
+    (1, 4160, 9, 64, True),     # one chunk past a 4-wave workgroup's first pass
     # decode GEMV for 2 <= M <= 8 (activations staged in LDS)
     (2, 9000, 33, 128, True),   # K > 4096: several chunk iterations
     (4, 5000, 100, 16, True),   # block 16, iterations
