@@ -232,22 +232,73 @@ int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int b_t
 
 typedef int int4v __attribute__((ext_vector_type(4)));
 
+// Epilogue operands of one lane: A's zero point for each of its 8 rows, and
+// per column (2 of them) the pack's zero-point terms, the fp32 rescale's B
+// scale and the requantisation's multiplier and bias.  Loaded at the start of
+// the kernel, unconditionally (clamped indices; arrays a call does not use are
+// read from the zero page `pad`), so they arrive during the K loop instead of
+// as a chain of dependent round trips after it (a load under a branch ends in
+// a full wait).
+struct MmiEpiIn {
+  int32_t z[2][4];
+  int32_t e[2], cs[2];
+  float bs[2];
+  double mch[2];
+  int32_t bias[2];
+  float as;
+};
+
+__device__ __forceinline__ void mmi_epi_load(MmiEpiIn &in, int64_t bz, int64_t M, int64_t N,
+                                             int64_t m0, int64_t n0, int lane,
+                                             const int32_t *__restrict__ colsum,
+                                             int64_t cs_bstride, const int32_t *__restrict__ ecol,
+                                             const int32_t *__restrict__ azp, int64_t azp_len,
+                                             const MmiEpi &o, const void *pad) {
+  const int r16 = lane & 15, q = lane >> 4;
+  const bool zload = azp_len > 0 && !o.azp_is_const;
+  const int32_t *zp = zload ? azp : (const int32_t *)pad;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      int64_t row = m0 + i * 16 + q * 4 + r;
+      row = row < M ? row : M - 1;
+      in.z[i][r] = zp[(zload && azp_len > 1) ? row : 0];
+    }
+  const bool fy = o.yf != nullptr;
+  in.as = (fy ? o.a_scale : (const float *)pad)[0];
+  const float *bsp = fy ? o.b_scale : (const float *)pad;
+  const bool rq2 = o.rq_mode == 2, hb = rq2 && o.rq_bias != nullptr;
+  const double *mp = rq2 ? o.rq_mult_ch : (const double *)pad;
+  const int32_t *bp = hb ? o.rq_bias : (const int32_t *)pad;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    int64_t col = n0 + j * 16 + r16;
+    col = col < N ? col : N - 1;
+    in.e[j] = ecol[bz * o.ecol_bstride + col];
+    in.cs[j] = colsum[bz * cs_bstride + col];
+    in.bs[j] = bsp[(fy && o.b_scale_len != 1) ? col : 0];
+    const int64_t ch = o.trans ? bz * N + col : col;  // output channel (requant mode 2)
+    in.mch[j] = mp[rq2 ? ch : 0];
+    in.bias[j] = bp[hb ? ch : 0];
+  }
+}
+
 // Epilogue shared by both MatMulInteger kernels: completes the row sums,
 // applies the exact integer zero-point corrections and stores what `o` asks
 // for (int32, the fused fp32 rescale, 8-bit requantisation).  16x16 i32
 // accumulator layout: lane l holds column l%16 and rows 4*(l/16) + r.
-__device__ __forceinline__ void mmi_epilogue(
-    const int4v (&acc)[2][2], int (&rsum)[2], int a_signed, int64_t bz, int64_t M, int64_t K,
-    int64_t N, int64_t m0, int64_t n0, int lane, const int32_t *__restrict__ colsum,
-    int64_t cs_bstride, const int32_t *__restrict__ ecol, const int32_t *__restrict__ azp,
-    int64_t azp_len, const MmiEpi &o) {
+__device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[2][2], int (&rsum)[2],
+                                             const MmiEpiIn &in, int a_signed, int64_t bz,
+                                             int64_t M, int64_t K, int64_t N, int64_t m0,
+                                             int64_t n0, int lane, int64_t azp_len,
+                                             const MmiEpi &o) {
   const int r16 = lane & 15, q = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 2; t++) {
     rsum[t] += __shfl_xor(rsum[t], 16, 64);
     rsum[t] += __shfl_xor(rsum[t], 32, 64);
   }
-  const float as = o.yf ? *o.a_scale : 0.0f;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     int32_t rs[4], cm[4];
@@ -256,25 +307,17 @@ __device__ __forceinline__ void mmi_epilogue(
     for (int r = 0; r < 4; r++) {
       rs[r] = __shfl(rsum[i], q * 4 + r, 64);  // lane holding that row's sum
       row[r] = m0 + i * 16 + q * 4 + r;
-      int32_t z = 0;
-      if (azp_len == 1) z = o.azp_is_const ? o.azp_const : azp[0];
-      else if (azp_len > 1 && row[r] < M) z = azp[row[r]];
+      const int32_t z = o.azp_is_const ? o.azp_const : (azp_len > 0 ? in.z[i][r] : 0);
       cm[r] = (a_signed ? 0 : 128) - z;
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int64_t col = n0 + j * 16 + r16;
       if (col >= N) continue;
-      const uint32_t e = (uint32_t)ecol[bz * o.ecol_bstride + col];
-      const uint32_t cs = (uint32_t)colsum[bz * cs_bstride + col];
-      const int64_t ch = o.trans ? bz * N + col : col;  // output channel (requant mode 2)
-      float sj = 0.0f;
-      if (o.yf) sj = as * o.b_scale[o.b_scale_len == 1 ? 0 : col];
-      double mch = 0.0, bias = 0.0;
-      if (o.rq_mode == 2) {
-        mch = o.rq_mult_ch[ch];
-        if (o.rq_bias) bias = (double)o.rq_bias[ch];
-      }
+      const uint32_t e = (uint32_t)in.e[j];
+      const uint32_t cs = (uint32_t)in.cs[j];
+      const float sj = in.as * in.bs[j];
+      const double mch = in.mch[j], bias = (double)in.bias[j];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         if (row[r] >= M) continue;
@@ -307,7 +350,8 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
     const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
-    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o, int fast) {
+    int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o, int fast,
+    const void *__restrict__ pad) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t bz = blockIdx.z;
@@ -334,6 +378,8 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = (int4v){0, 0, 0, 0};
   int rsum[2] = {0, 0};
+  MmiEpiIn ein;
+  mmi_epi_load(ein, bz, M, N, m0, n0, lane, colsum, cs_bstride, ecol, azp, azp_len, o, pad);
 
   for (int64_t k0 = 0; k0 < kpad; k0 += 64) {
     const int64_t kq = k0 + q * 16;
@@ -378,8 +424,7 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
       for (int j = 0; j < 2; j++)
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
   }
-  mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
-               azp_len, o);
+  mmi_epilogue(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o);
 }
 
 
@@ -451,6 +496,9 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = (int4v){0, 0, 0, 0};
   int rsum[2] = {0, 0};
+  // issued before the first chunk, so the chunk waits below cover them too
+  MmiEpiIn ein;
+  mmi_epi_load(ein, bz, M, N, m0, n0, lane, colsum, cs_bstride, ecol, azp, azp_len, o, pad);
 
   issue(0, 0);
   if (nchunks > 1) issue(1, 1);
@@ -489,8 +537,7 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
       issue(c + 2, s);
     }
   }
-  mmi_epilogue(acc, rsum, a_signed, bz, M, K, N, m0, n0, lane, colsum, cs_bstride, ecol, azp,
-               azp_len, o);
+  mmi_epilogue(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o);
 }
 
 int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, int a_signed,
@@ -501,6 +548,7 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
   if (!out.y && !out.yf && !out.yq) return fail(MMNB_ERR_ARG, "MatMulInteger: no output");
   MmiEpi o = out;
   o.ecol_bstride = p->ecol_bstride;
+  if (m <= 0 || n <= 0 || batch <= 0) return MMNB_OK;
   const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
   if (fast && ctx->d_pad)
@@ -514,7 +562,7 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
                 a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                 p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, (const int32_t *)p->d_colsum,
                 p->batch == 1 ? (int64_t)0 : n, (const int32_t *)p->d_ecol, n, d_azp, azp_len, o,
-                fast);
+                fast, (const void *)ctx->d_pad);
 }
 
 // ---------------------------------------------------------------------------
