@@ -260,6 +260,186 @@ __global__ __launch_bounds__(256) void k_attn_rows(
 }
 
 // ---------------------------------------------------------------------------
+// Attention rows on the matrix cores: v_mfma_f32_16x16x4_f32 (fp32 products
+// and sums, as in k_attn_rows, in another order).  A workgroup takes 16
+// queries of one head; its 8 waves take the key blocks (16 keys) round robin
+// and merge their (max, sum, o) through LDS at the end, pairwise in a fixed
+// order.  Per key block a wave forms S^T = K Q^T (16 keys x 16 queries,
+// HD/4 MFMAs), runs the online softmax on it and accumulates O^T += V^T P^T
+// (HD/4 MFMAs).  16x16x4 operand layouts: A lane l = row l%16, k slot l/16;
+// B lane l = column l%16, k slot l/16; D lane l = column l%16, rows
+// 4(l/16) + r.  For lane (c = l%16, g = l/16):
+//   S^T step t: A = K[key c][d], B = Q[query c][d], d = g*HD/4 + t;
+//     D = the scores of query c for keys 4g + r.
+//   O^T step t: k slot g' carries key 4g' + t, so B is the lane's own p[t];
+//     A = V[key 4g + t][c*HD/16 + db] for d block db;
+//     D = o of query c at d = (4g + r)*HD/16 + db.
+// K and V go straight to registers (float4 / float2 loads); the two key
+// blocks of an iteration have all their loads in flight before the first
+// block's arithmetic.
+// ---------------------------------------------------------------------------
+constexpr int kAttnMfWaves = 8;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int N>
+__device__ __forceinline__ void ld_run(const float *__restrict__ p, float *v) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int e = 0; e < N; e += 4) {
+      const float4 x = *(const float4 *)(p + e);
+      v[e] = x.x; v[e + 1] = x.y; v[e + 2] = x.z; v[e + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; e += 2) {
+      const float2 x = *(const float2 *)(p + e);
+      v[e] = x.x; v[e + 1] = x.y;
+    }
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * kAttnMfWaves) void k_attn_mfma(
+    const float *__restrict__ Q, int64_t q_row_stride, int64_t seq, int nh, int kvh,
+    const float *__restrict__ pk, const float *__restrict__ pv, int64_t cap, int64_t P,
+    float scale, const float *__restrict__ bias, int bias_heads, float *__restrict__ out,
+    int64_t out_row_stride) {
+  constexpr int kQd = HD / 4;   // d values per lane of an S^T operand
+  constexpr int kVd = HD / 16;  // d blocks of O^T (d values per lane per key)
+  __shared__ float s_slot[kAttnMfWaves / 2][kQd + 2][64];
+  const int w = threadIdx.x >> 6, ln = threadIdx.x & 63, c = ln & 15, g = ln >> 4;
+  const int h = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int kv = h / (nh / kvh);
+  const int64_t q0 = (int64_t)blockIdx.x * 16;
+  const int64_t qi = q0 + c;
+  const bool qok = qi < seq;
+  const int64_t T = P + seq;
+  const int64_t last = qok ? P + qi : -1;  // last key query c sees
+  const int64_t qmax = (q0 + 16 < seq ? q0 + 16 : seq) - 1;
+  const int nkb = (int)((P + qmax + 1 + 15) / 16);  // key blocks any query here sees
+  const float *Kb = pk + (b * kvh + kv) * cap * HD;
+  const float *Vb = pv + (b * kvh + kv) * cap * HD;
+  const float *brow = bias ? bias + ((b * bias_heads + (h % bias_heads)) * seq +
+                                     (qok ? qi : 0)) * T
+                           : nullptr;
+
+  float qf[kQd];
+  ld_run<kQd>(Q + (b * seq + (qok ? qi : seq - 1)) * q_row_stride + (int64_t)h * HD + g * kQd,
+              qf);
+#pragma unroll
+  for (int t = 0; t < kQd; t++) qf[t] = qok ? qf[t] : 0.0f;
+
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o[kVd];
+#pragma unroll
+  for (int db = 0; db < kVd; db++) o[db] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto load_block = [&](int kb, float (&kf)[kQd], float (&vf)[4][kVd]) {
+    int64_t key = (int64_t)kb * 16 + c;
+    key = key < T ? key : T - 1;
+    ld_run<kQd>(Kb + key * HD + g * kQd, kf);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      int64_t kt = (int64_t)kb * 16 + 4 * g + t;
+      kt = kt < T ? kt : T - 1;
+      ld_run<kVd>(Vb + kt * HD + c * kVd, vf[t]);
+    }
+  };
+  auto block = [&](int kb, const float (&kf)[kQd], const float (&vf)[4][kVd]) {
+    f32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < kQd; t++) s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t], qf[t], s4, 0, 0, 0);
+    float sv[4];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t key = (int64_t)kb * 16 + 4 * g + r;
+      const bool ok = key <= last;
+      float v = s4[r] * scale;
+      if (bias) v += brow[ok ? key : 0];
+      sv[r] = ok ? v : -INFINITY;
+      bm = fmaxf(bm, sv[r]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mn = fmaxf(m, bm);
+    float p[4], corr = 1.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) p[r] = 0.0f;
+    if (mn != -INFINITY) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) p[r] = sv[r] == -INFINITY ? 0.0f : expf(sv[r] - mn);
+      corr = m == -INFINITY ? 0.0f : expf(m - mn);
+    }
+    float ps = (p[0] + p[1]) + (p[2] + p[3]);
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * corr + ps;
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < kVd; db++) o[db] *= corr;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int db = 0; db < kVd; db++)
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[t][db], p[t], o[db], 0, 0, 0);
+  };
+
+  for (int kb0 = w; kb0 < nkb; kb0 += 2 * kAttnMfWaves) {
+    const int kb1 = kb0 + kAttnMfWaves;
+    float kf0[kQd], kf1[kQd], vf0[4][kVd], vf1[4][kVd];
+    load_block(kb0, kf0, vf0);
+    load_block(kb1 < nkb ? kb1 : kb0, kf1, vf1);  // unconditional (clamped)
+    block(kb0, kf0, vf0);
+    if (kb1 < nkb) block(kb1, kf1, vf1);
+  }
+
+  // ---- merge the waves' partials: (0,4) (1,5) (2,6) (3,7), then (0,2)
+  // (1,3), then (0,1); each wave stores its lanes' state in lane order
+#pragma unroll
+  for (int half = kAttnMfWaves / 2; half >= 1; half >>= 1) {
+    __syncthreads();
+    if (w >= half && w < 2 * half) {
+      float *sl = &s_slot[w - half][0][0];
+#pragma unroll
+      for (int db = 0; db < kVd; db++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sl[(db * 4 + r) * 64 + ln] = o[db][r];
+      sl[kQd * 64 + ln] = m;
+      sl[(kQd + 1) * 64 + ln] = l;
+    }
+    __syncthreads();
+    if (w < half) {
+      const float *sl = &s_slot[w][0][0];
+      const float m2 = sl[kQd * 64 + ln], l2 = sl[(kQd + 1) * 64 + ln];
+      const float M = fmaxf(m, m2);
+      if (M != -INFINITY) {
+        const float a1 = m == -INFINITY ? 0.0f : expf(m - M);
+        const float a2 = m2 == -INFINITY ? 0.0f : expf(m2 - M);
+        l = a1 * l + a2 * l2;
+#pragma unroll
+        for (int db = 0; db < kVd; db++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) o[db][r] = a1 * o[db][r] + a2 * sl[(db * 4 + r) * 64 + ln];
+        m = M;
+      }
+    }
+  }
+  if (w == 0 && qok) {
+    const float inv = 1.0f / l;
+    float *orow = out + (b * seq + qi) * out_row_stride + (int64_t)h * HD;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int db = 0; db < kVd; db += 2) {
+        const float2 v2 = {o[db][r] * inv, o[db + 1][r] * inv};
+        *(float2 *)(orow + (4 * g + r) * kVd + db) = v2;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Decoder prefill helpers.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_embed_rows(const int64_t *__restrict__ tok,
@@ -696,6 +876,22 @@ static int launch_attn_rows(mmnb_ctx *ctx, const float *q, int64_t q_stride, int
                             const float *pv, int64_t cap, int64_t P, float scale,
                             const float *bias, int bias_heads, float *out, int64_t out_stride) {
   const dim3 grid((unsigned)((seq + kAttnQ - 1) / kAttnQ), (unsigned)nh, (unsigned)batch);
+  // matrix-core kernel: head size a multiple of 32, float4-aligned rows
+  const bool al = ((((uintptr_t)q | (uintptr_t)pk | (uintptr_t)pv | (uintptr_t)out) & 15) == 0) &&
+                  q_stride % 4 == 0 && out_stride % 4 == 0;
+  if (al && ctx->attn_mfma) {
+#define MMNB_ATTN_MF(HD)                                                                      \
+  launch(ctx, kKernDecAttn, k_attn_mfma<HD>, grid, dim3(64 * kAttnMfWaves), 0, q, q_stride,  \
+         seq, nh, kvh, pk, pv, cap, P, scale, bias, bias_heads, out, out_stride)
+    switch (hd) {
+      case 32: return MMNB_ATTN_MF(32);
+      case 64: return MMNB_ATTN_MF(64);
+      case 96: return MMNB_ATTN_MF(96);
+      case 128: return MMNB_ATTN_MF(128);
+      default: break;
+    }
+#undef MMNB_ATTN_MF
+  }
   return launch(ctx, kKernDecAttn, k_attn_rows, grid, dim3(256), 0, q, q_stride, seq, nh, kvh,
                 hd, pk, pv, cap, P, scale, bias, bias_heads, out, out_stride);
 }

@@ -83,6 +83,9 @@ struct mmnb_ctx {
   // Tuning override of the multi-row GEMV column groups per workgroup
   // (MMNB_GEMV_CG; 0 = auto).
   int gemv_cg = 0;
+  // Prefill attention on the matrix cores (MMNB_ATTN_MFMA: 0 selects the
+  // vector-ALU kernel; on by default).
+  int attn_mfma = 1;
   // Prefill GEMM LDS stages (2 or 3; MMNB_GEMM_STAGES tuning override).
   int gemm_stages = 2;
   // Prefill GEMM 128-column blocks per tile (MMNB_GEMM_CB: 1 or 2; 0 = auto).

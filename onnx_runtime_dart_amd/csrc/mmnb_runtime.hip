@@ -121,6 +121,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v >= 1 && v <= 8) ctx->gemv_cg = v;
   }
+  if (const char *r = std::getenv("MMNB_ATTN_MFMA")) {
+    const int v = std::atoi(r);
+    if (v == 0 || v == 1) ctx->attn_mfma = v;
+  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

@@ -178,3 +178,27 @@ def test_dynamic_matmul_chain_bit_exact(ctx, m, k, n, per_col):
     for buf in (dx, dbs, daq, dsc, dzp, dacc, dy):
         buf.free()
     pack.free()
+
+
+@pytest.mark.parametrize("m,k,n,per_col", [(512, 1024, 3072, True), (65, 336, 130, False)])
+def test_dynamic_matmul_chain_without_int32_output(ctx, m, k, n, per_col):
+    # d_acc NULL: only the fp32 result leaves the kernel; still bit-exact
+    rng = np.random.default_rng(3 * m + k + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    b_scale = (rng.uniform(0.001, 0.01, n if per_col else 1)).astype(np.float32)
+    pack = ops.pack_integer(b, np.array(0, np.int8), ctx=ctx)
+    dx, dbs = ctx.to_device(x), ctx.to_device(b_scale)
+    daq, dsc, dzp, dy = ctx.alloc(m * k), ctx.alloc(4), ctx.alloc(4), ctx.alloc(m * n * 4)
+    _lib.check(ctx.lib.mmnb_dynamic_matmul_dev(ctx.handle, pack.handle, dx.ptr, m, dbs.ptr,
+                                               b_scale.size, daq.ptr, dsc.ptr, dzp.ptr, None,
+                                               dy.ptr))
+    ctx.synchronize()
+    y = dy.numpy(np.float32, (m, n))
+    ry, rs, rz = refcpu.dynamic_quantize_linear(x)
+    np.testing.assert_array_equal(daq.numpy(np.uint8, (m, k)), ry)
+    ref = refcpu.rescale(refcpu.matmul_integer(ry, b, rz, 0), rs, b_scale)
+    np.testing.assert_array_equal(y, ref)
+    for buf in (dx, dbs, daq, dsc, dzp, dy):
+        buf.free()
+    pack.free()
