@@ -22,6 +22,7 @@ the last decode step's logits against a prefill of the same sequence
 (GEMM path, other attention kernel) to FULL_TOL.
 """
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -164,7 +165,10 @@ def test_gqa_golden(ctx, case):
                                                   (1, 37, 50, 8, 2, 128, True),
                                                   (2, 37, 50, 8, 2, 128, False),
                                                   (1, 70, 0, 16, 8, 128, False),
-                                                  (1, 1, 200, 16, 8, 128, True)])
+                                                  (1, 1, 200, 16, 8, 128, True),
+                                                  (1, 40, 30, 4, 4, 32, False),
+                                                  (1, 33, 17, 6, 2, 96, True),
+                                                  (2, 200, 100, 16, 8, 128, False)])
 def test_gqa_vs_oracle(ctx, b, s, P, nh, kvh, hd, rot):
     rng = np.random.default_rng(s + P)
     q = rng.standard_normal((b, s, nh * hd)).astype(np.float32)
@@ -178,6 +182,52 @@ def test_gqa_vs_oracle(ctx, b, s, P, nh, kvh, hd, rot):
     assert normwise_rel_err(got[0], want[0]) <= 1e-5
     np.testing.assert_array_equal(got[1], want[1])
     np.testing.assert_array_equal(got[2], want[2])
+
+
+@pytest.mark.parametrize("bias_heads", [1, 8])
+def test_gqa_bias_vs_oracle(ctx, bias_heads):
+    # attention bias [b, bias_heads, s, T] on a head size the matrix-core
+    # kernel takes (the fixtures' heads are 8 and 16 wide)
+    b, s, P, nh, kvh, hd = 2, 37, 20, 8, 4, 64
+    rng = np.random.default_rng(bias_heads)
+    q = rng.standard_normal((b, s, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((b, s, kvh * hd)).astype(np.float32)
+    v = rng.standard_normal((b, s, kvh * hd)).astype(np.float32)
+    pk = rng.standard_normal((b, kvh, P, hd)).astype(np.float32)
+    pv = rng.standard_normal((b, kvh, P, hd)).astype(np.float32)
+    bias = rng.standard_normal((b, bias_heads, s, P + s)).astype(np.float32)
+    got = gpu_gqa(ctx, q, k, v, nh, kvh, None, pk, pv, bias=bias)
+    want = D.gqa(q, k, v, nh, kvh, None, pk, pv, bias=bias)
+    assert normwise_rel_err(got[0], want[0]) <= 1e-5
+
+
+@pytest.fixture(scope="module")
+def valu_attn_ctx():
+    # a context whose prefill attention takes the vector-ALU kernel
+    saved = os.environ.get("MMNB_ATTN_MFMA")
+    os.environ["MMNB_ATTN_MFMA"] = "0"
+    try:
+        c = _lib.Context(0)
+    finally:
+        if saved is None:
+            os.environ.pop("MMNB_ATTN_MFMA", None)
+        else:
+            os.environ["MMNB_ATTN_MFMA"] = saved
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("b,s,P,nh,kvh,hd", [(1, 70, 0, 16, 8, 128), (1, 33, 17, 6, 2, 96)])
+def test_gqa_vector_alu_kernel_vs_oracle(valu_attn_ctx, b, s, P, nh, kvh, hd):
+    rng = np.random.default_rng(7 * s + P)
+    q = rng.standard_normal((b, s, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((b, s, kvh * hd)).astype(np.float32)
+    v = rng.standard_normal((b, s, kvh * hd)).astype(np.float32)
+    pk = rng.standard_normal((b, kvh, P, hd)).astype(np.float32) if P else None
+    pv = rng.standard_normal((b, kvh, P, hd)).astype(np.float32) if P else None
+    got = gpu_gqa(valu_attn_ctx, q, k, v, nh, kvh, None, pk, pv)
+    want = D.gqa(q, k, v, nh, kvh, None, pk, pv)
+    assert normwise_rel_err(got[0], want[0]) <= 1e-5
 
 
 def test_op_argument_errors(ctx):
