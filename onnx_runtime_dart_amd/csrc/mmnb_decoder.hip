@@ -74,6 +74,105 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *X, int64_t dim,
 }
 
 // ---------------------------------------------------------------------------
+// k_rmsnorm (same sums, same products, so the same fp32 values) written
+// straight into the prefill GEMM's prepared activations (prep_a_store16), so
+// the GEMM that consumes the norm needs no k_prep_a launch.  One workgroup
+// per row of the padded row count; rows >= M and k >= dim are written as
+// zeros.  dim <= 4096: the row sits in LDS between the sum of squares
+// (thread t sums k = t, t+256, ..., as in k_rmsnorm) and the conversion
+// (thread t owns k = 16t .. 16t+15).  With `add` the row is x + add, also
+// written back to xsum.
+// ---------------------------------------------------------------------------
+constexpr int kPrepMaxDim = 4096;
+
+__device__ __forceinline__ int prep_row_exponent(float mx, float *wmx) {
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) wmx[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  return prep_a_exponent(fmaxf(fmaxf(wmx[0], wmx[1]), fmaxf(wmx[2], wmx[3])));
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_prep(const float *X, int64_t M, int64_t dim,
+                                                      const float *__restrict__ G, float eps,
+                                                      const float *add, float *xsum,
+                                                      int64_t segsp, int64_t kp,
+                                                      int *__restrict__ row_exp,
+                                                      uint4 *__restrict__ out) {
+  __shared__ double sh[4];
+  __shared__ float srow[kPrepMaxDim];
+  __shared__ float wmx[4];
+  const int64_t r = blockIdx.x;
+  const bool live = r < M;  // whole workgroup
+  const int t = threadIdx.x;
+  double inv = 0.0;
+  if (live) {
+    double ss = 0.0;
+    for (int64_t k = t; k < dim; k += blockDim.x) {
+      float v = X[r * dim + k];
+      if (add) {
+        v = v + add[r * dim + k];
+        xsum[r * dim + k] = v;
+      }
+      srow[k] = v;
+      ss += (double)v * (double)v;
+    }
+    ss = block_sum_d(ss, sh);  // its barriers also publish srow
+    inv = 1.0 / sqrt(ss / (double)dim + (double)eps);
+  }
+  const int64_t k0 = 16 * t;
+  float v[16];
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const int64_t k = k0 + e;
+    const bool ok = live && k < dim;
+    const float gk = G[ok ? k : 0];
+    const float y = (float)((double)srow[k] * inv * (double)gk);
+    v[e] = ok ? y : 0.0f;
+    mx = fmaxf(mx, fabsf(v[e]));
+  }
+  const int ex = prep_row_exponent(mx, wmx);
+  if (t == 0 && live) row_exp[r] = ex;
+  if (k0 < kp) prep_a_store16(out, segsp, r, k0, v, ex);  // kp may be below 4096
+#pragma unroll
+  for (int e = 0; e < 16; e++) v[e] = 0.0f;
+  for (int64_t kz = k0 + kPrepMaxDim; kz < kp; kz += kPrepMaxDim)
+    prep_a_store16(out, segsp, r, kz, v, 0);
+}
+
+// k_swiglu_rows into the prepared activations of the down projection (one
+// workgroup per padded row, I <= 4096, thread t owns k = 16t .. 16t+15).
+__global__ __launch_bounds__(256) void k_swiglu_prep(const float *__restrict__ gu, int64_t M,
+                                                     int64_t I, int64_t segsp, int64_t kp,
+                                                     int *__restrict__ row_exp,
+                                                     uint4 *__restrict__ out) {
+  __shared__ float wmx[4];
+  const int64_t r = blockIdx.x;
+  const bool live = r < M;
+  const int t = threadIdx.x;
+  const int64_t k0 = 16 * t;
+  float v[16];
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const int64_t k = k0 + e;
+    const bool ok = live && k < I;
+    const int64_t i = ok ? r * 2 * I + 2 * k : 0;
+    const float g = gu[i], u = gu[i + 1];
+    const float sig = (float)(1.0 / (1.0 + exp(-(double)g)));
+    v[e] = ok ? (g * sig) * u : 0.0f;
+    mx = fmaxf(mx, fabsf(v[e]));
+  }
+  const int ex = prep_row_exponent(mx, wmx);
+  if (t == 0 && live) row_exp[r] = ex;
+  if (k0 < kp) prep_a_store16(out, segsp, r, k0, v, ex);  // kp may be below 4096
+#pragma unroll
+  for (int e = 0; e < 16; e++) v[e] = 0.0f;
+  for (int64_t kz = k0 + kPrepMaxDim; kz < kp; kz += kPrepMaxDim)
+    prep_a_store16(out, segsp, r, kz, v, 0);
+}
+
+// ---------------------------------------------------------------------------
 // Rotary embedding of one [heads, head] row block at position p (3-D layout
 // [b, s, heads * head]).  Rotated pairs in double, as the reference.
 // ---------------------------------------------------------------------------
@@ -1210,11 +1309,31 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
   if ((rc = launch(ctx, kKernDecOps, k_embed_rows, dim3((unsigned)n), dim3(256), 0,
                    (const int64_t *)d->tok, (const float *)d->embed, H, d->x)))
     return rc;
+  // With more than 8 rows the projections take the MFMA GEMM; the norms and
+  // SwiGLU that feed them then write its prepared activations themselves
+  // (k_rmsnorm_prep, k_swiglu_prep) instead of fp32 rows for k_prep_a.
+  const bool fuse = ctx->prep_fuse && n > 8 && H <= kPrepMaxDim && I <= kPrepMaxDim;
+  // x (+= add) normalised with gamma, as the input of the projection `next`
+  auto norm_into = [&](const float *gamma, const float *add, const mmnb_pack *next) -> int {
+    if (!fuse) return launch_rmsnorm(ctx, d->x, n, H, gamma, eps, d->h, add, add ? d->x : nullptr);
+    int64_t segsp = 0, mpad = 0;
+    void *ap = nullptr;
+    int *ex = nullptr;
+    int e = gemm_prepared_a(ctx, next, n, &segsp, &mpad, &ap, &ex);
+    if (e) return e;
+    return launch(ctx, kKernDecOps, k_rmsnorm_prep, dim3((unsigned)mpad), dim3(256), 0,
+                  (const float *)d->x, n, H, gamma, eps, add, add ? d->x : nullptr, segsp,
+                  segsp * kSegK, ex, (uint4 *)ap);
+  };
+  auto gemm_from_norm = [&](const mmnb_pack *pk, float *y) -> int {
+    return fuse ? launch_matmul_nbits_prepared(ctx, pk, n, y)
+                : launch_matmul_nbits(ctx, pk, d->h, H, n, y);
+  };
+  if ((rc = norm_into(d->layers[0].ln1, nullptr, d->layers[0].qkv))) return rc;
   for (int64_t li = 0; li < c.layers; li++) {
     const mmnb_decoder::Layer &L = d->layers[(size_t)li];
     float *ck = d->cache_k + li * kvh * Lmax * hd, *cv = d->cache_v + li * kvh * Lmax * hd;
-    if ((rc = launch_rmsnorm(ctx, d->x, n, H, L.ln1, eps, d->h, nullptr, nullptr))) return rc;
-    if ((rc = launch_matmul_nbits(ctx, L.qkv, d->h, H, n, d->qkv))) return rc;
+    if ((rc = gemm_from_norm(L.qkv, d->qkv))) return rc;
     if ((rc = launch(ctx, kKernDecOps, k_qk_prep_rows, dim3((unsigned)n, (unsigned)(nh + kvh)),
                      dim3((unsigned)hd), 0, (const float *)d->qkv, QKV, (int)nh, (int)kvh,
                      (int)hd, (const float *)L.qn, (const float *)L.kn, eps,
@@ -1225,18 +1344,33 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
       return rc;
     if ((rc = launch_matmul_nbits(ctx, L.o, d->attn, nh * hd, n, d->tmp))) return rc;
     // x += o; h = rmsnorm(x)
-    if ((rc = launch_rmsnorm(ctx, d->x, n, H, L.ln2, eps, d->h, d->tmp, d->x))) return rc;
-    if ((rc = launch_matmul_nbits(ctx, L.gu, d->h, H, n, d->gu))) return rc;
-    if ((rc = launch(ctx, kKernDecOps, k_swiglu_rows,
-                     dim3((unsigned)((I + 255) / 256), (unsigned)n), dim3(256), 0,
-                     (const float *)d->gu, I, d->act)))
+    if ((rc = norm_into(L.ln2, d->tmp, L.gu))) return rc;
+    if ((rc = gemm_from_norm(L.gu, d->gu))) return rc;
+    if (fuse) {
+      int64_t segsp = 0, mpad = 0;
+      void *ap = nullptr;
+      int *ex = nullptr;
+      if ((rc = gemm_prepared_a(ctx, L.down, n, &segsp, &mpad, &ap, &ex))) return rc;
+      if ((rc = launch(ctx, kKernDecOps, k_swiglu_prep, dim3((unsigned)mpad), dim3(256), 0,
+                       (const float *)d->gu, n, I, segsp, segsp * kSegK, ex, (uint4 *)ap)))
+        return rc;
+      if ((rc = launch_matmul_nbits_prepared(ctx, L.down, n, d->tmp))) return rc;
+    } else {
+      if ((rc = launch(ctx, kKernDecOps, k_swiglu_rows,
+                       dim3((unsigned)((I + 255) / 256), (unsigned)n), dim3(256), 0,
+                       (const float *)d->gu, I, d->act)))
+        return rc;
+      if ((rc = launch_matmul_nbits(ctx, L.down, d->act, I, n, d->tmp))) return rc;
+    }
+    // x += down, and (but after the last layer) the next layer's input norm
+    if (li + 1 < c.layers) {
+      const mmnb_decoder::Layer &Ln = d->layers[(size_t)li + 1];
+      if ((rc = norm_into(Ln.ln1, d->tmp, Ln.qkv))) return rc;
+    } else if ((rc = launch(ctx, kKernDecOps, k_rmsnorm, dim3((unsigned)n), dim3(256), 0,
+                            (const float *)d->x, H, (const float *)d->final_norm, eps, d->h,
+                            (const float *)d->tmp, d->x))) {
       return rc;
-    if ((rc = launch_matmul_nbits(ctx, L.down, d->act, I, n, d->tmp))) return rc;
-    // x += down (the next norm reads x)
-    if ((rc = launch(ctx, kKernDecOps, k_rmsnorm, dim3((unsigned)n), dim3(256), 0,
-                     (const float *)d->x, H, (const float *)d->final_norm, eps, d->h,
-                     (const float *)d->tmp, d->x)))
-      return rc;
+    }
   }
   // greedy token of the last row: final norm fused into lm_head
   if ((rc = launch_dec_gemv(ctx, d->lm, d->x + (n - 1) * H, d->final_norm, eps, kDecArgmax,

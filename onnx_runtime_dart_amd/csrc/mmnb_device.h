@@ -58,4 +58,46 @@ __device__ __forceinline__ void st_act(float *p, float v) {
     *p = v;
 }
 
+// ---- The prefill GEMM's prepared activations (written by k_prep_a, or by a
+// producer kernel that owns whole rows).  Row m is scaled by 2^e_m, e_m
+// chosen from the row's largest magnitude so that it lands in [2^13, 2^14),
+// and split into two fp16 terms hi = fp16(a'), lo = fp16(a' - hi).  Layout:
+// one 1 KB unit per (32-row block, 64-k segment s, 16-k step j, part hi|lo),
+// lane l holding row l%32, k = 64s + 16j + 8(l/32) + {0,4,1,5,2,6,3,7}.
+
+// The row exponent e_m for a row whose largest magnitude is mx (0 for an
+// all-zero or non-finite row).
+__device__ __forceinline__ int prep_a_exponent(float mx) {
+  return (mx > 0.0f && mx < INFINITY) ? 13 - ilogbf(mx) : 0;
+}
+
+typedef _Float16 prep_h8 __attribute__((ext_vector_type(8)));
+
+// Stores k = k0 .. k0+15 (k0 a multiple of 16) of row `row`, values v,
+// exponent ex, into the units of a layout with segsp segments per row block.
+__device__ __forceinline__ void prep_a_store16(uint4 *__restrict__ out, int64_t segsp,
+                                               int64_t row, int64_t k0, const float *v,
+                                               int ex) {
+  const int64_t rb = row >> 5;
+  const int rl = (int)(row & 31);
+  const int64_t s = k0 >> 6;
+  const int j = (int)((k0 >> 4) & 3);
+  const int64_t base = ((rb * segsp + s) * 4 + j) * 2;  // unit index of part 0
+#pragma unroll
+  for (int g = 0; g < 2; g++) {
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = ldexpf(v[8 * g + e], ex);
+      const _Float16 h = (_Float16)x;
+      hi[e] = h;
+      lo[e] = (_Float16)(x - (float)h);
+    }
+    const prep_h8 hv = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
+    const prep_h8 lv = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
+    out[(base + 0) * 64 + 32 * g + rl] = __builtin_bit_cast(uint4, hv);
+    out[(base + 1) * 64 + 32 * g + rl] = __builtin_bit_cast(uint4, lv);
+  }
+}
+
 }  // namespace mmnb

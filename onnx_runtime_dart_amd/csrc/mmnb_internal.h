@@ -86,6 +86,9 @@ struct mmnb_ctx {
   // Prefill attention on the matrix cores (MMNB_ATTN_MFMA: 0 selects the
   // vector-ALU kernel; on by default).
   int attn_mfma = 1;
+  // Decoder prefill: norms / SwiGLU write the GEMM's prepared activations
+  // (MMNB_PREP_FUSE: 0 keeps fp32 rows + k_prep_a; on by default).
+  int prep_fuse = 1;
   // Prefill GEMM LDS stages (2 or 3; MMNB_GEMM_STAGES tuning override).
   int gemm_stages = 2;
   // Prefill GEMM 128-column blocks per tile (MMNB_GEMM_CB: 1 or 2; 0 = auto).
@@ -243,6 +246,15 @@ int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_
 // MatMulNBits: y[m, n] = a[m, k] * W;  lda = row stride of a (elements).
 int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
                         int64_t lda, int64_t m, float *d_y);
+// The prefill GEMM (M > 8) with its activations prepared by the caller's own
+// kernel instead of k_prep_a: gemm_prepared_a returns where to write them
+// (scratch: the hi/lo fp16 units, [mpad / 32][segsp][4][2] x 1 KB, and the
+// int row exponents [mpad]; rows >= M and k >= K zero) for this pack and M;
+// launch_matmul_nbits_prepared then runs the GEMM on them.  Nothing that
+// takes the same scratch may run in between.
+int gemm_prepared_a(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, int64_t *segsp,
+                    int64_t *mpad, void **d_ap, int **d_exp);
+int launch_matmul_nbits_prepared(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, float *d_y);
 
 // DynamicQuantizeLinear on device.
 int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y,

@@ -982,45 +982,23 @@ __global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int
 #pragma unroll
   for (int r = 0; r < kPrepRows; r++) {
     const float m_ = fmaxf(fmaxf(wmax[r][0], wmax[r][1]), fmaxf(wmax[r][2], wmax[r][3]));
-    ex[r] = (m_ > 0.0f && m_ < INFINITY) ? 13 - ilogbf(m_) : 0;
+    ex[r] = prep_a_exponent(m_);
     if (t == 0 && r0 + r < M) row_exp[r0 + r] = ex[r];
   }
   // ---- convert: thread t writes, per 4096-k chunk, step j = t%4 of segment
   // s = chunk*64 + t/4, both halves g, both parts, for its rows
-  const int64_t rb = r0 >> 5;
-  const int rl = (int)(r0 & 31);
   for (int64_t k0 = 16 * t; k0 < kp; k0 += 4096) {
-    const int64_t s = k0 >> 6;
-    const int j = (int)((k0 >> 4) & 3);
-    const int64_t base = ((rb * segsp + s) * 4 + j) * 2;  // unit index of part 0
-    float v[kPrepRows][16];
 #pragma unroll
     for (int r = 0; r < kPrepRows; r++) {
+      float v[16];
       if (k0 < 4096) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) v[r][e] = keep[r][e];
+        for (int e = 0; e < 16; e++) v[e] = keep[r][e];
       } else {
-        load8(r0 + r, k0, &v[r][0]);
-        load8(r0 + r, k0 + 8, &v[r][8]);
+        load8(r0 + r, k0, &v[0]);
+        load8(r0 + r, k0 + 8, &v[8]);
       }
-    }
-#pragma unroll
-    for (int g = 0; g < 2; g++) {
-#pragma unroll
-      for (int r = 0; r < kPrepRows; r++) {
-        _Float16 hi[8], lo[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float x = ldexpf(v[r][8 * g + e], ex[r]);
-          const _Float16 h = (_Float16)x;
-          hi[e] = h;
-          lo[e] = (_Float16)(x - (float)h);
-        }
-        const half8_t hv = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
-        const half8_t lv = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
-        out[(base + 0) * 64 + 32 * g + rl + r] = __builtin_bit_cast(uint4, hv);
-        out[(base + 1) * 64 + 32 * g + rl + r] = __builtin_bit_cast(uint4, lv);
-      }
+      prep_a_store16(out, segsp, r0 + r, k0, v, ex[r]);
     }
   }
 }
@@ -1539,8 +1517,15 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
-static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
-                       int64_t m, float *d_y) {
+// Launch shape of the prefill GEMM for a pack and M (tile width, K groups,
+// LDS stages, K slices) and the padded segment count of the prepared A.
+struct GemmPlan {
+  int64_t segs, mpad, segsp, tiles;
+  int gx, gy, cb, nbps, groups, nst, ksplit;
+  size_t ap_bytes, shmem;
+};
+
+static int gemm_plan(const mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, GemmPlan &pl) {
   const int64_t segs = p->k64 / kSegK;
   const int64_t mpad = (m + kGemmBM - 1) / kGemmBM * kGemmBM;
   const int gy = (int)(mpad / kGemmBM);
@@ -1583,15 +1568,21 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   const size_t shmem = (size_t)groups * nst * (1024 + 256 * cb + 64 * cb * nbps) * 16;
   if (shmem > (size_t)ctx->lds_max)
     return fail(MMNB_ERR_UNSUPPORTED, "GEMM: LDS stages exceed the device limit");
-  void *d_ap = nullptr, *d_exp = nullptr, *d_part = nullptr;
+  pl = GemmPlan{segs, mpad, segsp, tiles, gx, gy, cb, nbps, groups, nst, ksplit, ap_bytes, shmem};
+  return MMNB_OK;
+}
+
+// The GEMM proper on a prepared A (d_ap, d_exp laid out for `pl`).
+static int gemm_run(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, const GemmPlan &pl,
+                    const void *d_ap, const void *d_exp, float *d_y) {
+  const int64_t segs = pl.segs, segsp = pl.segsp, tiles = pl.tiles;
+  const int gx = pl.gx, gy = pl.gy, cb = pl.cb, nbps = pl.nbps, groups = pl.groups,
+            nst = pl.nst, ksplit = pl.ksplit;
+  const size_t shmem = pl.shmem;
+  void *d_part = nullptr;
   int rc;
-  if ((rc = scratch_get(ctx, 2, ap_bytes, &d_ap))) return rc;
-  if ((rc = scratch_get(ctx, 3, (size_t)mpad * 4, &d_exp))) return rc;
   if (ksplit > 1 &&
       (rc = scratch_get(ctx, 10, (size_t)tiles * ksplit * 32 * cb * 256 * 4, &d_part)))
-    return rc;
-  if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(mpad / kPrepRows)), dim3(256), 0,
-                    d_a, lda, m, p->k, segsp, (int *)d_exp, (uint4 *)d_ap)))
     return rc;
   const int bs_log2 = ilog2(p->block);
   const dim3 grid((unsigned)(gx * gy * ksplit));
@@ -1626,6 +1617,44 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   MMNB_GEMM_NB(2, 1, 1);
 #undef MMNB_GEMM_NB
 #undef MMNB_GEMM_LAUNCH
+}
+
+
+static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
+                       int64_t m, float *d_y) {
+  GemmPlan pl;
+  int rc;
+  if ((rc = gemm_plan(ctx, p, m, pl))) return rc;
+  void *d_ap = nullptr, *d_exp = nullptr;
+  if ((rc = scratch_get(ctx, 2, pl.ap_bytes, &d_ap))) return rc;
+  if ((rc = scratch_get(ctx, 3, (size_t)pl.mpad * 4, &d_exp))) return rc;
+  if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(pl.mpad / kPrepRows)), dim3(256), 0,
+                    d_a, lda, m, p->k, pl.segsp, (int *)d_exp, (uint4 *)d_ap)))
+    return rc;
+  return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y);
+}
+
+int gemm_prepared_a(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, int64_t *segsp,
+                    int64_t *mpad, void **d_ap, int **d_exp) {
+  if (m <= 8) return fail(MMNB_ERR_ARG, "prepared A: M <= 8 takes the GEMV");
+  GemmPlan pl;
+  int rc;
+  if ((rc = gemm_plan(ctx, p, m, pl))) return rc;
+  if ((rc = scratch_get(ctx, 2, pl.ap_bytes, d_ap))) return rc;
+  if ((rc = scratch_get(ctx, 3, (size_t)pl.mpad * 4, (void **)d_exp))) return rc;
+  *segsp = pl.segsp;
+  *mpad = pl.mpad;
+  return MMNB_OK;
+}
+
+int launch_matmul_nbits_prepared(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, float *d_y) {
+  GemmPlan pl;
+  int rc;
+  if ((rc = gemm_plan(ctx, p, m, pl))) return rc;
+  void *d_ap = nullptr, *d_exp = nullptr;
+  if ((rc = scratch_get(ctx, 2, pl.ap_bytes, &d_ap))) return rc;
+  if ((rc = scratch_get(ctx, 3, (size_t)pl.mpad * 4, &d_exp))) return rc;
+  return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y);
 }
 
 int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,

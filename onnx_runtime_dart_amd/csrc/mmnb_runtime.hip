@@ -125,6 +125,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v == 0 || v == 1) ctx->attn_mfma = v;
   }
+  if (const char *r = std::getenv("MMNB_PREP_FUSE")) {
+    const int v = std::atoi(r);
+    if (v == 0 || v == 1) ctx->prep_fuse = v;
+  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

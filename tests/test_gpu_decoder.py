@@ -303,6 +303,44 @@ def test_decoder_vs_oracle(ctx, cfg, prompt_len, steps):
         dec.free()
 
 
+@pytest.fixture(scope="module")
+def unfused_ctx():
+    # a context whose decoder prefill writes fp32 norm / SwiGLU rows and runs
+    # k_prep_a before each projection
+    saved = os.environ.get("MMNB_PREP_FUSE")
+    os.environ["MMNB_PREP_FUSE"] = "0"
+    try:
+        c = _lib.Context(0)
+    finally:
+        if saved is None:
+            os.environ.pop("MMNB_PREP_FUSE", None)
+        else:
+            os.environ["MMNB_PREP_FUSE"] = saved
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("cfg,prompt_len", [(SMALL, 20), (QWEN_HEADS, 48), (QWEN_HEADS, 70)],
+                         ids=["small", "qwen_heads", "qwen_heads_two_row_tiles"])
+def test_prefill_fused_prep_bit_identical(ctx, unfused_ctx, cfg, prompt_len):
+    # The norms and SwiGLU that write the GEMM's prepared activations compute
+    # the same fp32 values as the separate kernels + k_prep_a: same logits,
+    # bit for bit, and the same decode afterwards.
+    w = G.random_weights(cfg, seed=11)
+    prompt = np.random.default_rng(prompt_len).integers(0, cfg.vocab, prompt_len)
+    out = []
+    for c in (ctx, unfused_ctx):
+        dec = G.GpuDecoder(w, c)
+        try:
+            tok = dec.prefill(prompt)
+            out.append((tok, dec.logits().copy(), dec.decode(4).copy()))
+        finally:
+            dec.free()
+    assert out[0][0] == out[1][0]
+    np.testing.assert_array_equal(out[0][1], out[1][1])
+    np.testing.assert_array_equal(out[0][2], out[1][2])
+
+
 def test_decoder_argument_errors(ctx):
     w = G.random_weights(SMALL, seed=1)
     dec = G.GpuDecoder(w, ctx)
