@@ -73,31 +73,37 @@ __device__ __forceinline__ int prep_a_exponent(float mx) {
 
 typedef _Float16 prep_h8 __attribute__((ext_vector_type(8)));
 
-// Stores k = k0 .. k0+15 (k0 a multiple of 16) of row `row`, values v,
-// exponent ex, into the units of a layout with segsp segments per row block.
-__device__ __forceinline__ void prep_a_store16(uint4 *__restrict__ out, int64_t segsp,
-                                               int64_t row, int64_t k0, const float *v,
-                                               int ex) {
+// Stores half g (k = k0 + 8g .. k0 + 8g + 7; k0 a multiple of 16) of row
+// `row`, values v[0..7], exponent ex, into the units of a layout with segsp
+// segments per row block.
+__device__ __forceinline__ void prep_a_store8(uint4 *__restrict__ out, int64_t segsp,
+                                              int64_t row, int64_t k0, int g, const float *v,
+                                              int ex) {
   const int64_t rb = row >> 5;
   const int rl = (int)(row & 31);
   const int64_t s = k0 >> 6;
   const int j = (int)((k0 >> 4) & 3);
   const int64_t base = ((rb * segsp + s) * 4 + j) * 2;  // unit index of part 0
+  _Float16 hi[8], lo[8];
 #pragma unroll
-  for (int g = 0; g < 2; g++) {
-    _Float16 hi[8], lo[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float x = ldexpf(v[8 * g + e], ex);
-      const _Float16 h = (_Float16)x;
-      hi[e] = h;
-      lo[e] = (_Float16)(x - (float)h);
-    }
-    const prep_h8 hv = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
-    const prep_h8 lv = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
-    out[(base + 0) * 64 + 32 * g + rl] = __builtin_bit_cast(uint4, hv);
-    out[(base + 1) * 64 + 32 * g + rl] = __builtin_bit_cast(uint4, lv);
+  for (int e = 0; e < 8; e++) {
+    const float x = ldexpf(v[e], ex);
+    const _Float16 h = (_Float16)x;
+    hi[e] = h;
+    lo[e] = (_Float16)(x - (float)h);
   }
+  const prep_h8 hv = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
+  const prep_h8 lv = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
+  out[(base + 0) * 64 + 32 * g + rl] = __builtin_bit_cast(uint4, hv);
+  out[(base + 1) * 64 + 32 * g + rl] = __builtin_bit_cast(uint4, lv);
+}
+
+// Both halves: k = k0 .. k0+15 of row `row`, values v[0..15].
+__device__ __forceinline__ void prep_a_store16(uint4 *__restrict__ out, int64_t segsp,
+                                               int64_t row, int64_t k0, const float *v,
+                                               int ex) {
+  prep_a_store8(out, segsp, row, k0, 0, v, ex);
+  prep_a_store8(out, segsp, row, k0, 1, v + 8, ex);
 }
 
 }  // namespace mmnb

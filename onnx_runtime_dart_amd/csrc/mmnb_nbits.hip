@@ -988,18 +988,23 @@ __global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int
   // ---- convert: thread t writes, per 4096-k chunk, step j = t%4 of segment
   // s = chunk*64 + t/4, both halves g, both parts, for its rows
   for (int64_t k0 = 16 * t; k0 < kp; k0 += 4096) {
+    float v[kPrepRows][16];
 #pragma unroll
     for (int r = 0; r < kPrepRows; r++) {
-      float v[16];
       if (k0 < 4096) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) v[e] = keep[r][e];
+        for (int e = 0; e < 16; e++) v[r][e] = keep[r][e];
       } else {
-        load8(r0 + r, k0, &v[0]);
-        load8(r0 + r, k0 + 8, &v[8]);
+        load8(r0 + r, k0, &v[r][0]);
+        load8(r0 + r, k0 + 8, &v[r][8]);
       }
-      prep_a_store16(out, segsp, r0 + r, k0, v, ex[r]);
     }
+    // the rows' pieces of one half are adjacent (rl, rl+1): store them
+    // back to back
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+      for (int r = 0; r < kPrepRows; r++) prep_a_store8(out, segsp, r0 + r, k0, g, &v[r][8 * g], ex[r]);
   }
 }
 
