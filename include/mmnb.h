@@ -420,7 +420,9 @@ int mmnb_decoder_logits(mmnb_decoder *dec, float *logits);
 /* Tokens held in the KV cache. */
 int mmnb_decoder_position(mmnb_decoder *dec, int64_t *pos);
 /* Decode steps replay the recorded HIP graph (use_graph != 0, the default)
- * or launch the step's kernels one by one (for per-kernel timing). */
+ * or launch the step's kernels one by one.  While kernel timing is on
+ * (mmnb_kernel_timing) steps always launch one by one, so that no timing
+ * event is recorded into the graph. */
 int mmnb_decoder_set_graph(mmnb_decoder *dec, int use_graph);
 /* Empty the KV cache (weights stay). */
 int mmnb_decoder_reset(mmnb_decoder *dec);

@@ -945,12 +945,14 @@ __global__ __launch_bounds__(256) void k_dec_attn(const DecState *__restrict__ s
   const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
   if (split >= nsplit) return;  // whole workgroup
   dec_attn_partial<HD, false>(a, pos, split, kh);
-  // ---- publish: every partial store has completed before the count moves
+  // ---- publish: the barrier orders every thread's partial stores before
+  // thread 0's count; its release (agent scope) pairs with the last split's
+  // acquire, and that workgroup's barrier extends it to the merge's loads.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev =
-        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == nsplit - 1;
   }
   __syncthreads();
@@ -1470,7 +1472,9 @@ int mmnb_decoder_decode(mmnb_decoder *d, int64_t steps, int32_t *tokens) {
   if (rc) return rc;
   hipStream_t s = ctx->stream;
   const int64_t first = d->steps_done;
-  if (!d->use_graph) {
+  // Kernel timing takes events from each dispatch, which a graph would
+  // capture and replay: with timing on, the steps launch eagerly instead.
+  if (!d->use_graph || ctx->timing) {
     for (int64_t i = 0; i < steps; i++)
       if ((rc = dec_record_step(d))) return rc;
     if (tokens)

@@ -390,7 +390,12 @@ int64_t attr_i(const Node &n, const char *name, int64_t dflt, bool *found = null
   return ok ? it->second.i : dflt;
 }
 
-int dt_float(int dtype) { return dtype == kF16 ? MMNB_DT_F16 : MMNB_DT_F32; }
+// MMNB_DT_F32 / MMNB_DT_F16 for a float initializer, 0 for any other type
+// (a uint8 or int32 tensor is not reinterpreted as floats: its byte length
+// was checked for its own element size).
+int dt_float(int dtype) {
+  return dtype == kF16 ? MMNB_DT_F16 : dtype == kF32 ? MMNB_DT_F32 : 0;
+}
 
 std::vector<int64_t> to_i64(const Bytes &b) {
   std::vector<int64_t> v((size_t)b.count());
@@ -497,11 +502,18 @@ int mmnb_model_load(mmnb_ctx *ctx, const char *path, mmnb_model **out) {
       d.scales = bs.p;
       d.scales_len = bs.count();
       d.scales_type = dt_float(ts->dtype);
+      if (!d.scales_type)
+        return cleanup(fail(MMNB_ERR_UNSUPPORTED, "MatMulNBits " + label +
+                                                      ": scales must be float or float16"));
       if (tz) {
         if ((rc = ld.bytes(*tz, &bz))) return cleanup(rc);
         d.zero_points = bz.p;
         d.zero_points_len = bz.count();
         d.zero_points_type = tz->dtype == kU8 ? MMNB_DT_U8 : dt_float(tz->dtype);
+        if (!d.zero_points_type)
+          return cleanup(fail(MMNB_ERR_UNSUPPORTED,
+                              "MatMulNBits " + label +
+                                  ": zero points must be uint8, float or float16"));
         d.zero_points_layout = tz->dims.size() == 2 ? MMNB_ZP_PER_COLUMN : MMNB_ZP_FLAT;
       }
       std::vector<int32_t> g32;
@@ -521,6 +533,9 @@ int mmnb_model_load(mmnb_ctx *ctx, const char *path, mmnb_model **out) {
         d.bias = bbias.p;
         d.bias_len = bbias.count();
         d.bias_type = dt_float(tbias->dtype);
+        if (!d.bias_type)
+          return cleanup(fail(MMNB_ERR_UNSUPPORTED,
+                              "MatMulNBits " + label + ": bias must be float or float16"));
       }
       if ((rc = mmnb_pack_nbits_ex(ctx, &d, &pack))) return cleanup(rc);
     } else if (n.op == "MatMulInteger" || n.op == "QLinearMatMul") {
@@ -535,6 +550,8 @@ int mmnb_model_load(mmnb_ctx *ctx, const char *path, mmnb_model **out) {
       std::vector<int64_t> z;
       if (tz) {
         if ((rc = ld.bytes(*tz, &bz))) return cleanup(rc);
+        if (tz->dtype != kU8 && tz->dtype != kI8)
+          return cleanup(fail(MMNB_ERR_UNSUPPORTED, n.op + ": zero point must be uint8/int8"));
         z = to_i64(bz);
       }
       const int64_t kk = tb->dims[tb->dims.size() - 2], nn = tb->dims.back();
@@ -558,6 +575,8 @@ int mmnb_model_load(mmnb_ctx *ctx, const char *path, mmnb_model **out) {
       std::vector<int64_t> z;
       if (tz) {
         if ((rc = ld.bytes(*tz, &bz))) return cleanup(rc);
+        if (tz->dtype != kU8 && tz->dtype != kI8)
+          return cleanup(fail(MMNB_ERR_UNSUPPORTED, n.op + ": zero point must be uint8/int8"));
         z = to_i64(bz);
       }
       if ((rc = mmnb_pack_conv(ctx, bw.p, tw->dtype == kI8, dims[0], dims[1], dims[2], dims[3],

@@ -168,9 +168,11 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) 
 // Every lane issues all of its R weight loads (16 B each), their scales and
 // zero points, and its 32 activations before doing any arithmetic, so a
 // workgroup has its whole share of the weight stream in flight at once.  The
-// activations of a chunk are loaded once and reused for R columns.  Per dword
-// the lane forms sum_e a*q and folds the block's zero point through sum a:
-//     acc += scale * (sum a*q) - (scale*zp) * (sum a).
+// activations of a chunk are loaded once and reused for R columns.  Each
+// nibble becomes the exact (q - zp), scaled by a power of two (dq_nibbles),
+// before the fp32 FMAs: acc += scale * sum a * (q - zp), as the reference's
+// per-weight (q - zp) * scale (a block whose nibbles all equal the zero
+// point adds exactly zero).
 // The 32 lanes of a column half-wave reduce with DPP/swizzle, the waves
 // through LDS.
 // ---------------------------------------------------------------------------
@@ -266,25 +268,15 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
       for (int r = 0; r < R; r++)
         wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
     }
-    // ---- arithmetic
-    float sc[R][NBPC], sz[R][NBPC];
+    // ---- arithmetic: exact (q - zp) per weight, scaled by dq_unscale
+    float sc[R][NBPC];
+    uint32_t zc[R][NBPC];
 #pragma unroll
     for (int q = 0; q < NBPC; q++)
 #pragma unroll
       for (int r = 0; r < R; r++) {
-        const int zpv = HAS_ZP ? (int)((zraw[r][q] >> zsh[r][q]) & 0xF) : 8;
         sc[r][q] = inbq[q] ? sraw[r][q] : 0.0f;
-        sz[r][q] = inbq[q] ? sraw[r][q] * (float)zpv : 0.0f;
-      }
-    float sa[M][NBPC];
-#pragma unroll
-    for (int m = 0; m < M; m++)
-#pragma unroll
-      for (int q = 0; q < NBPC; q++) {
-        float v = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32 / NBPC; e++) v += av[m][q * (32 / NBPC) + e];
-        sa[m][q] = v;
+        zc[r][q] = HAS_ZP ? dq8_const((int)((zraw[r][q] >> zsh[r][q]) & 0xF)) : 0u;
       }
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -297,26 +289,15 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
 #pragma unroll
         for (int jj = 0; jj < 4 / NBPC; jj++) {
           const int j = q * (4 / NBPC) + jj;
-          const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
           float qv[8];
-          qv[0] = (float)(lo & 0xFF);
-          qv[1] = (float)(hi & 0xFF);
-          qv[2] = (float)((lo >> 8) & 0xFF);
-          qv[3] = (float)((hi >> 8) & 0xFF);
-          qv[4] = (float)((lo >> 16) & 0xFF);
-          qv[5] = (float)((hi >> 16) & 0xFF);
-          qv[6] = (float)(lo >> 24);
-          qv[7] = (float)(hi >> 24);
+          dq_nibbles<HAS_ZP>(wd[j], zc[r][q], qv);
 #pragma unroll
           for (int m = 0; m < M; m++)
 #pragma unroll
             for (int e = 0; e < 8; e++) d[m] = fmaf(av[m][8 * j + e], qv[e], d[m]);
         }
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-          acc[m][r] = fmaf(sc[r][q], d[m], acc[m][r]);
-          acc[m][r] = fmaf(-sz[r][q], sa[m][q], acc[m][r]);
-        }
+        for (int m = 0; m < M; m++) acc[m][r] = fmaf(sc[r][q], d[m], acc[m][r]);
       }
     }
   }
@@ -334,7 +315,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     float v = 0.0f;
     for (int ww = 0; ww < nw; ww++) v += red[ww][m][cl];
     const int col = col0 + cl;
-    if (col < N) Y[(int64_t)m * N + col] = v;
+    if (col < N) Y[(int64_t)m * N + col] = v * dq_unscale<HAS_ZP>();
   }
 }
 
@@ -383,8 +364,8 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
 //          kDecArgmax (lm_head: each workgroup stores the best key
 //          (orderable value << 32 | ~index) of its columns; the greedy
 //          token is the maximum key, ties going to the lowest index).
-// Lane layout and arithmetic follow k_gemv_valu with M = 1 and one
-// quantisation block per chunk; K is at most 4096 (one chunk per lane).
+// Lane layout and arithmetic (exact q - 8 per weight) follow k_gemv_valu
+// with M = 1 and one quantisation block per chunk; K is at most 4096 (one chunk per lane).
 // ---------------------------------------------------------------------------
 
 template <int R, bool NORM, int EPI>
@@ -455,10 +436,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
 #pragma unroll
     for (int e = 0; e < 32; e++) av[e] = av[e] * inv * gv[e];
   }
-  // ---- arithmetic (zero point 8: acc += sc * sum(a q) - 8 sc * sum(a))
-  float sa = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 32; e++) sa += av[e];
+  // ---- arithmetic: exact 16 (q - 8) per weight (dq_nibbles), unscaled below
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -466,22 +444,13 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
     float d = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
       float qv[8];
-      qv[0] = (float)(lo & 0xFF);
-      qv[1] = (float)(hi & 0xFF);
-      qv[2] = (float)((lo >> 8) & 0xFF);
-      qv[3] = (float)((hi >> 8) & 0xFF);
-      qv[4] = (float)((lo >> 16) & 0xFF);
-      qv[5] = (float)((hi >> 16) & 0xFF);
-      qv[6] = (float)(lo >> 24);
-      qv[7] = (float)(hi >> 24);
+      dq_nibbles<false>(wd[j], 0u, qv);
 #pragma unroll
       for (int e = 0; e < 8; e++) d = fmaf(av[8 * j + e], qv[e], d);
     }
     const float sc = cv ? sraw[r] : 0.0f;
-    acc[r] = fmaf(sc, d, 0.0f);
-    acc[r] = fmaf(-8.0f * sc, sa, acc[r]);
+    acc[r] = sc * d;
   }
   // ---- reductions: 32 lanes of a half-wave, then the waves
 #pragma unroll
@@ -494,6 +463,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
   const int i = threadIdx.x;
   if (i < 2 * R) {
     for (int ww = 0; ww < nw; ww++) v += red[ww][i];
+    v *= dq_unscale<false>();
   }
   const int col = col0 + i;
   if constexpr (EPI == kDecPlain) {
@@ -590,8 +560,8 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
 // r < R).  A workgroup runs cg column groups side by side (cg*kw waves)
 // and walks the groups grid-stride, reusing the staged activations.  Per
 // dword j of a chunk a lane reads its 8*M activations once and applies them
-// to its R columns.  Each nibble becomes float(q) - zp (exact) before the
-// fp32 FMAs, so no separate zero-point term is needed.
+// to its R columns.  Each nibble becomes the exact (q - zp), scaled by a
+// power of two (dq_nibbles), before the fp32 FMAs.
 // ---------------------------------------------------------------------------
 // Weight, scale and zero-point loads of one chunk (lane's chunk c of its R
 // columns); kept separate so the first group's loads can be issued before
@@ -725,20 +695,11 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
         }
 #pragma unroll
         for (int r = 0; r < R; r++) {
-          const float zf = HAS_ZP ? (float)((ch.zraw[r][q] >> ch.zsh[r][q]) & 0xF) : 8.0f;
-          // byte converts and subtracts run at the full VALU rate (mixed
-          // fp16/fp32 FMAs and packed fp16 ops at half rate on gfx950)
-          const uint32_t wd = ch.wv[r][j];
-          const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+          const uint32_t zc =
+              HAS_ZP ? dq8_const((int)((ch.zraw[r][q] >> ch.zsh[r][q]) & 0xF)) : 0u;
+          // exact scaled (q - zp), one SDWA convert per nibble (dq_nibbles)
           float qv[8];
-          qv[0] = (float)(lo & 0xFF) - zf;
-          qv[1] = (float)(hi & 0xFF) - zf;
-          qv[2] = (float)((lo >> 8) & 0xFF) - zf;
-          qv[3] = (float)((hi >> 8) & 0xFF) - zf;
-          qv[4] = (float)((lo >> 16) & 0xFF) - zf;
-          qv[5] = (float)((hi >> 16) & 0xFF) - zf;
-          qv[6] = (float)(lo >> 24) - zf;
-          qv[7] = (float)(hi >> 24) - zf;
+          dq_nibbles<HAS_ZP>(ch.wv[r][j], zc, qv);
 #pragma unroll
           for (int m = 0; m < M; m++) {
             float x = d[m][r];
@@ -782,7 +743,7 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
       float v = 0.0f;
       for (int ww = 0; ww < kw; ww++) v += red[sg * kw + ww][m][cl];
       const int col = gi * (2 * R) + cl;
-      if (gi < groups && col < N) Y[(int64_t)m * N + col] = v;
+      if (gi < groups && col < N) Y[(int64_t)m * N + col] = v * dq_unscale<HAS_ZP>();
     }
     __syncthreads();
   }
@@ -1473,11 +1434,15 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
             st_act<true>(pt + (size_t)split * kPart + ((rb * CB + cb) * 16 + r) * 256 + tid,
                          acc[rb][cb][r]);
     }
+    // Ordering: the workgroup barrier orders every thread's partial stores
+    // before thread 0's count, whose release (agent scope) pairs with the
+    // acquire of the last slice's count, which the barrier below extends to
+    // that workgroup's loads.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
       const int prev =
-          __hip_atomic_fetch_add(&tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(&tile_cnt[tile], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       s_last = prev == ksplit - 1;
     }
     __syncthreads();

@@ -341,6 +341,83 @@ def test_prefill_fused_prep_bit_identical(ctx, unfused_ctx, cfg, prompt_len):
     np.testing.assert_array_equal(out[0][2], out[1][2])
 
 
+def prune_matrix(m, rng, dead_cols=0.125, keep=0.01):
+    """Nibbles set to 8 (the zero point of a pack without zero points, so
+    W = 0 exactly): whole columns (returned) and all but `keep` of the rest."""
+    n, nb, half = m.b_q.shape
+    q = np.stack([m.b_q & 0xF, m.b_q >> 4], -1)
+    dead = rng.random(q.shape) >= keep
+    cols = np.flatnonzero(rng.random(n) < dead_cols)
+    dead[cols] = True
+    q = np.where(dead, 8, q)
+    m.b_q = (q[..., 0] | (q[..., 1] << 4)).astype(np.uint8)
+    return cols
+
+
+def test_decoder_pruned_weights_vs_oracle(ctx):
+    # Every MatMulNBits of the session (the decode GEMVs with their fused
+    # norms / epilogues included) on weights that mostly equal the zero point:
+    # logits of all-zero lm_head columns are exactly 0, as in the reference,
+    # and the rest match the oracle.
+    w = G.random_weights(SMALL, seed=13)
+    rng = np.random.default_rng(17)
+    for L in w.layers:
+        for name in ("q", "k", "v", "o", "gate", "up", "down"):
+            prune_matrix(getattr(L, name), rng, dead_cols=0.0, keep=0.05)
+    dead = prune_matrix(w.lm_head, rng)
+    assert dead.size > 0
+    prompt = rng.integers(0, SMALL.vocab, 12)
+    dec = G.GpuDecoder(w, ctx)
+    try:
+        ref = oracle_model(w)
+        ref_logits = ref.forward(prompt)[-1]
+        tok = dec.prefill(prompt)
+        got = dec.logits()
+        assert np.all(got[dead] == 0.0)
+        assert normwise_rel_err(got, ref_logits) <= DEC_TOL
+        check_token(tok, ref_logits)
+        toks = dec.decode(6)
+        feed = tok
+        for i in range(6):
+            ref_logits = ref.forward([feed])[-1]
+            check_token(int(toks[i]), ref_logits)
+            feed = int(toks[i])
+        got = dec.logits()
+        assert np.all(got[dead] == 0.0)
+        assert normwise_rel_err(got, ref_logits) <= DEC_TOL
+    finally:
+        dec.free()
+
+
+def test_decode_with_kernel_timing_launches_eagerly(ctx):
+    # With kernel timing on, a decode launches the step's kernels one by one
+    # (no graph holds the timing events): same tokens as the graph replay, and
+    # every step's kernels are in the timing record.
+    w = G.random_weights(SMALL, seed=3)
+    prompt = np.arange(9) * 7
+    dec = G.GpuDecoder(w, ctx)
+    try:
+        dec.prefill(prompt)
+        ref = dec.decode(5).copy()
+        dec.reset()
+        dec.prefill(prompt)
+        ctx.kernel_timing(True, max_launches=4096)
+        try:
+            got = dec.decode(5).copy()
+            kt = ctx.kernel_timing_read()
+        finally:
+            ctx.kernel_timing(False)
+        np.testing.assert_array_equal(got, ref)
+        assert kt["k_dec_gemv_lm"][0] == 5
+        assert kt["k_dec_attn"][0] == 5 * SMALL.layers
+        # a graph recorded after timing is switched off replays as before
+        dec.reset()
+        dec.prefill(prompt)
+        np.testing.assert_array_equal(dec.decode(5), ref)
+    finally:
+        dec.free()
+
+
 def test_decoder_argument_errors(ctx):
     w = G.random_weights(SMALL, seed=1)
     dec = G.GpuDecoder(w, ctx)

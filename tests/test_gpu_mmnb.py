@@ -105,10 +105,16 @@ def test_prefill_full_oracle(ctx, m, n, block):
     p = synth.mmnb_problem(m, 4096, n, block, True, seed=2, outlier_frac=0.01)
     y = run_gpu(ctx, p)
     assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
 
 
-@pytest.mark.parametrize("m,n,block", [(512, 4096, 32), (512, 14336, 128),
-                                       (2048, 4096, 128), (2048, 14336, 32)])
+# Every (M, N, block) of the prefill sweep: M in {128, 512, 2048}, K = 4096,
+# N in {4096, 14336}, block 32 and 128 with zero points (the launch shape --
+# tile width, K slices -- differs across them).
+C3 = [(m, n, b) for m in (128, 512, 2048) for n in (4096, 14336) for b in (32, 128)]
+
+
+@pytest.mark.parametrize("m,n,block", C3)
 def test_prefill_full_size_row_sample(ctx, m, n, block):
     # Rows are independent: the oracle on a sample of rows is the exact
     # reference for those rows of the full-size product.
@@ -196,6 +202,65 @@ def test_zero_rows_and_tiny_magnitudes(ctx):
         if r == 3:
             continue
         assert normwise_rel_err(y[r], ref[r]) <= TOL, r
+
+
+def zero_point_grid(p):
+    """[n, n_blocks] zero point of every (column, block): nibble
+    col * n_blocks + blk of the packed input, low nibble first, or 8 without
+    one (onnx_qlinear_ops.dart:132-137)."""
+    nb = p.n_blocks
+    if p.zero_points is None:
+        return np.full((p.n, nb), 8, np.uint8)
+    zi = np.arange(p.n * nb)
+    return ((p.zero_points[zi >> 1] >> (4 * (zi & 1))) & 0xF).astype(np.uint8).reshape(p.n, nb)
+
+
+def prune_to_zero_point(p, seed, dead_cols=0.125, dead_blocks=0.25, keep=None):
+    """Sets nibbles to their block's zero point, so that W = (q - zp) * scale
+    is exactly 0 there: whole columns (returned), whole (column, block)
+    pairs and, with `keep`, all but that fraction of the other weights.
+    Padding nibbles past K stay zero."""
+    rng = np.random.default_rng(seed)
+    n, nb, half = p.b_q.shape
+    q = np.stack([p.b_q & 0xF, p.b_q >> 4], -1).reshape(n, nb, 2 * half)
+    z = np.broadcast_to(zero_point_grid(p)[:, :, None], q.shape)
+    dead = rng.random(q.shape) >= (1.0 if keep is None else keep)
+    dead |= (rng.random((n, nb)) < dead_blocks)[:, :, None]
+    cols = np.flatnonzero(rng.random(n) < dead_cols)
+    dead[cols] = True
+    q = np.where(dead, z, q)
+    q = q.reshape(n, nb * 2 * half)
+    q[:, p.k:] = 0
+    q = q.reshape(n, nb, half, 2)
+    p.b_q = (q[..., 0] | (q[..., 1] << 4)).astype(np.uint8)
+    return cols
+
+
+@pytest.mark.parametrize("m", [1, 4, 64])
+@pytest.mark.parametrize("block,zp", [(128, False), (32, True), (64, True)])
+@pytest.mark.parametrize("keep", [None, 0.001], ids=["blocks", "sparse"])
+def test_weights_equal_to_zero_point(ctx, m, block, zp, keep):
+    # Pruned weights: columns and blocks whose nibbles all equal the zero
+    # point give W = 0 exactly in the reference, and so exactly 0 here; the
+    # accumulation bound (sum |a||W| is small) catches a zero point folded in
+    # after the products (scale * sum a q - scale * zp * sum a).
+    p = synth.mmnb_problem(m, 4096, 512, block, zp, seed=31 + m + block)
+    cols = prune_to_zero_point(p, seed=block + m, keep=keep)
+    assert cols.size > 0
+    y = run_gpu(ctx, p)
+    assert np.all(y[:, cols] == 0.0)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
+
+
+@pytest.mark.parametrize("k,block,zp", [(9000, 128, True), (12288, 32, False)])
+def test_weights_equal_to_zero_point_long_k(ctx, k, block, zp):
+    p = synth.mmnb_problem(1, k, 300, block, zp, seed=41)
+    cols = prune_to_zero_point(p, seed=k, keep=0.002)
+    y = run_gpu(ctx, p)
+    assert np.all(y[:, cols] == 0.0)
+    assert normwise_rel_err(y, oracle(p)) <= TOL
+    check_bound(p, y)
 
 
 def test_all_zero_nibbles_closed_form(ctx):

@@ -139,3 +139,48 @@ def test_malformed_file_rejects(ctx, tmp_path):
     path.write_bytes(b"\x3a\xff\xff\xff\xff\x0f garbage")
     with pytest.raises(ValueError):
         LoadedModel(path, ctx)
+
+
+@pytest.mark.parametrize("which,arr", [
+    ("scales", np.ones((4, 1), np.uint8)),            # 1 byte per value, read as floats
+    ("scales", np.ones((4, 1), np.int32)),
+    ("zero_points", np.full((4, 1), 8, np.int8)),
+    ("bias", np.zeros(4, np.int32)),
+])
+def test_wrong_initializer_types_are_unsupported(ctx, tmp_path, which, arr):
+    # Scales, bias and float zero points must be float / float16 and packed
+    # zero points uint8: another type is rejected before anything reads its
+    # bytes with the wrong element size.
+    b = np.zeros((4, 1, 16), np.uint8)
+    ins = {"scales": np.ones((4, 1), np.float32), "zero_points": None, "bias": None}
+    ins[which] = arr
+    inits = [W.tensor("B", b), W.tensor("S", ins["scales"])]
+    names = ["A", "B", "S"]
+    if ins["zero_points"] is not None or ins["bias"] is not None:
+        names.append("Z" if ins["zero_points"] is not None else "")
+        if ins["zero_points"] is not None:
+            inits.append(W.tensor("Z", ins["zero_points"]))
+    if ins["bias"] is not None:
+        names += ["", "BIAS"]
+        inits.append(W.tensor("BIAS", ins["bias"]))
+    nodes = [W.node("MatMulNBits", names, ["Y"], K=32, N=4, bits=4, block_size=32)]
+    path = tmp_path / "m.onnx"
+    path.write_bytes(W.model(nodes, inits))
+    with pytest.raises(NotImplementedError):
+        LoadedModel(path, ctx)
+
+
+@pytest.mark.parametrize("op", ["MatMulInteger", "ConvInteger"])
+def test_integer_op_zero_point_must_be_8_bit(ctx, tmp_path, op):
+    if op == "MatMulInteger":
+        w = np.zeros((16, 8), np.int8)
+        zp = np.zeros(8, np.int32)
+    else:
+        w = np.zeros((4, 2, 3, 3), np.int8)
+        zp = np.zeros(4, np.int32)
+    inits = [W.tensor("W", w), W.tensor("Z", zp)]
+    nodes = [W.node(op, ["X", "W", "", "Z"], ["Y"])]
+    path = tmp_path / "m.onnx"
+    path.write_bytes(W.model(nodes, inits))
+    with pytest.raises(NotImplementedError):
+        LoadedModel(path, ctx)
