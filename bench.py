@@ -3,18 +3,23 @@
 
 Headline (the JSON line's "value"): the decode-shape MatMulNBits GEMV,
 M=1, K=N=4096, block 128, symmetric, in GB/s of algorithmic traffic
-(K*N/2 + N*ceil(K/bs)*4 + M*K*4 + M*N*4 bytes per call).  One step = one
-MatMulNBits call on one weight pack; the packs rotate over > 300 MB of
-distinct weights (more than the 256 MB Infinity Cache) so every call streams
-its weights from HBM.  The timed region replays a HIP graph of the rotation
-(so host launch overhead does not starve the GPU), bracketed by device
-synchronisation and HIP events on the library's stream.
+(K*N/2 + N*ceil(K/bs)*4 + M*K*4 + M*N*4 bytes per call).  One step is one
+pass of the operator over one batch of synthetic weights: a call on each of
+P distinct weight packs (P = 38 at the headline, > 300 MB, more than the
+256 MB Infinity Cache, so every call streams its weights from HBM).  A step
+is recorded once as a HIP graph; --warmup replays run untimed, then exactly
+--steps replays are timed between device synchronisations with HIP events
+on the library's stream (the stream the kernels run on).
 
 Also reported (extra keys on the same line):
-  roofline      the GEMV kernel: achieved GB/s from its own dispatch events
-                (kernel execution time, what rocprofv3 kernel-trace reports)
+  roofline      the GEMV kernel: algorithmic bytes per launch / its average
+                launch duration over the timed region (timed region / launches,
+                every launch in it being that kernel); the per-dispatch event
+                duration is listed beside it
   cpu_baseline  the oracle (a C restatement of the reference's Dart
-                algorithm) on the host, single thread, bounded sample
+                algorithm) on the host: the headline call, plus legs for the
+                single-node config, the M=512 prefill GEMM and the int8 chain
+                (one warmup, then min and mean over the timed calls)
   gemm          prefill GEMM M=512, K=N=4096, block 32 with zero points:
                 TFLOP/s and its MFMA roofline
   int8          DynamicQuantizeLinear [512,1024] -> MatMulInteger
@@ -64,34 +69,33 @@ def make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed):
 
 
 def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup):
-    """Whole-job time per call (graph replay) and kernel durations per name."""
+    """One step = one call on each pack (recorded once as a HIP graph).
+    Returns (timed steps, ms per step, ms per call, dispatch-event kernel
+    durations per name)."""
     P = len(packs)
 
     def issue_round():
         for p in packs:
             lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, p.handle, da.ptr, m, dy.ptr))
 
-    # warmup (also sizes any scratch before capture)
-    for _ in range(max(1, warmup // P)):
-        issue_round()
+    issue_round()  # sizes any scratch before capture
     ctx.synchronize()
     ctx.graph_begin()
     issue_round()
     g = ctx.graph_end()
-    reps = max(1, steps // P)
-    for _ in range(max(1, warmup // P)):
+    for _ in range(warmup):
         ctx.graph_launch(g)
     ctx.synchronize()
     ctx.event_record(0)
-    for _ in range(reps):
+    for _ in range(steps):
         ctx.graph_launch(g)
     ctx.event_record(1)
     ctx.synchronize()
     total_ms = ctx.event_elapsed_ms(0, 1)
     ctx.graph_destroy(g)
-    n_steps = reps * P
-    # kernel durations from the dispatches themselves
-    nk = min(n_steps, 4096)
+    # per-dispatch event durations, for reference (they include a fixed
+    # dispatch cost that back-to-back launches do not pay)
+    nk = min(steps * P, 2048)
     ctx.kernel_timing(True, max_launches=4 * nk)
     done = 0
     while done < nk:
@@ -99,7 +103,7 @@ def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup):
         done += P
     kt = ctx.kernel_timing_read()
     ctx.kernel_timing(False)
-    return n_steps, total_ms / n_steps, kt
+    return steps, total_ms / steps, total_ms / (steps * P), kt
 
 
 def kernel_avg_ms(kt, name):
@@ -108,19 +112,21 @@ def kernel_avg_ms(kt, name):
 
 
 def bench_gemv(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup, seed=1):
-    per_pack = mmnb_bytes(m, k, n, bs, zp)
+    per_call = mmnb_bytes(m, k, n, bs, zp)
     count = max(2, int(np.ceil(ROTATE_BYTES / (k * n // 2 + n * ((k + bs - 1) // bs) * 4))))
     packs = make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed)
     a = synth.activations(m, k, seed)
     da = ctx.to_device(a)
     dy = ctx.alloc(m * n * 4)
-    n_steps, ms_step, kt = time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup)
+    n_steps, ms_step, ms_call, kt = time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup)
     kname = "k_gemv_valu" if "k_gemv_valu" in kt else sorted(kt)[0]
-    kms = kernel_avg_ms(kt, kname)
+    ev_ms = kernel_avg_ms(kt, kname)
     res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "packs": count,
-           "bytes_per_call": per_pack, "steps": n_steps, "ms_per_call": ms_step,
-           "gbs": per_pack / (ms_step * 1e-3) / 1e9, "kernel": kname,
-           "kernel_ms": kms, "kernel_gbs": per_pack / (kms * 1e-3) / 1e9,
+           "bytes_per_call": per_call, "bytes_per_step": per_call * count,
+           "steps": n_steps, "calls": n_steps * count, "ms_per_step": ms_step,
+           "ms_per_call": ms_call, "gbs": per_call / (ms_call * 1e-3) / 1e9, "kernel": kname,
+           "kernel_ms": ms_call, "kernel_gbs": per_call / (ms_call * 1e-3) / 1e9,
+           "dispatch_event_us": ev_ms * 1e3,
            "kernels": {k_: {"count": v[0], "avg_us": v[1] / v[0] * 1e3,
                             "min_us": v[2] * 1e3, "max_us": v[3] * 1e3}
                        for k_, v in kt.items()}}
@@ -137,7 +143,7 @@ def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
                           ctx=ctx)
     da = ctx.to_device(p.a)
     dy = ctx.alloc(m * n * 4)
-    n_steps, ms_step, kt = time_mmnb(ctx, lib, [pack], da, m, dy, steps, warmup)
+    n_steps, _, ms_step, kt = time_mmnb(ctx, lib, [pack], da, m, dy, steps, warmup)
     flops = 2.0 * m * k * n
     gk = kernel_avg_ms(kt, "k_gemm_mfma")
     # k_prep_a: the activation prep launch (row exponents and hi/lo split)
@@ -449,38 +455,82 @@ def measured_traffic(workload):
         return None
 
 
-def cpu_baseline(synth, m, k, n, bs, zp, budget_s):
-    """The oracle (C restatement of the reference's Dart MatMulNBits:
-    dequantise to a fresh K x N fp32 buffer, then the sequential-k fp32
-    GEMV) timed on this host, single thread: the reference runs this op on
-    one isolate (its pool never takes MatMulNBits)."""
-    from oracle import refcpu
-
-    p = synth.mmnb_problem(m, k, n, bs, zp, seed=1, scale_range=(0.002, 0.02))
-    refcpu.matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k, n, 4, bs)  # warm
+def _time_cpu(fn, budget_s, min_iters=2):
+    """tool/bench.dart's method: one untimed warmup call, then timed calls
+    until the budget is spent (at least min_iters); (min, mean, count) in s."""
+    fn()
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    while time.perf_counter() < t_end or len(times) < min_iters:
         t0 = time.perf_counter()
-        refcpu.matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k, n, 4, bs)
+        fn()
         times.append(time.perf_counter() - t0)
-    per = mmnb_bytes(m, k, n, bs, zp)
-    mean = float(np.mean(times))
-    threads = refcpu.host_threads()
-    # column-sliced multi-thread variant (the pool's partition), for context
-    tmt = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        refcpu.matmul_nbits(p.a, p.b_q, p.scales, p.zero_points, k, n, 4, bs,
-                            threads=threads)
-        tmt.append(time.perf_counter() - t0)
-    return {"value": per / mean / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"MatMulNBits M={m} K={k} N={n} block {bs} "
-                      f"{'with' if zp else 'no'} zero points, {len(times)} calls "
-                      f"({sum(times):.1f} s), mean {mean * 1e3:.1f} ms/call, "
-                      f"min {min(times) * 1e3:.1f} ms",
-            "multi_thread": {"value": per / float(np.min(tmt)) / 1e9, "cores": threads,
-                             "ms_per_call": float(np.min(tmt)) * 1e3}}
+    return min(times), float(np.mean(times)), len(times)
+
+
+def cpu_baseline(synth, budget_s):
+    """The oracle (C restatement of the reference's Dart arithmetic) timed on
+    this host.  MatMulNBits dequantises to a fresh K x N fp32 buffer, then
+    runs the sequential-k fp32 GEMV/GEMM; the reference runs it on one
+    isolate (its pool never takes MatMulNBits, onnx_graph.dart:578-614), so
+    the headline figure is single-threaded.  Legs: the single-node config,
+    the M=512 prefill GEMM (all host threads, column-sliced like the pool's
+    partition, plus one thread on a 16-row sample) and the int8 chain
+    (DynamicQuantizeLinear -> MatMulInteger -> rescale, one thread)."""
+    from oracle import refcpu
+
+    threads = min(16, refcpu.host_threads())
+    # headline: M=1 K=N=4096 block 128, symmetric
+    m, k, n, bs = 1, 4096, 4096, 128
+    p = synth.mmnb_problem(m, k, n, bs, False, seed=1, scale_range=(0.002, 0.02))
+    lo, mean, cnt = _time_cpu(lambda: refcpu.matmul_nbits(p.a, p.b_q, p.scales, None, k, n, 4,
+                                                          bs), 0.35 * budget_s)
+    per = mmnb_bytes(m, k, n, bs, False)
+    out = {"value": per / mean / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"MatMulNBits M={m} K={k} N={n} block {bs}, no zero points: 1 warmup + "
+                     f"{cnt} timed calls, mean {mean * 1e3:.1f} ms, min {lo * 1e3:.1f} ms",
+           "min_ms": lo * 1e3, "mean_ms": mean * 1e3}
+    legs = {}
+    # single-node config: M=1 K=N=1024 block 32 with zero points
+    p1 = synth.mmnb_problem(1, 1024, 1024, 32, True, seed=0)
+    lo, mean, cnt = _time_cpu(lambda: refcpu.matmul_nbits(p1.a, p1.b_q, p1.scales,
+                                                          p1.zero_points, 1024, 1024, 4, 32),
+                              0.1 * budget_s)
+    legs["single_node_m1_k1024_n1024_bs32_zp"] = {
+        "value": mmnb_bytes(1, 1024, 1024, 32, True) / mean / 1e9, "unit": "GB/s", "cores": 1,
+        "min_ms": lo * 1e3, "mean_ms": mean * 1e3, "calls": cnt}
+    # prefill GEMM: M=512 K=N=4096 block 32 with zero points
+    pg = synth.mmnb_problem(512, 4096, 4096, 32, True, seed=2, outlier_frac=0.01)
+    lo, mean, cnt = _time_cpu(lambda: refcpu.matmul_nbits(pg.a, pg.b_q, pg.scales,
+                                                          pg.zero_points, 4096, 4096, 4, 32,
+                                                          threads=threads),
+                              0.2 * budget_s, min_iters=1)
+    flops = 2.0 * 512 * 4096 * 4096
+    rows = np.arange(16)
+    lo1, mean1, cnt1 = _time_cpu(lambda: refcpu.matmul_nbits(pg.a[rows], pg.b_q, pg.scales,
+                                                             pg.zero_points, 4096, 4096, 4, 32),
+                                 0.1 * budget_s, min_iters=1)
+    legs["prefill_m512_k4096_n4096_bs32_zp"] = {
+        "value": flops / mean / 1e12, "unit": "TFLOP/s", "cores": threads,
+        "min_ms": lo * 1e3, "mean_ms": mean * 1e3, "calls": cnt,
+        "one_thread_16_rows": {"value": 2.0 * 16 * 4096 * 4096 / mean1 / 1e12,
+                               "unit": "TFLOP/s", "cores": 1, "min_ms": lo1 * 1e3,
+                               "mean_ms": mean1 * 1e3, "calls": cnt1}}
+    # int8 chain: DQL [512,1024] -> MatMulInteger [1024,3072] -> fp32 rescale
+    x, b = synth.int8_chain_problem(512, 1024, 3072)
+    bscale = np.array([0.01], np.float32)
+
+    def chain():
+        y, sc, zp = refcpu.dynamic_quantize_linear(x)
+        acc = refcpu.matmul_integer(y, b, zp, 0)
+        return refcpu.rescale(acc, sc, bscale)
+
+    lo, mean, cnt = _time_cpu(chain, 0.25 * budget_s, min_iters=1)
+    legs["int8_chain_m512_k1024_n3072"] = {
+        "value": 2.0 * 512 * 1024 * 3072 / mean / 1e12, "unit": "TOP/s", "cores": 1,
+        "min_ms": lo * 1e3, "mean_ms": mean * 1e3, "calls": cnt}
+    out["legs"] = legs
+    return out
 
 
 def profile_pass(ctx, lib, ops, synth, kind):
@@ -541,10 +591,12 @@ def profile_pass(ctx, lib, ops, synth, kind):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2160)
-    ap.add_argument("--warmup", type=int, default=216)
+    ap.add_argument("--steps", type=int, default=20,
+                    help="timed steps (one step = one call on each rotated weight pack)")
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="headline only, no extras")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-budget", type=float, default=16.0,
+                    help="seconds of host time for the CPU baseline legs")
     ap.add_argument("--profile", action="store_true",
                     help="counter pass for rocprofv3 (prints no JSON): the kernel chosen by "
                          "--profile-kind, then a 64 MiB device-to-device copy (10 calls) as "
@@ -572,33 +624,36 @@ def main():
 
     head = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 128, False, args.steps,
                       args.warmup)
-    print(f"# headline GEMV: {head['gbs']:.0f} GB/s whole-job, kernel "
-          f"{head['kernel_gbs']:.0f} GB/s ({head['kernel_ms'] * 1e3:.2f} us)",
-          file=sys.stderr, flush=True)
+    print(f"# headline GEMV: {head['gbs']:.0f} GB/s, {head['ms_per_call'] * 1e3:.2f} us per "
+          f"call ({head['packs']} calls per step), dispatch event "
+          f"{head['dispatch_event_us']:.2f} us", file=sys.stderr, flush=True)
     out = {
         "metric": "int4 MatMulNBits GB/s (M=1) & TFLOPS (M=512), % of HBM/MFMA roofline",
         "value": round(head["gbs"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": head["steps"],
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["ms_per_call"],
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 weights (u4 packed), fp32 activations/accumulate",
-        "data": "synthetic (seeded), weights rotated over >300 MB",
-        "config": {"workload": "MatMulNBits decode GEMV M=1 K=4096 N=4096 block 128 "
-                               "symmetric (one call per step)",
+        "dtype": "u4 weights, f32 activations and accumulation",
+        "data": "synthetic (seeded): random nibbles and scales, A ~ N(0,1)",
+        "config": {"workload": f"MatMulNBits decode GEMV M=1 K=4096 N=4096 block 128, "
+                               f"symmetric; one step = one call on each of {head['packs']} "
+                               f"distinct weight packs (> 300 MB, streamed from HBM)",
                    "m": 1, "k": 4096, "n": 4096, "block_size": 128, "zero_points": False,
-                   "packs_rotated": head["packs"], "bytes_per_step": head["bytes_per_call"],
-                   "parallelism": "single GPU"},
+                   "calls_per_step": head["packs"], "bytes_per_call": head["bytes_per_call"],
+                   "bytes_per_step": head["bytes_per_step"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("gemv_m1_k4096_n4096_bs128"),
                      "kernel": head["kernel"],
-                     "kernel_avg_us": round(head["kernel_ms"] * 1e3, 3)},
+                     "kernel_avg_us": round(head["ms_per_call"] * 1e3, 3),
+                     "launches_timed": head["calls"],
+                     "dispatch_event_us": round(head["dispatch_event_us"], 3)},
     }
     if not args.quick:
         try:
@@ -607,7 +662,7 @@ def main():
             print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['kernel_gbs']:.0f} GB/s kernel",
                   file=sys.stderr, flush=True)
             out["gemv_large"] = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128,
-                                           False, 60, 6, seed=4)
+                                           False, 20, 3, seed=4)
             print(f"# GEMV K=N=16384: {out['gemv_large']['kernel_gbs']:.0f} GB/s kernel",
                   file=sys.stderr, flush=True)
             out["gemm"] = bench_gemm(ctx, lib, ops, synth, 512, 4096, 4096, 32, True,
@@ -621,7 +676,7 @@ def main():
             sweep = []
             for m in (1, 4, 8):
                 for (k, n) in synth.DECODE_PROJECTIONS:
-                    r = bench_gemv(ctx, lib, ops, synth, m, k, n, 128, False, 1000, 100)
+                    r = bench_gemv(ctx, lib, ops, synth, m, k, n, 128, False, 10, 2)
                     sweep.append({kk: r[kk] for kk in ("m", "k", "n", "gbs", "kernel_gbs",
                                                        "kernel_ms", "bytes_per_call")})
             out["decode_sweep"] = sweep
@@ -637,8 +692,7 @@ def main():
             print(f"# platform: {out['platform']}", file=sys.stderr, flush=True)
         except Exception as e:  # extras must not hide the headline
             out["extras_error"] = repr(e)
-    out["cpu_baseline"] = cpu_baseline(synth, 1, 4096, 4096, 128, False,
-                                       args.cpu_budget if not args.quick else 3.0)
+    out["cpu_baseline"] = cpu_baseline(synth, args.cpu_budget if not args.quick else 6.0)
     print(json.dumps(out), flush=True)
 
 

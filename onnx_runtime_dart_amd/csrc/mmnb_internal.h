@@ -255,6 +255,11 @@ int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
 int gemm_prepared_a(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, int64_t *segsp,
                     int64_t *mpad, void **d_ap, int **d_exp);
 int launch_matmul_nbits_prepared(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, float *d_y);
+// MatMulNBits (plain packs) with all scratch carved from ws (ws_bytes,
+// 256-byte aligned); MMNB_ERR_UNSUPPORTED if the call needs more.  Calls no
+// allocator.
+int launch_matmul_nbits_ws(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
+                           int64_t m, float *d_y, void *ws, size_t ws_bytes);
 
 // DynamicQuantizeLinear on device.
 int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y,

@@ -157,93 +157,83 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) 
 }
 
 // ---------------------------------------------------------------------------
-// Decode-shape GEMV on the vector ALUs (fp32 FMA), M <= 8.
+// Decode-shape GEMV on the vector ALUs (fp32 FMA), M = 1.
 //
 // A column's K extent is cut into 16-byte chunks (32 nibbles); chunk c =
 // (segment s = c/2, half g = c%2) holds k = 64s + 16j + 8g + e for dword
 // j = 0..3, nibble e = 0..7.  A workgroup owns 2R columns and all of K:
 //   wave w, lane l: half h = l/32 picks one column of each pair, t = l%32;
-//   the lane owns chunk c = 32w + t (+ 32W per extra iteration) of the R
+//   the lane owns chunk c = 32w + t (+ 32 nw per extra iteration) of the R
 //   columns 2r + h, r = 0..R-1.
-// Every lane issues all of its R weight loads (16 B each), their scales and
-// zero points, and its 32 activations before doing any arithmetic, so a
-// workgroup has its whole share of the weight stream in flight at once.  The
-// activations of a chunk are loaded once and reused for R columns.  Each
-// nibble becomes the exact (q - zp), scaled by a power of two (dq_nibbles),
-// before the fp32 FMAs: acc += scale * sum a * (q - zp), as the reference's
-// per-weight (q - zp) * scale (a block whose nibbles all equal the zero
-// point adds exactly zero).
-// The 32 lanes of a column half-wave reduce with DPP/swizzle, the waves
-// through LDS.
+// Up to 4 waves split K (one pass covers K <= 4096; longer K iterates:
+// 16-wave workgroups covering K = 16384 in one pass measured 20% slower).
+// Per iteration a lane issues all of its loads -- its 32 activations, the scales (and zero
+// points), then the R weight chunks in column order -- before any
+// arithmetic, pinned there by a scheduling barrier: left to itself the
+// compiler sinks loads next to their first use, which splits them into
+// several dependent round trips.  Column r's arithmetic then waits only for
+// loads up to its own chunk.  The activations of a chunk are reused for R
+// columns.  Each nibble becomes the exact (q - zp), scaled by a power of two
+// (dq_nibbles), before the fp32 FMAs: acc += scale * sum a * (q - zp), as
+// the reference's per-weight (q - zp) * scale (a block whose nibbles all
+// equal the zero point adds exactly zero).  The 32 lanes of a column
+// half-wave reduce with DPP/swizzle, the waves through LDS.
 // ---------------------------------------------------------------------------
 
-constexpr int kGemvMaxWaves = 4;
+constexpr int kGemvMaxWaves = 4;   // M = 1 GEMV
+constexpr int kDecMaxWaves = 4;    // decoder-step GEMV (K <= 4096)
 
-template <int M, int R, int NBPC, bool HAS_ZP>
+template <int R, int NBPC, bool HAS_ZP, bool FAST>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
-    const float *__restrict__ A, int64_t lda, const uint8_t *__restrict__ W,
-    int64_t col_bytes, const float *__restrict__ S, const uint8_t *__restrict__ Z, int nb,
-    int bs_log2, int K, int N, float *__restrict__ Y, int C, int iters, int fast) {
-  __shared__ float red[kGemvMaxWaves][M][2 * R];
+    const float *__restrict__ A, const uint8_t *__restrict__ W, int64_t col_bytes,
+    const float *__restrict__ S, const uint8_t *__restrict__ Z, int nb, int bs_log2, int K,
+    int N, float *__restrict__ Y, int C, int iters) {
+  __shared__ float red[kGemvMaxWaves][2 * R];
   const int nw = blockDim.x >> 6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int h = l >> 5, t = l & 31;
   const int col0 = blockIdx.x * (2 * R);
 
   int colr[R];
-  bool colok[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int c = col0 + 2 * r + h;
-    colok[r] = c < N;
-    colr[r] = colok[r] ? c : N - 1;
+    colr[r] = c < N ? c : N - 1;
   }
-  float acc[M][R];
+  float acc[R];
 #pragma unroll
-  for (int m = 0; m < M; m++)
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
+  for (int r = 0; r < R; r++) acc[r] = 0.0f;
 
   for (int it = 0; it < iters; it++) {
     const int c = 32 * w + t + it * 32 * nw;
     const bool cv = c < C;
     const int cc = cv ? c : 0;
     const int s = cc >> 1, g = cc & 1;
-    // ---- issue every load of this chunk.  M = 1: activations first (L2
-    // hits, used by every column), then scales / zero points, then the weights
-    // in column order, so column 0's arithmetic starts while later columns'
-    // weights are in flight.  M > 1: weights first (the activation registers
-    // grow with M; issuing them last keeps the weight stream ahead).
-    float av[M][32];
-    uint4 wv[R];
-    if constexpr (M > 1) {
-#pragma unroll
-      for (int r = 0; r < R; r++)
-        wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
-    }
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-      const float *ar = A + (int64_t)m * lda + s * kSegK + 8 * g;
+    // ---- every load of this iteration.  A lane past the last chunk reads
+    // chunk 0 (cc) with zero scales, so it adds exactly nothing.
+    float av[32];
+    const float *ar = A + s * kSegK + 8 * g;
+    if constexpr (FAST) {
+      // rows hold k64 values: every 8-float run of a chunk is inside the row
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        if (fast) {
-          // unconditional: a lane past the last chunk reads chunk 0 (cc) and
-          // its scales are zero, so it adds exactly nothing
-          const float4 x0 = *(const float4 *)(ar + 16 * j);
-          const float4 x1 = *(const float4 *)(ar + 16 * j + 4);
-          av[m][8 * j + 0] = x0.x; av[m][8 * j + 1] = x0.y;
-          av[m][8 * j + 2] = x0.z; av[m][8 * j + 3] = x0.w;
-          av[m][8 * j + 4] = x1.x; av[m][8 * j + 5] = x1.y;
-          av[m][8 * j + 6] = x1.z; av[m][8 * j + 7] = x1.w;
-        } else {
-          const int k0 = s * kSegK + 8 * g + 16 * j;
+        const float4 x0 = *(const float4 *)(ar + 16 * j);
+        const float4 x1 = *(const float4 *)(ar + 16 * j + 4);
+        av[8 * j + 0] = x0.x; av[8 * j + 1] = x0.y; av[8 * j + 2] = x0.z; av[8 * j + 3] = x0.w;
+        av[8 * j + 4] = x1.x; av[8 * j + 5] = x1.y; av[8 * j + 6] = x1.z; av[8 * j + 7] = x1.w;
+      }
+    } else {
 #pragma unroll
-          for (int e = 0; e < 8; e++) av[m][8 * j + e] = (cv && k0 + e < K) ? ar[16 * j + e] : 0.0f;
+      for (int j = 0; j < 4; j++) {
+        const int k0 = s * kSegK + 8 * g + 16 * j;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int k = k0 + e < K ? k0 + e : K - 1;
+          const float x = A[k];
+          av[8 * j + e] = (cv && k0 + e < K) ? x : 0.0f;
         }
       }
     }
-    // raw scale / zero-point loads (no arithmetic on loaded values here, so
-    // the loads stay in flight together)
     float sraw[R][NBPC];
     uint32_t zraw[R][NBPC];
     bool inbq[NBPC];
@@ -263,91 +253,70 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
         zsh[r][q] = (zi & 1) * 4;
       }
     }
-    if constexpr (M == 1) {
+    uint4 wv[R];
 #pragma unroll
-      for (int r = 0; r < R; r++)
-        wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
-    }
+    for (int r = 0; r < R; r++)
+      wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+    __builtin_amdgcn_sched_barrier(0);
     // ---- arithmetic: exact (q - zp) per weight, scaled by dq_unscale
-    float sc[R][NBPC];
-    uint32_t zc[R][NBPC];
-#pragma unroll
-    for (int q = 0; q < NBPC; q++)
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        sc[r][q] = inbq[q] ? sraw[r][q] : 0.0f;
-        zc[r][q] = HAS_ZP ? dq8_const((int)((zraw[r][q] >> zsh[r][q]) & 0xF)) : 0u;
-      }
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const uint32_t wd[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
 #pragma unroll
       for (int q = 0; q < NBPC; q++) {
-        float d[M];
-#pragma unroll
-        for (int m = 0; m < M; m++) d[m] = 0.0f;
+        const uint32_t zc =
+            HAS_ZP ? dq8_const((int)((zraw[r][q] >> zsh[r][q]) & 0xF)) : 0u;
+        float d = 0.0f;
 #pragma unroll
         for (int jj = 0; jj < 4 / NBPC; jj++) {
           const int j = q * (4 / NBPC) + jj;
           float qv[8];
-          dq_nibbles<HAS_ZP>(wd[j], zc[r][q], qv);
+          dq_nibbles<HAS_ZP>(wd[j], zc, qv);
 #pragma unroll
-          for (int m = 0; m < M; m++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) d[m] = fmaf(av[m][8 * j + e], qv[e], d[m]);
+          for (int e = 0; e < 8; e++) d = fmaf(av[8 * j + e], qv[e], d);
         }
-#pragma unroll
-        for (int m = 0; m < M; m++) acc[m][r] = fmaf(sc[r][q], d[m], acc[m][r]);
+        acc[r] = fmaf(inbq[q] ? sraw[r][q] : 0.0f, d, acc[r]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
   // ---- reductions: 32 lanes of a half-wave, then the waves
 #pragma unroll
-  for (int m = 0; m < M; m++)
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const float v = half_wave_sum(acc[m][r]);
-      if (t == 0) red[w][m][2 * r + h] = v;
-    }
+  for (int r = 0; r < R; r++) {
+    const float v = half_wave_sum(acc[r]);
+    if (t == 0) red[w][2 * r + h] = v;
+  }
   __syncthreads();
-  for (int i = threadIdx.x; i < M * 2 * R; i += blockDim.x) {
-    const int m = i / (2 * R), cl = i % (2 * R);
+  if ((int)threadIdx.x < 2 * R) {
     float v = 0.0f;
-    for (int ww = 0; ww < nw; ww++) v += red[ww][m][cl];
-    const int col = col0 + cl;
-    if (col < N) Y[(int64_t)m * N + col] = v * dq_unscale<HAS_ZP>();
+    for (int ww = 0; ww < nw; ww++) v += red[ww][threadIdx.x];
+    const int col = col0 + threadIdx.x;
+    if (col < N) Y[col] = v * dq_unscale<HAS_ZP>();
   }
 }
 
-template <int M, int R>
-static int launch_gemv_mr(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const float *A,
-                          int64_t lda, const mmnb_pack *p, float *Y, int C, int iters,
-                          int fast, int bs_log2) {
+template <int R>
+static int launch_gemv_r(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const float *A,
+                         const mmnb_pack *p, float *Y, int C, int iters, bool fast,
+                         int bs_log2) {
   const int nb = (int)p->n_blocks, K = (int)p->k, N = (int)p->n;
-#define MMNB_GEMV_LAUNCH(Q)                                                                  \
-  return p->has_zp                                                                         \
-             ? launch(ctx, kKernGemv, k_gemv_valu<M, R, Q, true>, grid, block, 0, A, lda,    \
-                      p->d_w, p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C,  \
-                      iters, fast)                                                          \
-             : launch(ctx, kKernGemv, k_gemv_valu<M, R, Q, false>, grid, block, 0, A, lda,   \
-                      p->d_w, p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C,  \
-                      iters, fast)
-  if (nbpc == 4) MMNB_GEMV_LAUNCH(4);
-  if (nbpc == 2) MMNB_GEMV_LAUNCH(2);
-  MMNB_GEMV_LAUNCH(1);
+#define MMNB_GEMV_LAUNCH(Q, ZP, F)                                                           \
+  return launch(ctx, kKernGemv, k_gemv_valu<R, Q, ZP, F>, grid, block, 0, A, p->d_w,         \
+                p->col_bytes, p->d_scales, p->d_zp, nb, bs_log2, K, N, Y, C, iters)
+#define MMNB_GEMV_LAUNCH_Q(ZP, F)             \
+  {                                          \
+    if (nbpc == 4) MMNB_GEMV_LAUNCH(4, ZP, F); \
+    if (nbpc == 2) MMNB_GEMV_LAUNCH(2, ZP, F); \
+    MMNB_GEMV_LAUNCH(1, ZP, F);                \
+  }
+  if (p->has_zp) {
+    if (fast) MMNB_GEMV_LAUNCH_Q(true, true);
+    MMNB_GEMV_LAUNCH_Q(true, false);
+  }
+  if (fast) MMNB_GEMV_LAUNCH_Q(false, true);
+  MMNB_GEMV_LAUNCH_Q(false, false);
+#undef MMNB_GEMV_LAUNCH_Q
 #undef MMNB_GEMV_LAUNCH
-}
-
-template <int M>
-static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
-                         const float *A, int64_t lda, const mmnb_pack *p, float *Y, int C,
-                         int iters, int fast, int bs_log2) {
-  if (M <= 2 && R == 8)
-    return launch_gemv_mr<M, (M <= 2 ? 8 : 1)>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
-  if (M <= 4 && R == 4)
-    return launch_gemv_mr<M, (M <= 4 ? 4 : 1)>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
-  if (R == 2) return launch_gemv_mr<M, 2>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
-  return launch_gemv_mr<M, 1>(ctx, nbpc, grid, block, A, lda, p, Y, C, iters, fast, bs_log2);
 }
 
 // ---------------------------------------------------------------------------
@@ -369,13 +338,13 @@ static int launch_gemv_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 block,
 // ---------------------------------------------------------------------------
 
 template <int R, bool NORM, int EPI>
-__global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
+__global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
     const float *__restrict__ X, const float *__restrict__ gamma, float eps,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S, int nb,
     int bs_log2, int K, int N, const float *resid, float *Y,
     unsigned long long *__restrict__ argmax, int C) {
-  __shared__ float red[kGemvMaxWaves][2 * R];
-  __shared__ float nrm[kGemvMaxWaves];
+  __shared__ float red[kDecMaxWaves][2 * R];
+  __shared__ float nrm[kDecMaxWaves];
   __shared__ float outv[2 * R];
   const int nw = blockDim.x >> 6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -421,6 +390,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_dec_gemv(
 #pragma unroll
   for (int r = 0; r < R; r++)
     wv[r] = *(const uint4 *)(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
+  // every load above is in flight before any arithmetic (see k_gemv_valu)
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (NORM) {
     float ss = 0.0f;
     if (h == 0 && cv) {
@@ -796,20 +767,35 @@ static int launch_gemv_lds_m(mmnb_ctx *ctx, int R, int nbpc, dim3 grid, dim3 blo
 static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y);
 
-// 2 <= M <= 8: the LDS-staged kernel, or the MFMA GEMM when A does not fit
-// the workgroup's LDS.
-static int launch_gemv_multi(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
-                             int64_t lda, int64_t m, float *d_y) {
+// Waves splitting K (kw), chunk iterations and staged-activation LDS bytes
+// of the multi-row GEMV for M rows.
+static size_t gemv_multi_lds(const mmnb_pack *p, int64_t m, int *kw_out, int *iters_out) {
   const int C = (int)(p->col_bytes / 16);
   int kw = (C + 31) / 32, iters = 1;
   if (kw > 4) {
     iters = (kw + 3) / 4;
     kw = (C + 32 * iters - 1) / (32 * iters);
   }
+  if (kw_out) *kw_out = kw;
+  if (iters_out) *iters_out = iters;
   const int cs = 32 * kw * iters;
-  const size_t shmem = (size_t)m * 8 * (cs + 1) * 16;
-  // the kernel also holds a static 8 x M x 8 float reduction buffer
-  if (shmem + 8 * 8 * 8 * 4 > (size_t)ctx->lds_max) return launch_gemm(ctx, p, d_a, lda, m, d_y);
+  return (size_t)m * 8 * (cs + 1) * 16;
+}
+
+// Whether 2 <= M <= 8 rows of A fit the multi-row GEMV's LDS (the kernel
+// also holds a static 8 x M x 8 float reduction buffer).
+static bool gemv_multi_fits(const mmnb_ctx *ctx, const mmnb_pack *p, int64_t m) {
+  return gemv_multi_lds(p, m, nullptr, nullptr) + 8 * 8 * 8 * 4 <= (size_t)ctx->lds_max;
+}
+
+// 2 <= M <= 8: the LDS-staged kernel, or the MFMA GEMM when A does not fit
+// the workgroup's LDS.
+static int launch_gemv_multi(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a,
+                             int64_t lda, int64_t m, float *d_y) {
+  const int C = (int)(p->col_bytes / 16);
+  int kw, iters;
+  const size_t shmem = gemv_multi_lds(p, m, &kw, &iters);
+  if (!gemv_multi_fits(ctx, p, m)) return launch_gemm(ctx, p, d_a, lda, m, d_y);
   const int64_t n = p->n;
   // Every workgroup stages all of A, so fewer, wider workgroups win: up to
   // 8 waves (cg column groups of kw waves), then the most columns per lane
@@ -847,7 +833,7 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
                        int64_t m, float *d_y) {
   if (m > 1) return launch_gemv_multi(ctx, p, d_a, lda, m, d_y);
   const int C = (int)(p->col_bytes / 16);  // chunks per column
-  // waves splitting K: one chunk per lane up to 16 waves, then iterate
+  // waves splitting K: one chunk per lane up to 4 waves, then iterate
   int nw = (C + 31) / 32;
   int iters = 1;
   if (nw > kGemvMaxWaves) {
@@ -864,10 +850,13 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   // Aligned float4 path: every 8-float run of a chunk lies inside the row,
   // i.e. rows hold k64 values (zero padded past K by the host entry point, or
   // K itself is a multiple of 64).
-  const int f = ((lda % 4 == 0) && (((uintptr_t)d_a & 15) == 0) && (lda >= p->k64)) ? 1 : 0;
+  const bool f = (lda % 4 == 0) && (((uintptr_t)d_a & 15) == 0) && (lda >= p->k64);
   const int bs_log2 = ilog2(p->block);
   const int nbpc = p->block >= 64 ? 1 : (p->block == 32 ? 2 : 4);
-  return launch_gemv_m<1>(ctx, R, nbpc, grid, block, d_a, lda, p, d_y, C, iters, f, bs_log2);
+  if (R == 8) return launch_gemv_r<8>(ctx, nbpc, grid, block, d_a, p, d_y, C, iters, f, bs_log2);
+  if (R == 4) return launch_gemv_r<4>(ctx, nbpc, grid, block, d_a, p, d_y, C, iters, f, bs_log2);
+  if (R == 2) return launch_gemv_r<2>(ctx, nbpc, grid, block, d_a, p, d_y, C, iters, f, bs_log2);
+  return launch_gemv_r<1>(ctx, nbpc, grid, block, d_a, p, d_y, C, iters, f, bs_log2);
 }
 
 // ---------------------------------------------------------------------------
@@ -896,7 +885,12 @@ constexpr int kPrepRows = 2;
 __global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int64_t lda,
                                                 int64_t M, int64_t K, int64_t segsp,
                                                 int *__restrict__ row_exp,
-                                                uint4 *__restrict__ out) {
+                                                uint4 *__restrict__ out,
+                                                int *__restrict__ clear, int nclear) {
+  // the GEMM's K-slice counters when they live in a caller's workspace:
+  // zeroed here, before the GEMM (the next launch on the stream) counts in
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < nclear; i += blockDim.x) clear[i] = 0;
   __shared__ float wmax[kPrepRows][4];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t r0 = (int64_t)blockIdx.x * kPrepRows;
@@ -1543,17 +1537,19 @@ static int gemm_plan(const mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, GemmPla
 }
 
 // The GEMM proper on a prepared A (d_ap, d_exp laid out for `pl`).
+// K-slice partial tiles of a plan (bytes; 0 without K slices).
+static size_t gemm_part_bytes(const GemmPlan &pl) {
+  return pl.ksplit > 1 ? (size_t)pl.tiles * pl.ksplit * 32 * pl.cb * 256 * 4 : 0;
+}
+
+// d_part: the K-slice partial tiles (gemm_part_bytes), d_cnt: the per-tile
+// arrival counters (zero at rest); both unused without K slices.
 static int gemm_run(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, const GemmPlan &pl,
-                    const void *d_ap, const void *d_exp, float *d_y) {
-  const int64_t segs = pl.segs, segsp = pl.segsp, tiles = pl.tiles;
+                    const void *d_ap, const void *d_exp, float *d_y, void *d_part, int *d_cnt) {
+  const int64_t segs = pl.segs, segsp = pl.segsp;
   const int gx = pl.gx, gy = pl.gy, cb = pl.cb, nbps = pl.nbps, groups = pl.groups,
             nst = pl.nst, ksplit = pl.ksplit;
   const size_t shmem = pl.shmem;
-  void *d_part = nullptr;
-  int rc;
-  if (ksplit > 1 &&
-      (rc = scratch_get(ctx, 10, (size_t)tiles * ksplit * 32 * cb * 256 * 4, &d_part)))
-    return rc;
   const int bs_log2 = ilog2(p->block);
   const dim3 grid((unsigned)(gx * gy * ksplit));
 #define MMNB_GEMM_LAUNCH(Q, NS, GR, CB)                                                      \
@@ -1567,7 +1563,7 @@ static int gemm_run(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, const GemmPlan
     return launch(ctx, kKernGemm, kern, grid, dim3(256 * GR), shmem, (const uint4 *)d_ap,   \
                   (const int *)d_exp, (int)segs, (int)segsp, p->d_w, p->col_bytes,          \
                   p->d_st, p->d_zt, (int)p->ldsz, (int)p->n_blocks, bs_log2, (int)m,        \
-                  (int)p->n, gx, gy, d_y, ksplit, (float *)d_part, ctx->d_gemm_cnt);        \
+                  (int)p->n, gx, gy, d_y, ksplit, (float *)d_part, d_cnt);                  \
   }
 #define MMNB_GEMM_NB(NS, GR, CB)                     \
   {                                                  \
@@ -1590,18 +1586,27 @@ static int gemm_run(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, const GemmPlan
 }
 
 
+// The context's K-slice partials (grow-only scratch) for a plan.
+static int gemm_ctx_part(mmnb_ctx *ctx, const GemmPlan &pl, void **d_part) {
+  *d_part = nullptr;
+  const size_t pb = gemm_part_bytes(pl);
+  return pb ? scratch_get(ctx, 10, pb, d_part) : MMNB_OK;
+}
+
 static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                        int64_t m, float *d_y) {
   GemmPlan pl;
   int rc;
   if ((rc = gemm_plan(ctx, p, m, pl))) return rc;
-  void *d_ap = nullptr, *d_exp = nullptr;
+  void *d_ap = nullptr, *d_exp = nullptr, *d_part = nullptr;
   if ((rc = scratch_get(ctx, 2, pl.ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)pl.mpad * 4, &d_exp))) return rc;
+  if ((rc = gemm_ctx_part(ctx, pl, &d_part))) return rc;
   if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(pl.mpad / kPrepRows)), dim3(256), 0,
-                    d_a, lda, m, p->k, pl.segsp, (int *)d_exp, (uint4 *)d_ap)))
+                    d_a, lda, m, p->k, pl.segsp, (int *)d_exp, (uint4 *)d_ap, (int *)nullptr,
+                    0)))
     return rc;
-  return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y);
+  return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y, d_part, ctx->d_gemm_cnt);
 }
 
 int gemm_prepared_a(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, int64_t *segsp,
@@ -1621,10 +1626,46 @@ int launch_matmul_nbits_prepared(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, f
   GemmPlan pl;
   int rc;
   if ((rc = gemm_plan(ctx, p, m, pl))) return rc;
-  void *d_ap = nullptr, *d_exp = nullptr;
+  void *d_ap = nullptr, *d_exp = nullptr, *d_part = nullptr;
   if ((rc = scratch_get(ctx, 2, pl.ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)pl.mpad * 4, &d_exp))) return rc;
-  return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y);
+  if ((rc = gemm_ctx_part(ctx, pl, &d_part))) return rc;
+  return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y, d_part, ctx->d_gemm_cnt);
+}
+
+// MatMulNBits with every scratch buffer carved from a caller's workspace
+// (ws, ws_bytes; 256-byte aligned): the GEMM's K-slice counters, row
+// exponents, prepared activations and K-slice partials, each followed by
+// kTailPad bytes of slack.  Allocates nothing.
+int launch_matmul_nbits_ws(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
+                           int64_t m, float *d_y, void *ws, size_t ws_bytes) {
+  // the GEMVs use no scratch (the multi-row one falls back to the GEMM when A
+  // does not fit its LDS: that GEMM takes the workspace below)
+  if (m == 1 || (m <= 8 && gemv_multi_fits(ctx, p, m)))
+    return launch_gemv(ctx, p, d_a, lda, m, d_y);
+  GemmPlan pl;
+  int rc;
+  if ((rc = gemm_plan(ctx, p, m, pl))) return rc;
+  auto up = [](size_t b) { return (b + kTailPad + 255) / 256 * 256; };
+  const size_t o_cnt = 0;
+  const size_t o_exp = o_cnt + up((size_t)kGemmMaxSplitTiles * 4);
+  const size_t o_ap = o_exp + up((size_t)pl.mpad * 4);
+  const size_t o_part = o_ap + up(pl.ap_bytes);
+  const size_t need = o_part + up(gemm_part_bytes(pl));
+  if (need > ws_bytes)
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "MatMulNBits: this M x K needs " + std::to_string(need) +
+                    " bytes of scratch, more than the " + std::to_string(ws_bytes) +
+                    "-byte fixed workspace");
+  char *b = (char *)ws;
+  int *d_cnt = (int *)(b + o_cnt);
+  const int nclear = pl.ksplit > 1 ? (int)pl.tiles : 0;
+  if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(pl.mpad / kPrepRows)), dim3(256), 0,
+                    d_a, lda, m, p->k, pl.segsp, (int *)(b + o_exp), (uint4 *)(b + o_ap), d_cnt,
+                    nclear)))
+    return rc;
+  return gemm_run(ctx, p, m, pl, b + o_ap, b + o_exp, d_y,
+                  pl.ksplit > 1 ? (void *)(b + o_part) : nullptr, d_cnt);
 }
 
 int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
