@@ -108,6 +108,25 @@ int mmnb_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *pack, const float *a,
 int mmnb_matmul_nbits_dev(mmnb_ctx *ctx, const mmnb_pack *pack,
                           const float *d_a, int64_t m, float *d_y);
 
+/* Allocation-free form of mmnb_matmul_nbits_dev.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture that has not run the call before, serving loops
+ * and harnesses that forbid hipMalloc).  Same kernels and result bits as
+ * mmnb_matmul_nbits_dev for packs from mmnb_pack_nbits; the prefill GEMM's
+ * scratch (prepared activations, row exponents, K-slice partials and
+ * counters) comes from a fixed device array of
+ * mmnb_noalloc_workspace_bytes() bytes per GPU (64 MiB, held from library
+ * load until the process ends) instead of the context's grow-only buffers.
+ * Calls whose scratch would exceed it return MMNB_ERR_UNSUPPORTED (M x K up
+ * to 2048 x 4096 fits); packs from mmnb_pack_nbits_ex with g_idx, bias,
+ * bits 8 or float zero points return MMNB_ERR_UNSUPPORTED.  All calls on one
+ * GPU share the array: calls that overlap on one GPU (two streams or two
+ * contexts at once) race. */
+int mmnb_matmul_nbits_dev_noalloc(mmnb_ctx *ctx, const mmnb_pack *pack,
+                                  const float *d_a, int64_t m, float *d_y);
+/* Bytes of the fixed workspace behind mmnb_matmul_nbits_dev_noalloc. */
+int64_t mmnb_noalloc_workspace_bytes(void);
+
 /* ---- MatMulNBits beyond the reference's 4-bit form -----------------------
  * The reference accepts bits = 4, uint8 zero points in its flat layout and
  * fp32 scales, and throws UnsupportedError for g_idx / bias inputs

@@ -34,6 +34,8 @@ SIGNATURES = {
                                _i64, _P(_vp)]),
     "mmnb_matmul_nbits": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mmnb_matmul_nbits_dev": (_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mmnb_matmul_nbits_dev_noalloc": (_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mmnb_noalloc_workspace_bytes": (_i64, []),
     "mmnb_dynamic_quantize_linear": (_int, [_vp, _vp, _i64, _vp, _P(ctypes.c_float),
                                             _P(_i64)]),
     "mmnb_dynamic_quantize_linear_dev": (_int, [_vp, _vp, _i64, _vp, _vp, _vp]),

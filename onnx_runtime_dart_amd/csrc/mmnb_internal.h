@@ -97,6 +97,9 @@ struct mmnb_ctx {
   int gemm_ksplit = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
+  // Device address of this device's fixed workspace for
+  // mmnb_matmul_nbits_dev_noalloc (set by noalloc_setup at init).
+  void *noalloc_ws = nullptr;
 };
 
 struct mmnb_pack {
@@ -260,6 +263,9 @@ int launch_matmul_nbits_prepared(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, f
 // allocator.
 int launch_matmul_nbits_ws(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                            int64_t m, float *d_y, void *ws, size_t ws_bytes);
+// Finds this device's fixed no-alloc workspace (once per context, with the
+// context's device current).
+int noalloc_setup(mmnb_ctx *ctx);
 
 // DynamicQuantizeLinear on device.
 int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y,

@@ -154,6 +154,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     delete ctx;
     return check_hip(e, "hipMalloc(pad page, GEMM counters)");
   }
+  if (int rc = noalloc_setup(ctx)) {
+    (void)mmnb_shutdown(ctx);  // no packs yet: releases everything above
+    return rc;
+  }
   *out = ctx;
   return MMNB_OK;
 }
