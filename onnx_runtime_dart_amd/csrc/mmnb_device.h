@@ -11,6 +11,14 @@ namespace mmnb {
 // bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// 16-byte global->LDS DMA of one lane (global_load_lds_dwordx4): lane l's
+// 16 bytes from g land at lds + 16 l (lds wave-uniform).  A plain function
+// so that template kernels can use it: the builtin written directly in a
+// template kernel's body makes the host pass drop that kernel's launch stub.
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
 // v + (v moved by the DPP control CTRL), every lane.
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {

@@ -27,7 +27,12 @@ namespace mmnb {
 // ---------------------------------------------------------------------------
 constexpr int kDqlThreads = 256;
 constexpr int kDqlMaxBlocks = 1024;
+constexpr int kDqlUnroll = 4;  // 16-byte loads a thread issues before using any
 
+// Per-block min/max partials.  Each thread issues kDqlUnroll float4 loads
+// (indices clamped into range: a repeated element changes neither extreme)
+// before comparing any, so a grid-stride pass is one round trip per
+// kDqlUnroll loads instead of one per load.
 __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restrict__ x,
                                                             int64_t n,
                                                             float2 *__restrict__ part) {
@@ -35,27 +40,31 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restr
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const bool vec = (((uintptr_t)x) & 15) == 0;
-  if (vec) {
+  int64_t done = 0;
+  if (vec && n >= 4) {
     const int64_t n4 = n >> 2;
     const float4 *x4 = (const float4 *)x;
-    for (int64_t i = tid; i < n4; i += stride) {
-      const float4 v = x4[i];
-      mn = v.x < mn ? v.x : mn; mx = v.x > mx ? v.x : mx;
-      mn = v.y < mn ? v.y : mn; mx = v.y > mx ? v.y : mx;
-      mn = v.z < mn ? v.z : mn; mx = v.z > mx ? v.z : mx;
-      mn = v.w < mn ? v.w : mn; mx = v.w > mx ? v.w : mx;
+    for (int64_t base = tid; base < n4; base += stride * kDqlUnroll) {
+      float4 v[kDqlUnroll];
+#pragma unroll
+      for (int u = 0; u < kDqlUnroll; u++) {
+        const int64_t i = base + u * stride;
+        v[u] = x4[i < n4 ? i : n4 - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < kDqlUnroll; u++) {
+        mn = v[u].x < mn ? v[u].x : mn; mx = v[u].x > mx ? v[u].x : mx;
+        mn = v[u].y < mn ? v[u].y : mn; mx = v[u].y > mx ? v[u].y : mx;
+        mn = v[u].z < mn ? v[u].z : mn; mx = v[u].z > mx ? v[u].z : mx;
+        mn = v[u].w < mn ? v[u].w : mn; mx = v[u].w > mx ? v[u].w : mx;
+      }
     }
-    for (int64_t i = (n4 << 2) + tid; i < n; i += stride) {
-      const float v = x[i];
-      mn = v < mn ? v : mn;
-      mx = v > mx ? v : mx;
-    }
-  } else {
-    for (int64_t i = tid; i < n; i += stride) {
-      const float v = x[i];
-      mn = v < mn ? v : mn;
-      mx = v > mx ? v : mx;
-    }
+    done = n4 << 2;
+  }
+  for (int64_t i = done + tid; i < n; i += stride) {
+    const float v = x[i];
+    mn = v < mn ? v : mn;
+    mx = v > mx ? v : mx;
   }
   for (int off = 32; off > 0; off >>= 1) {
     const float a = __shfl_xor(mn, off, 64), b = __shfl_xor(mx, off, 64);
@@ -131,16 +140,28 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)y) & 3) == 0);
   int64_t done = 0;
-  if (vec) {
+  if (vec && n >= 4) {
     const int64_t n4 = n >> 2;
     const float4 *x4 = (const float4 *)x;
     uint32_t *y4 = (uint32_t *)y;
-    for (int64_t i = tid; i < n4; i += stride) {
-      const float4 v = x4[i];
-      const uint32_t b = (uint32_t)dql_q(v.x, scale, zp) | ((uint32_t)dql_q(v.y, scale, zp) << 8) |
-                         ((uint32_t)dql_q(v.z, scale, zp) << 16) |
-                         ((uint32_t)dql_q(v.w, scale, zp) << 24);
-      y4[i] = b;
+    // kDqlUnroll loads in flight per thread (clamped indices; only the
+    // in-range results are stored)
+    for (int64_t base = tid; base < n4; base += stride * kDqlUnroll) {
+      float4 v[kDqlUnroll];
+#pragma unroll
+      for (int u = 0; u < kDqlUnroll; u++) {
+        const int64_t i = base + u * stride;
+        v[u] = x4[i < n4 ? i : n4 - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < kDqlUnroll; u++) {
+        const int64_t i = base + u * stride;
+        const uint32_t b = (uint32_t)dql_q(v[u].x, scale, zp) |
+                           ((uint32_t)dql_q(v[u].y, scale, zp) << 8) |
+                           ((uint32_t)dql_q(v[u].z, scale, zp) << 16) |
+                           ((uint32_t)dql_q(v[u].w, scale, zp) << 24);
+        if (i < n4) y4[i] = b;
+      }
     }
     done = n4 << 2;
   }
@@ -152,14 +173,15 @@ int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *
   void *d_part = nullptr;
   int rc;
   if ((rc = scratch_get(ctx, 3, sizeof(float2) * kDqlMaxBlocks, &d_part))) return rc;
-  // ~8 float4 per thread in pass 1
-  int64_t blocks = (n + (int64_t)kDqlThreads * 32 - 1) / ((int64_t)kDqlThreads * 32);
+  // one batch of kDqlUnroll float4 per thread when the grid allows
+  const int64_t per_block = (int64_t)kDqlThreads * kDqlUnroll * 4;
+  int64_t blocks = (n + per_block - 1) / per_block;
   if (blocks < 1) blocks = 1;
   if (blocks > kDqlMaxBlocks) blocks = kDqlMaxBlocks;
   if ((rc = launch(ctx, kKernDqlMinmax, k_dql_minmax, dim3((unsigned)blocks), dim3(kDqlThreads),
                     0, d_x, n, (float2 *)d_part)))
     return rc;
-  int64_t qblocks = (n + (int64_t)kDqlThreads * 16 - 1) / ((int64_t)kDqlThreads * 16);
+  int64_t qblocks = (n + per_block - 1) / per_block;
   if (qblocks < 1) qblocks = 1;
   if (qblocks > 4096) qblocks = 4096;
   return launch(ctx, kKernDqlQuant, k_dql_quant, dim3((unsigned)qblocks), dim3(kDqlThreads), 0,
@@ -181,28 +203,61 @@ int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *
 // padded) with its column sums; row sums of A' come from v_dot4 on the
 // operand registers.
 // ---------------------------------------------------------------------------
-__global__ void k_prep_int_b(const uint8_t *__restrict__ src, int b_signed, int b_trans,
-                             int64_t batch, int64_t k, int64_t n, int64_t kpad,
-                             int8_t *__restrict__ bt, int32_t *__restrict__ colsum) {
-  // one thread per (batch, column)
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= batch * n) return;
-  const int64_t b = idx / n, col = idx % n;
-  // element (b, kk, col) of B: [batch, k, n] or, transposed, [batch, n, k]
-  const uint8_t *s = b_trans ? src + (b * n + col) * k : src + b * k * n + col;
-  const int64_t ks = b_trans ? 1 : n;
-  int8_t *d = bt + (b * n + col) * kpad;
-  int32_t sum = 0;
-  for (int64_t kk = 0; kk < kpad; kk++) {
+// One 64 (k) x 64 (column) tile per workgroup: the source bytes are read
+// along whichever axis is contiguous (columns of a [batch, k, n] B, k of a
+// transposed [batch, n, k] convolution weight), turned through LDS, and
+// written k-contiguous per column as 16-byte stores; each column's partial
+// sum over the tile is added to colsum (zeroed beforehand; integer adds, so
+// the order does not matter).
+__global__ __launch_bounds__(256) void k_prep_int_b(const uint8_t *__restrict__ src,
+                                                    int b_signed, int b_trans, int64_t k,
+                                                    int64_t n, int64_t kpad,
+                                                    int8_t *__restrict__ bt,
+                                                    int32_t *__restrict__ colsum) {
+  __shared__ int8_t tile[64][64 + 4];  // [column][k]
+  const int64_t c0 = (int64_t)blockIdx.x * 64, k0 = (int64_t)blockIdx.y * 64;
+  const int64_t b = blockIdx.z;
+  const int t = threadIdx.x;
+  // load: thread t takes 16 consecutive elements along the contiguous axis
+  const int lo = (t & 3) * 16, hi = t >> 2;  // 16 along the fast axis, 1 along the slow
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    // (kk, col) of this element
+    const int64_t kk = b_trans ? k0 + lo + e : k0 + hi;
+    const int64_t col = b_trans ? c0 + hi : c0 + lo + e;
     int v = 0;
-    if (kk < k) {
-      const uint8_t raw = s[kk * ks];
+    if (kk < k && col < n) {
+      const uint8_t raw = b_trans ? src[(b * n + col) * k + kk] : src[(b * k + kk) * n + col];
       v = b_signed ? (int)(int8_t)raw : (int)raw - 128;
     }
-    d[kk] = (int8_t)v;
-    sum += v;
+    if (b_trans)
+      tile[hi][lo + e] = (int8_t)v;
+    else
+      tile[lo + e][hi] = (int8_t)v;
   }
-  colsum[idx] = sum;
+  __syncthreads();
+  // store: thread t writes k = k0 + lo .. +15 of column c0 + hi
+  const int64_t col = c0 + hi;
+  int sum = 0;
+  uint32_t w[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int8_t v = tile[hi][lo + 4 * d + e];
+      sum += v;
+      x |= (uint32_t)(uint8_t)v << (8 * e);
+    }
+    w[d] = x;
+  }
+  if (col < n) {
+    *(uint4 *)(bt + (b * n + col) * kpad + k0 + lo) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  // the four threads of a column: lanes 4j .. 4j+3
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  if ((t & 3) == 0 && col < n) atomicAdd(&colsum[b * n + col], sum);
 }
 
 // e = (uint8 ? 128 : 0) - b_zp for each of `cnt` columns (n, or batch*n
@@ -221,9 +276,10 @@ int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int b_t
                       int64_t batch, int64_t k, int64_t n, int64_t kpad, const int32_t *d_bzp,
                       int64_t bzp_len, int8_t *d_bt, int32_t *d_colsum, int32_t *d_ecol) {
   const int threads = 256;
-  const int64_t tot = batch * n;
-  int rc = launch(ctx, kKernPrepIntB, k_prep_int_b, dim3((unsigned)((tot + threads - 1) / threads)),
-                  dim3(threads), 0, d_src, b_signed, b_trans, batch, k, n, kpad, d_bt, d_colsum);
+  MMNB_HIP(hipMemsetAsync(d_colsum, 0, (size_t)(batch * n) * 4, ctx->stream));
+  int rc = launch(ctx, kKernPrepIntB, k_prep_int_b,
+                  dim3((unsigned)((n + 63) / 64), (unsigned)(kpad / 64), (unsigned)batch),
+                  dim3(threads), 0, d_src, b_signed, b_trans, k, n, kpad, d_bt, d_colsum);
   if (rc) return rc;
   const int64_t cnt = (bzp_len == batch * n && batch > 1) ? batch * n : n;
   return launch(ctx, kKernPrepIntB, k_prep_int_e, dim3((unsigned)((cnt + threads - 1) / threads)),
@@ -343,6 +399,81 @@ __device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[2][2], int (&rsu
   }
 }
 
+// Epilogue of the row-major int32 / fp32 outputs through LDS: the exact
+// zero-point corrections of mmi_epilogue, then the wave's 32 x 32 tile parked
+// in `tiles` (two 32 x 33 arrays: int32 and fp32; 8448 bytes per wave) and
+// stored back as 16 bytes per lane, 8 full 128-byte rows per instruction
+// (the MFMA layout would write 64-byte row pieces 16 columns wide).  The
+// caller's LDS must be free of other readers (a barrier after the K loop).
+__device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[2][2], int (&rsum)[2],
+                                                 const MmiEpiIn &ein, int a_signed, int64_t bz,
+                                                 int64_t M, int64_t K, int64_t N, int64_t m0,
+                                                 int64_t n0, int lane, int64_t azp_len,
+                                                 const MmiEpi &o, uint32_t *tiles) {
+  const int r16 = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    rsum[t] += __shfl_xor(rsum[t], 16, 64);
+    rsum[t] += __shfl_xor(rsum[t], 32, 64);
+  }
+  uint32_t *ti = tiles;                   // int32 tile [32][33]
+  float *tf = (float *)(tiles + 32 * 33);  // fp32 tile [32][33]
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    int32_t rs[4], cm[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      rs[r] = __shfl(rsum[i], q * 4 + r, 64);
+      const int32_t z = o.azp_is_const ? o.azp_const : (azp_len > 0 ? ein.z[i][r] : 0);
+      cm[r] = (a_signed ? 0 : 128) - z;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint32_t e = (uint32_t)ein.e[j], csum = (uint32_t)ein.cs[j];
+      const float sj = ein.as * ein.bs[j];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t c = (uint32_t)cm[r];
+        const uint32_t v = (uint32_t)acc[i][j][r] + e * (uint32_t)rs[r] + c * csum +
+                           (uint32_t)K * c * e;
+        const int at = (i * 16 + q * 4 + r) * 33 + j * 16 + r16;
+        ti[at] = v;
+        tf[at] = (float)(int32_t)v * sj;
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS writes, read back by its own lanes
+  // ---- stores: lane l -> row 8 pass + l/8, columns 4 (l % 8) .. +3
+  const int sc0 = (lane & 7) * 4;
+  const bool vec = n0 + 32 <= N && (N & 3) == 0 &&
+                   ((((uintptr_t)o.y) | ((uintptr_t)o.yf)) & 15) == 0;
+#pragma unroll
+  for (int pass = 0; pass < 4; pass++) {
+    const int rr = pass * 8 + (lane >> 3);
+    const int64_t row = m0 + rr;
+    uint32_t v[4];
+    float f[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      v[u] = ti[rr * 33 + sc0 + u];
+      f[u] = tf[rr * 33 + sc0 + u];
+    }
+    if (row >= M) continue;
+    const int64_t base = (bz * M + row) * N + n0 + sc0;
+    if (vec) {
+      if (o.y) *(uint4 *)(o.y + base) = make_uint4(v[0], v[1], v[2], v[3]);
+      if (o.yf) *(float4 *)(o.yf + base) = make_float4(f[0], f[1], f[2], f[3]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        if (n0 + sc0 + u >= N) continue;
+        if (o.y) o.y[base + u] = (int32_t)v[u];
+        if (o.yf) o.yf[base + u] = f[u];
+      }
+    }
+  }
+}
+
 // WG tile 64 x 64 (4 waves, 2 x 2), wave tile 32 x 32 = 2 x 2 MFMA tiles of
 // 16 x 16; K steps of 64.  Operand lanes: l%16 = row (A) / column (B),
 // l/16 = which 16-byte quarter of the 64-k step.
@@ -445,14 +576,18 @@ constexpr int kMmiPieces = kMmiKc / 16;                   // per row
 constexpr int kMmiSlotU4 = 64 * kMmiPieces;               // uint4 per operand per slot
 constexpr int kMmiLoads = 2 * (kMmiSlotU4 / 64) / 4;      // DMA loads per thread per chunk
 
+template <bool LDS_EPI>
 __global__ __launch_bounds__(256) void k_mmi_lds(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
     const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
     int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o,
     const uint8_t *__restrict__ pad) {
-  __shared__ uint4 sA[2][kMmiSlotU4];
-  __shared__ uint4 sB[2][kMmiSlotU4];
+  // one array: the A ring (slots 0-1) and the B ring (slots 2-3), which the
+  // LDS epilogue reuses whole
+  __shared__ uint4 smem[4][kMmiSlotU4];
+  uint4 (*sA)[kMmiSlotU4] = smem;
+  uint4 (*sB)[kMmiSlotU4] = smem + 2;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -485,8 +620,8 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
       const int8_t *gb = kk < kpad ? Bb + bcol * kpad + kk : (const int8_t *)pad;
       uint4 *da = &sA[s][i * 64];
       uint4 *db = &sB[s][i * 64];
-      __builtin_amdgcn_global_load_lds(ga, da, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(gb, db, 16, 0, 0);
+      dma16(ga, da);
+      dma16(gb, db);
     }
   };
 
@@ -537,8 +672,16 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
       issue(c + 2, s);
     }
   }
-  mmi_epilogue(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o);
+  if constexpr (LDS_EPI) {
+    __syncthreads();  // the ring is free: it holds the output tiles now
+    mmi_epilogue_lds(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o,
+                     (uint32_t *)&smem[0][0] + wave * 2 * 32 * 33);
+  } else {
+    mmi_epilogue(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o);
+  }
 }
+
+
 
 int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, int a_signed,
                           int64_t a_batch, int64_t m, const int32_t *d_azp, int64_t azp_len,
@@ -551,13 +694,15 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
   if (m <= 0 || n <= 0 || batch <= 0) return MMNB_OK;
   const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
-  if (fast && ctx->d_pad)
-    return launch(ctx, kKernMmi, k_mmi_lds, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
+  if (fast && ctx->d_pad) {
+    auto kern = (!o.yq && !o.trans) ? k_mmi_lds<true> : k_mmi_lds<false>;
+    return launch(ctx, kKernMmi, kern, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
                   a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                   p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad,
                   (const int32_t *)p->d_colsum, p->batch == 1 ? (int64_t)0 : n,
                   (const int32_t *)p->d_ecol, n, d_azp, azp_len, o,
                   (const uint8_t *)ctx->d_pad);
+  }
   return launch(ctx, kKernMmi, k_mmi_mfma, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
                 a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                 p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad, (const int32_t *)p->d_colsum,

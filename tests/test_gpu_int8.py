@@ -108,6 +108,11 @@ def test_mmi_int8_chain_shape(ctx):
     (np.uint8, np.int8, "row", "s", 2, 2, 16, 96, 40),
     (np.uint8, np.int8, "s", "s", None, None, 1, 1024, 3072),   # M = 1
     (np.uint8, np.int8, "s", "s", None, None, 130, 4096, 1),    # N = 1
+    # K % 16 == 0 up to 1024: all of K in one round trip; K steps not a
+    # multiple of 4 (A pieces padded to whole swizzle groups), M and N ragged
+    (np.uint8, np.int8, "row", "col", None, None, 100, 336, 200),
+    (np.uint8, np.uint8, "s", "col", None, None, 70, 1008, 96),
+    (np.int8, np.int8, None, "s", 2, None, 40, 720, 136),
 ])
 def test_mmi_brute_force(ctx, adt, bdt, az, bz, ab, bb, m, k, n):
     rng = np.random.default_rng(m * 31 + k + n)
