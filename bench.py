@@ -167,11 +167,35 @@ def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
     return res
 
 
+def _graph_us(ctx, fn, steps, warmup, per_graph=20):
+    """Per-call time of fn: a HIP graph of per_graph calls, warmup untimed
+    replays, then `steps` replays timed with events on the library stream."""
+    fn()
+    ctx.synchronize()
+    ctx.graph_begin()
+    for _ in range(per_graph):
+        fn()
+    g = ctx.graph_end()
+    for _ in range(warmup):
+        ctx.graph_launch(g)
+    ctx.synchronize()
+    ctx.event_record(0)
+    for _ in range(steps):
+        ctx.graph_launch(g)
+    ctx.event_record(1)
+    ctx.synchronize()
+    us = ctx.event_elapsed_ms(0, 1) * 1e3 / (steps * per_graph)
+    ctx.graph_destroy(g)
+    return us
+
+
 def bench_int8(ctx, lib, ops, synth, steps, warmup):
-    """The int8 chain twice: with the exact int32 accumulator also written
-    (the MatMulInteger node's own output kept) and fused (d_acc NULL: only
-    the fp32 result leaves the kernel, as in the graph where the int32 tensor
-    feeds Cast -> Mul alone)."""
+    """The int8 chain DQL [512,1024] -> MatMulInteger [1024,3072] -> rescale,
+    with the exact int32 accumulator also written (the MatMulInteger node's
+    own output kept) and fused (d_acc NULL: only the fp32 result leaves the
+    kernel, as in the graph where the int32 tensor feeds Cast -> Mul alone);
+    and its two ops alone (DQL; MatMulInteger with the int32 output, the
+    operator's own result).  Per-call times from graphs of 20 calls."""
     m, k, n = 512, 1024, 3072
     x, b = synth.int8_chain_problem(m, k, n)
     pack = ops.pack_integer(b, np.array(0, np.int8), ctx=ctx)
@@ -180,51 +204,34 @@ def bench_int8(ctx, lib, ops, synth, steps, warmup):
     daq, dsc, dzp = ctx.alloc(m * k), ctx.alloc(4), ctx.alloc(4)
     dacc, dy = ctx.alloc(m * n * 4), ctx.alloc(m * n * 4)
 
-    def run(acc_ptr):
-        def call():
-            lib.check(ctx.lib.mmnb_dynamic_matmul_dev(ctx.handle, pack.handle, dx.ptr, m,
-                                                      dbs.ptr, 1, daq.ptr, dsc.ptr, dzp.ptr,
-                                                      acc_ptr, dy.ptr))
-        for _ in range(warmup):
-            call()
-        ctx.synchronize()
-        ctx.graph_begin()
-        call()
-        g = ctx.graph_end()
-        ctx.synchronize()
-        ctx.event_record(0)
-        for _ in range(steps):
-            ctx.graph_launch(g)
-        ctx.event_record(1)
-        ctx.synchronize()
-        ms = ctx.event_elapsed_ms(0, 1) / steps
-        ctx.graph_destroy(g)
-        ctx.kernel_timing(True, max_launches=4 * min(steps, 1000))
-        for _ in range(min(steps, 1000)):
-            call()
-        kt = ctx.kernel_timing_read()
-        ctx.kernel_timing(False)
-        return ms, kt
+    def chain(acc_ptr):
+        lib.check(ctx.lib.mmnb_dynamic_matmul_dev(ctx.handle, pack.handle, dx.ptr, m, dbs.ptr, 1,
+                                                  daq.ptr, dsc.ptr, dzp.ptr, acc_ptr, dy.ptr))
 
-    ms, kt = run(dacc.ptr)
-    ms_fused, kt_fused = run(None)
-    mmi_bytes = m * k + k * n + 4 * m * n * 2  # A u8, B i8, int32 acc + fp32 y
-    mmi_bytes_fused = m * k + k * n + 4 * m * n  # A u8, B i8, fp32 y
+    def dql():
+        lib.check(ctx.lib.mmnb_dynamic_quantize_linear_dev(ctx.handle, dx.ptr, m * k, daq.ptr,
+                                                           dsc.ptr, dzp.ptr))
+
+    def mmi():
+        lib.check(ctx.lib.mmnb_matmul_integer_dev(ctx.handle, pack.handle, daq.ptr, 0, 1, m,
+                                                  dzp.ptr, 1, dacc.ptr))
+
+    chain_us = _graph_us(ctx, lambda: chain(dacc.ptr), steps, warmup)
+    fused_us = _graph_us(ctx, lambda: chain(None), steps, warmup)
+    dql_us = _graph_us(ctx, dql, steps, warmup)
+    mmi_us = _graph_us(ctx, mmi, steps, warmup)
+    mmi_bytes = m * k + k * n + 4 * m * n          # A u8, B i8, int32 out
     dql_bytes = 4 * m * k + m * k
-    mk = kernel_avg_ms(kt, "k_mmi_mfma")
-    mk_fused = kernel_avg_ms(kt_fused, "k_mmi_mfma")
-    res = {"m": m, "k": k, "n": n, "ms_per_chain": ms,
-           "kernels": {k_: {"count": v[0], "avg_us": v[1] / v[0] * 1e3}
-                       for k_, v in kt.items()},
-           "mmi_roofline": {"bound": "hbm", "achieved": mmi_bytes / (mk * 1e-3) / 1e9,
+    res = {"m": m, "k": k, "n": n, "ms_per_chain": chain_us * 1e-3,
+           "fused": {"ms_per_chain": fused_us * 1e-3},
+           "dql_us": dql_us, "dql_gbs": dql_bytes / (dql_us * 1e-6) / 1e9,
+           "mmi_us": mmi_us,
+           "mmi_roofline": {"bound": "hbm", "achieved": mmi_bytes / (mmi_us * 1e-6) / 1e9,
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": mmi_bytes / (mk * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                            "tops": 2.0 * m * k * n / (mk * 1e-3) / 1e12},
-           "fused": {"ms_per_chain": ms_fused, "mmi_kernel_us": mk_fused * 1e3,
-                     "mmi_gbs": mmi_bytes_fused / (mk_fused * 1e-3) / 1e9,
-                     "mmi_tops": 2.0 * m * k * n / (mk_fused * 1e-3) / 1e12},
-           "dql_gbs": dql_bytes / ((kernel_avg_ms(kt, "k_dql_minmax") +
-                                    kernel_avg_ms(kt, "k_dql_quant")) * 1e-3) / 1e9}
+                            "frac": mmi_bytes / (mmi_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                            "tops": 2.0 * m * k * n / (mmi_us * 1e-6) / 1e12,
+                            "int8_peak_frac": 2.0 * m * k * n / (mmi_us * 1e-6) / 1e12
+                            / INT8_PEAK_TOPS}}
     for bf in (dx, dbs, daq, dsc, dzp, dacc, dy):
         bf.free()
     pack.free()
@@ -669,10 +676,11 @@ def main():
                                      200, 20)
             print(f"# GEMM M=512: {out['gemm']['tflops']:.1f} TFLOP/s op, kernel "
                   f"{out['gemm']['roofline']['achieved']:.1f}", file=sys.stderr, flush=True)
-            out["int8"] = bench_int8(ctx, lib, ops, synth, 500, 50)
+            out["int8"] = bench_int8(ctx, lib, ops, synth, 20, 3)
             print(f"# int8 chain: {out['int8']['ms_per_chain'] * 1e3:.1f} us "
-                  f"(fused, no int32 output: {out['int8']['fused']['ms_per_chain'] * 1e3:.1f} us)",
-                  file=sys.stderr, flush=True)
+                  f"(fused, no int32 output: {out['int8']['fused']['ms_per_chain'] * 1e3:.1f} us;"
+                  f" DQL {out['int8']['dql_us']:.1f} us, MatMulInteger "
+                  f"{out['int8']['mmi_us']:.1f} us)", file=sys.stderr, flush=True)
             sweep = []
             for m in (1, 4, 8):
                 for (k, n) in synth.DECODE_PROJECTIONS:
