@@ -68,11 +68,15 @@ def make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed):
     return packs
 
 
-def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup):
-    """One step = one call on each pack (recorded once as a HIP graph).
+def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup, min_calls=32):
+    """One step = one call on each pack.  Each HIP graph holds enough whole
+    steps for at least min_calls calls (one step for the headline's 38
+    packs), so the gap between graph launches is amortised like the gap
+    between kernels; `steps` steps are timed (rounded up to whole graphs).
     Returns (timed steps, ms per step, ms per call, dispatch-event kernel
     durations per name)."""
     P = len(packs)
+    per_graph = max(1, -(-min_calls // P))  # steps per graph
 
     def issue_round():
         for p in packs:
@@ -81,13 +85,16 @@ def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup):
     issue_round()  # sizes any scratch before capture
     ctx.synchronize()
     ctx.graph_begin()
-    issue_round()
+    for _ in range(per_graph):
+        issue_round()
     g = ctx.graph_end()
-    for _ in range(warmup):
+    launches = -(-steps // per_graph)
+    steps = launches * per_graph
+    for _ in range(-(-warmup // per_graph)):
         ctx.graph_launch(g)
     ctx.synchronize()
     ctx.event_record(0)
-    for _ in range(steps):
+    for _ in range(launches):
         ctx.graph_launch(g)
     ctx.event_record(1)
     ctx.synchronize()
@@ -410,12 +417,21 @@ def bench_platform(ctx, lib):
     """Per-dispatch floor and streaming-read ceiling of this GPU, measured
     with the library's calibration kernels and the same dispatch events."""
     out = {}
-    ctx.kernel_timing(True, max_launches=400)
-    for _ in range(200):
-        lib.check(ctx.lib.mmnb_probe_empty(ctx.handle, 1024))
-    kt = ctx.kernel_timing_read()
-    ctx.kernel_timing(False)
-    out["empty_kernel_us"] = kt["k_probe_empty"][1] / kt["k_probe_empty"][0] * 1e3
+    # empty kernel of 1..1024 workgroups of 256 threads: duration from its
+    # dispatch events, and the per-launch cost inside a graph of 100 launches
+    sweep = {}
+    for blocks in (1, 64, 256, 512, 1024):
+        ctx.kernel_timing(True, max_launches=400)
+        for _ in range(200):
+            lib.check(ctx.lib.mmnb_probe_empty(ctx.handle, blocks))
+        kt = ctx.kernel_timing_read()
+        ctx.kernel_timing(False)
+        ev = kt["k_probe_empty"][1] / kt["k_probe_empty"][0] * 1e3
+        g_us = _graph_us(ctx, lambda: lib.check(ctx.lib.mmnb_probe_empty(ctx.handle, blocks)),
+                         steps=20, warmup=2, per_graph=100)
+        sweep[str(blocks)] = {"dispatch_event_us": ev, "in_graph_us": g_us}
+    out["empty_kernel_sweep"] = sweep
+    out["empty_kernel_us"] = sweep["1024"]["dispatch_event_us"]
     for label, size, nbuf, reps in (("read_8.95MB", 8945664, 37, 370),
                                     ("read_134MB", 134217728, 3, 30)):
         bufs = [ctx.alloc(size) for _ in range(nbuf)]

@@ -47,15 +47,19 @@ __device__ __forceinline__ float half_wave_sum(float v) {
 // point contributes exactly zero.  Folding the zero point in afterwards
 // (scale * sum a q - scale * zp * sum a) cancels catastrophically there.
 //
-// Both forms below put a scaled (q - zp) into the bytes of two dwords as
-// two's-complement int8 and convert each byte with one SDWA convert:
+// Each nibble becomes the exact (q - zp) times a power of two with one SDWA
+// convert:
 //   zero point 8 (no zero-point input): q ^ 8 is the 4-bit two's complement
-//     of q - 8, so the nibble moved to the top of its byte reads as
-//     16 (q - 8) in [-128, 112];
+//     of q - 8.  v_cvt_off_f32_i4 converts the signed 4-bit value in bits
+//     3:0 of its (byte-selected) operand to value / 16, so the low nibbles
+//     of w ^ 0x88888888 and of (w ^ 0x88888888) >> 4 give (q - 8) / 16
+//     directly: two bit operations per dword;
 //   any zero point z: 8q + (128 - 8z) lies in [8, 248] (no carry between
-//     bytes), and xor 0x80 turns that excess-128 byte into 8 (q - z).
-// The products a * 16(q - 8) and a * 8(q - z) are the exact products scaled
-// by a power of two; the kernels undo it once on the accumulated value.
+//     bytes), and xor 0x80 turns that excess-128 byte into 8 (q - z), read
+//     by a sign-extending byte convert.
+// The products a * (q - 8) / 16 and a * 8(q - z) are the exact products
+// scaled by a power of two; the kernels undo it once on the accumulated
+// value (dq_unscale).
 
 // Signed byte B of v as float (v_cvt_f32_i32 with an SDWA sign-extended
 // byte select: one instruction).
@@ -77,35 +81,60 @@ __device__ __forceinline__ float sbyte_f32(uint32_t v) {
   return r;
 }
 
-// The byte-offset constant of zero point z for dq8_bytes.
+// The signed 4-bit value in bits 3:0 of byte B of v, divided by 16
+// (v_cvt_off_f32_i4 with an SDWA byte select: one instruction).
+template <int B>
+__device__ __forceinline__ float snib16_f32(uint32_t v) {
+  float r;
+  if constexpr (B == 0)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0"
+        : "=v"(r) : "v"(v));
+  else if constexpr (B == 1)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+        : "=v"(r) : "v"(v));
+  else if constexpr (B == 2)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+        : "=v"(r) : "v"(v));
+  else
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=v"(r) : "v"(v));
+  return r;
+}
+
+// The byte-offset constant of zero point z for the explicit-zero-point form.
 __device__ __forceinline__ uint32_t dq8_const(int z) { return (uint32_t)(128 - 8 * z) * 0x01010101u; }
 
-// Scale of the dequantised values: 16 (zero point 8) or 8 (explicit zero
-// points); the kernels multiply their sums by its inverse.
+// Scale S of the dequantised values: 1/16 (zero point 8) or 8 (explicit
+// zero points); the kernels multiply their sums by 1 / S.
 template <bool HAS_ZP>
-constexpr float dq_unscale() { return HAS_ZP ? 0.125f : 0.0625f; }
+constexpr float dq_unscale() { return HAS_ZP ? 0.125f : 16.0f; }
 
-// Nibbles of w as 8 floats f[e] = S * (q_e - z), S = 16 (HAS_ZP false, z =
-// 8) or 8 (HAS_ZP true, zc = dq8_const(z)); exact.
+// Nibbles of w as 8 floats f[e] = S * (q_e - z), S = 1/16 (HAS_ZP false,
+// z = 8) or 8 (HAS_ZP true, zc = dq8_const(z)); exact.
 template <bool HAS_ZP>
 __device__ __forceinline__ void dq_nibbles(uint32_t w, uint32_t zc, float *f) {
-  uint32_t lo, hi;
   if constexpr (HAS_ZP) {
-    lo = (((w << 3) & 0x78787878u) + zc) ^ 0x80808080u;
-    hi = (((w >> 1) & 0x78787878u) + zc) ^ 0x80808080u;
+    const uint32_t lo = (((w << 3) & 0x78787878u) + zc) ^ 0x80808080u;
+    const uint32_t hi = (((w >> 1) & 0x78787878u) + zc) ^ 0x80808080u;
+    f[0] = sbyte_f32<0>(lo);
+    f[1] = sbyte_f32<0>(hi);
+    f[2] = sbyte_f32<1>(lo);
+    f[3] = sbyte_f32<1>(hi);
+    f[4] = sbyte_f32<2>(lo);
+    f[5] = sbyte_f32<2>(hi);
+    f[6] = sbyte_f32<3>(lo);
+    f[7] = sbyte_f32<3>(hi);
   } else {
-    const uint32_t x = w ^ 0x88888888u;
-    lo = (x << 4) & 0xF0F0F0F0u;
-    hi = x & 0xF0F0F0F0u;
+    const uint32_t x = w ^ 0x88888888u, xh = x >> 4;
+    f[0] = snib16_f32<0>(x);
+    f[1] = snib16_f32<0>(xh);
+    f[2] = snib16_f32<1>(x);
+    f[3] = snib16_f32<1>(xh);
+    f[4] = snib16_f32<2>(x);
+    f[5] = snib16_f32<2>(xh);
+    f[6] = snib16_f32<3>(x);
+    f[7] = snib16_f32<3>(xh);
   }
-  f[0] = sbyte_f32<0>(lo);
-  f[1] = sbyte_f32<0>(hi);
-  f[2] = sbyte_f32<1>(lo);
-  f[3] = sbyte_f32<1>(hi);
-  f[4] = sbyte_f32<2>(lo);
-  f[5] = sbyte_f32<2>(hi);
-  f[6] = sbyte_f32<3>(lo);
-  f[7] = sbyte_f32<3>(hi);
 }
 
 // Greedy-decoding key of a logit: orderable bits of v above ~col, so the

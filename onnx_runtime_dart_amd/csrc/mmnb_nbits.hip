@@ -277,8 +277,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
         }
         acc[r] = fmaf(inbq[q] ? sraw[r][q] : 0.0f, d, acc[r]);
       }
+      // column by column: the scheduler would otherwise hoist later
+      // columns' dequantisation and so wait for every weight load first
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
   // ---- reductions: 32 lanes of a half-wave, then the waves
 #pragma unroll
@@ -407,7 +409,9 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
 #pragma unroll
     for (int e = 0; e < 32; e++) av[e] = av[e] * inv * gv[e];
   }
-  // ---- arithmetic: exact 16 (q - 8) per weight (dq_nibbles), unscaled below
+  // ---- arithmetic: exact (q - 8) / 16 per weight (dq_nibbles), unscaled
+  // below; column by column (scheduling barriers), so that column r waits
+  // only for its own weights
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -422,6 +426,7 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
     }
     const float sc = cv ? sraw[r] : 0.0f;
     acc[r] = sc * d;
+    __builtin_amdgcn_sched_barrier(0);
   }
   // ---- reductions: 32 lanes of a half-wave, then the waves
 #pragma unroll

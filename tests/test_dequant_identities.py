@@ -2,13 +2,15 @@
 with (dq_nibbles in onnx_runtime_dart_amd/csrc/mmnb_device.h), and of the
 power of the accumulation-bound check used by the GPU parity tests.
 
-The kernels turn a dword of 8 nibbles into two dwords of signed bytes that
-hold the exact (q - zp) scaled by a power of two:
-  zero point 8:  x = w ^ 0x88888888; lo = (x << 4) & 0xF0F0F0F0,
-                 hi = x & 0xF0F0F0F0; byte b reads 16 (q - 8)
+The kernels turn a dword of 8 nibbles into 8 floats that hold the exact
+(q - zp) scaled by a power of two:
+  zero point 8:  x = w ^ 0x88888888, xh = x >> 4; the low nibble of byte b
+                 of x (of xh) is the 4-bit two's complement of q - 8 for
+                 nibble 2b (2b + 1), converted by v_cvt_off_f32_i4 (signed
+                 4-bit value / 16, its documented table) to (q - 8) / 16
   zero point z:  lo = (((w << 3) & 0x78787878) + c) ^ 0x80808080,
                  hi = (((w >> 1) & 0x78787878) + c) ^ 0x80808080,
-                 c = (128 - 8z) * 0x01010101; byte b reads 8 (q - z)
+                 c = (128 - 8z) * 0x01010101; signed byte b reads 8 (q - z)
 Checked here for every nibble value in every position and every z.
 """
 import numpy as np
@@ -34,17 +36,42 @@ def _nibbles(w):
     return np.stack([((w >> (4 * e)) & 0xF) for e in range(8)], -1).astype(np.int64)
 
 
-def _dq(w, z=None):
-    """The kernel's integer steps; returns [.., 8] values in nibble order."""
+# v_cvt_off_f32_i4: bits 3:0 of the operand, as a signed 4-bit value, / 16
+# (the instruction's table: 0b1000 -> -0.5, 0b1111 -> -0.0625, 0b0000 -> 0,
+# 0b0111 -> 0.4375)
+_CVT_OFF_I4 = {0b1000: -0.5, 0b1111: -0.0625, 0b0000: 0.0, 0b0111: 0.4375}
+
+
+def _cvt_off_f32_i4(v):
+    n = np.asarray(v, np.int64) & 0xF
+    return np.where(n >= 8, n - 16, n) / 16.0
+
+
+def test_cvt_off_table():
+    for n, want in _CVT_OFF_I4.items():
+        assert _cvt_off_f32_i4(n) == want
+        # the byte select passes the whole byte; only bits 3:0 count
+        assert _cvt_off_f32_i4(n | 0xA0) == want
+
+
+def _dq_zp8(w):
+    """The zero-point-8 kernel steps; [.., 8] floats in nibble order."""
     w = np.asarray(w, np.uint32)
-    if z is None:
-        x = w ^ np.uint32(0x88888888)
-        lo = (x << np.uint32(4)) & np.uint32(0xF0F0F0F0)
-        hi = x & np.uint32(0xF0F0F0F0)
-    else:
-        c = np.uint32(((128 - 8 * z) * 0x01010101) & 0xFFFFFFFF)
-        lo = (((w << np.uint32(3)) & np.uint32(0x78787878)) + c) ^ np.uint32(0x80808080)
-        hi = (((w >> np.uint32(1)) & np.uint32(0x78787878)) + c) ^ np.uint32(0x80808080)
+    x = w ^ np.uint32(0x88888888)
+    xh = x >> np.uint32(4)
+    out = np.empty(w.shape + (8,), np.float64)
+    for b in range(4):
+        out[..., 2 * b] = _cvt_off_f32_i4((x >> np.uint32(8 * b)) & np.uint32(0xFF))
+        out[..., 2 * b + 1] = _cvt_off_f32_i4((xh >> np.uint32(8 * b)) & np.uint32(0xFF))
+    return out
+
+
+def _dq(w, z):
+    """The explicit-zero-point kernel steps; [.., 8] values in nibble order."""
+    w = np.asarray(w, np.uint32)
+    c = np.uint32(((128 - 8 * z) * 0x01010101) & 0xFFFFFFFF)
+    lo = (((w << np.uint32(3)) & np.uint32(0x78787878)) + c) ^ np.uint32(0x80808080)
+    hi = (((w >> np.uint32(1)) & np.uint32(0x78787878)) + c) ^ np.uint32(0x80808080)
     lb, hb = _bytes_signed(lo), _bytes_signed(hi)
     out = np.empty(w.shape + (8,), np.int64)
     out[..., 0::2] = lb
@@ -69,7 +96,7 @@ def _all_words():
 
 def test_zero_point_8_identity():
     w = _all_words()
-    np.testing.assert_array_equal(_dq(w), 16 * (_nibbles(w) - 8))
+    np.testing.assert_array_equal(_dq_zp8(w), (_nibbles(w) - 8) / 16.0)
 
 
 @pytest.mark.parametrize("z", range(16))
