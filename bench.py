@@ -569,6 +569,15 @@ def profile_pass(ctx, lib, ops, synth, kind):
             lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, packs[i % count].handle, da.ptr,
                                                     m, dy.ptr))
         what = f"100 GEMV calls ({mmnb_bytes(m, k, n, bs, False)} algorithmic bytes each)"
+    elif kind == "gemv_large":
+        # eager dispatches with gaps between them, then graph replays back
+        # to back: a kernel trace shows the duration of both
+        r = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128, False, 40, 3, seed=4)
+        what = (f"GEMV K=N=16384 block 128: {r['calls']} graph-replayed calls "
+                f"({r['ms_per_call'] * 1e3:.2f} us per call) and the eager timing pass "
+                f"({r['dispatch_event_us']:.2f} us per dispatch)")
+        print(f"# profile pass: {what}", file=sys.stderr, flush=True)
+        return
     elif kind == "gemm":
         m, k, n, bs = 512, 4096, 4096, 32
         p = synth.mmnb_problem(m, k, n, bs, True, seed=2, outlier_frac=0.01)
@@ -625,8 +634,9 @@ def main():
                          "--profile-kind, then a 64 MiB device-to-device copy (10 calls) as "
                          "the counter calibration")
     ap.add_argument("--profile-kind", default="gemv",
-                    choices=["gemv", "gemm", "int8", "decoder"],
-                    help="gemv: headline GEMV, 100 calls over the rotated packs; gemm: "
+                    choices=["gemv", "gemv_large", "gemm", "int8", "decoder"],
+                    help="gemv: headline GEMV, 100 calls over the rotated packs; "
+                         "gemv_large: K=N=16384, graph replays and eager dispatches; gemm: "
                          "M=512 K=N=4096 block 32 with zero points, 20 calls; int8: the "
                          "DQL -> MatMulInteger -> rescale chain, 50 calls; decoder: the "
                          "Qwen3-shaped decoder, 256-token prefill + 64 steps, eager")

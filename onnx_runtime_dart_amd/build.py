@@ -9,6 +9,10 @@ then the objects are linked into the shared library.
 Packed FP32 instructions are disabled for all device code
 (-target-feature -packed-fp32-ops); the host pass warns that it does not
 know the feature, which is harmless.
+
+Host-only sources (the ONNX reader and MatMulNBits host preparation, which
+the CPU fuzz harness also builds under AddressSanitizer) are compiled with
+the host C++ compiler.
 """
 import os
 import shutil
@@ -23,6 +27,7 @@ OBJ = PKG / "_build"
 LIB = PKG / "libmmnb.so"
 SOURCES = ["mmnb_runtime.hip", "mmnb_nbits.hip", "mmnb_int8.hip", "mmnb_decoder.hip",
            "mmnb_qlinear.hip", "mmnb_nbits_ex.hip", "mmnb_model.hip", "mmnb_noalloc.hip"]
+HOST_SOURCES = ["mmnb_host.cpp"]
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -37,6 +42,16 @@ def hipcc():
     raise RuntimeError("hipcc not found (ROCm is required to build libmmnb)")
 
 
+def host_cxx():
+    for cand in (os.environ.get("CXX"), shutil.which("g++"), shutil.which("c++")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("no host C++ compiler (g++) found")
+
+
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
+
+
 def _filtered(r):
     return "\n".join(l for l in (r.stdout + r.stderr).splitlines()
                      if "packed-fp32-ops" not in l and l.strip())
@@ -47,20 +62,28 @@ def build(verbose=False, jobs=None):
     OBJ.mkdir(exist_ok=True)
     sources = [s for s in SOURCES if (CSRC / s).exists()]
 
+    host_sources = [s for s in HOST_SOURCES if (CSRC / s).exists()]
+    cxx = host_cxx() if host_sources else None
+
     def compile_one(src):
         obj = OBJ / (Path(src).stem + ".o")
-        cmd = [cc, f"--offload-arch={ARCH}", "-c"] + FLAGS + ["-o", str(obj), str(CSRC / src)]
+        if src in host_sources:
+            cmd = [cxx, "-c"] + HOST_FLAGS + ["-o", str(obj), str(CSRC / src)]
+        else:
+            cmd = [cc, f"--offload-arch={ARCH}", "-c"] + FLAGS + ["-o", str(obj),
+                                                                  str(CSRC / src)]
         return src, obj, cmd, subprocess.run(cmd, capture_output=True, text=True)
 
-    jobs = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    units = sources + host_sources
+    jobs = jobs or min(len(units), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        results = list(ex.map(compile_one, sources))
+        results = list(ex.map(compile_one, units))
     for src, _, cmd, r in results:
         if verbose:
             print(" ".join(cmd), flush=True)
         msgs = _filtered(r)
         if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src} ({r.returncode}):\n{msgs}")
+            raise RuntimeError(f"compiler failed on {src} ({r.returncode}):\n{msgs}")
         if verbose and msgs:
             print(msgs)
     out_tmp = LIB.with_suffix(".so.tmp")
