@@ -304,6 +304,7 @@ struct MmiEpiIn {
   float as;
 };
 
+template <int TI = 2>
 __device__ __forceinline__ void mmi_epi_load(MmiEpiIn &in, int64_t bz, int64_t M, int64_t N,
                                              int64_t m0, int64_t n0, int lane,
                                              const int32_t *__restrict__ colsum,
@@ -314,7 +315,7 @@ __device__ __forceinline__ void mmi_epi_load(MmiEpiIn &in, int64_t bz, int64_t M
   const bool zload = azp_len > 0 && !o.azp_is_const;
   const int32_t *zp = zload ? azp : (const int32_t *)pad;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TI; i++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       int64_t row = m0 + i * 16 + q * 4 + r;
@@ -344,19 +345,20 @@ __device__ __forceinline__ void mmi_epi_load(MmiEpiIn &in, int64_t bz, int64_t M
 // applies the exact integer zero-point corrections and stores what `o` asks
 // for (int32, the fused fp32 rescale, 8-bit requantisation).  16x16 i32
 // accumulator layout: lane l holds column l%16 and rows 4*(l/16) + r.
-__device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[2][2], int (&rsum)[2],
+template <int TI = 2>
+__device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[TI][2], int (&rsum)[TI],
                                              const MmiEpiIn &in, int a_signed, int64_t bz,
                                              int64_t M, int64_t K, int64_t N, int64_t m0,
                                              int64_t n0, int lane, int64_t azp_len,
                                              const MmiEpi &o) {
   const int r16 = lane & 15, q = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
+  for (int t = 0; t < TI; t++) {
     rsum[t] += __shfl_xor(rsum[t], 16, 64);
     rsum[t] += __shfl_xor(rsum[t], 32, 64);
   }
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < TI; i++) {
     int32_t rs[4], cm[4];
     int64_t row[4];
 #pragma unroll
@@ -400,26 +402,28 @@ __device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[2][2], int (&rsu
 }
 
 // Epilogue of the row-major int32 / fp32 outputs through LDS: the exact
-// zero-point corrections of mmi_epilogue, then the wave's 32 x 32 tile parked
-// in `tiles` (two 32 x 33 arrays: int32 and fp32; 8448 bytes per wave) and
-// stored back as 16 bytes per lane, 8 full 128-byte rows per instruction
-// (the MFMA layout would write 64-byte row pieces 16 columns wide).  The
-// caller's LDS must be free of other readers (a barrier after the K loop).
-__device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[2][2], int (&rsum)[2],
+// zero-point corrections of mmi_epilogue, then the wave's (16 TI) x 32 tile
+// parked in `tiles` (two (16 TI) x 33 arrays: int32 and fp32; 4224 TI bytes
+// per wave) and stored back as 16 bytes per lane, 8 full 128-byte rows per
+// instruction (the MFMA layout would write 64-byte row pieces 16 columns
+// wide).  The caller's LDS must be free of other readers (a barrier after
+// the K loop).
+template <int TI = 2>
+__device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[TI][2], int (&rsum)[TI],
                                                  const MmiEpiIn &ein, int a_signed, int64_t bz,
                                                  int64_t M, int64_t K, int64_t N, int64_t m0,
                                                  int64_t n0, int lane, int64_t azp_len,
                                                  const MmiEpi &o, uint32_t *tiles) {
   const int r16 = lane & 15, q = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
+  for (int t = 0; t < TI; t++) {
     rsum[t] += __shfl_xor(rsum[t], 16, 64);
     rsum[t] += __shfl_xor(rsum[t], 32, 64);
   }
-  uint32_t *ti = tiles;                   // int32 tile [32][33]
-  float *tf = (float *)(tiles + 32 * 33);  // fp32 tile [32][33]
+  uint32_t *ti = tiles;                          // int32 tile [16 TI][33]
+  float *tf = (float *)(tiles + 16 * TI * 33);  // fp32 tile [16 TI][33]
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
+  for (int i = 0; i < TI; i++) {
     int32_t rs[4], cm[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -448,7 +452,7 @@ __device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[2][2], int (
   const bool vec = n0 + 32 <= N && (N & 3) == 0 &&
                    ((((uintptr_t)o.y) | ((uintptr_t)o.yf)) & 15) == 0;
 #pragma unroll
-  for (int pass = 0; pass < 4; pass++) {
+  for (int pass = 0; pass < 2 * TI; pass++) {
     const int rr = pass * 8 + (lane >> 3);
     const int64_t row = m0 + rr;
     uint32_t v[4];
@@ -560,109 +564,126 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 
 
 // MatMulInteger with LDS staging by direct global->LDS DMA
-// (global_load_lds_dwordx4, 16 B per lane, no VGPR round trip).  Same tile
-// and arithmetic as k_mmi_mfma.  K moves in chunks of kMmiKc bytes through a
-// two-slot ring: the next chunk is in flight while the current one is
-// multiplied (every thread issues the same kMmiLoads DMA loads per chunk, so
-// "chunk c has landed" is vmcnt <= kMmiLoads while chunk c+1 is pending; a
-// barrier then publishes it, another frees its slot).  LDS rows hold
-// kMmiPieces 16-byte pieces; piece c of row r is stored at slot c ^ (r & 15)
-// so the 16 rows an MFMA operand read touches land in 16 different bank
-// groups.  Pieces past K (or rows past M) are read from a constant page whose
-// bytes become zero after the int8 offset.  Requires K % 16 == 0 and a
-// 16-byte aligned A.
+// (global_load_lds_dwordx4, 16 B per lane, no VGPR round trip).  Workgroup
+// tile TM x 64 (TM = 64 or 32), 4 waves in 2 x 2, wave tile (TM/2) x 32 of
+// 16 x 16 MFMA tiles, K steps of 64 as k_mmi_mfma.  K moves in chunks of
+// kMmiKc bytes through a two-slot ring: the next chunk is in flight while the
+// current one is multiplied (every thread issues the same number of DMA
+// loads per chunk, so "chunk c has landed" is vmcnt <= that number while
+// chunk c+1 is pending; a barrier then publishes it, another frees its
+// slot).  LDS rows hold kMmiPieces 16-byte pieces; piece c of row r is
+// stored at slot c ^ (r & 15) so the 16 rows an MFMA operand read touches
+// land in 16 different bank groups.  Pieces past K (or rows past M) are read
+// from a constant page whose bytes become zero after the int8 offset.
+// Requires K % 16 == 0 and a 16-byte aligned A.
+//
+// TM = 32 doubles the workgroups for the same output: L2 -> LDS streaming
+// rises with the waves per CU (three 48 KB workgroups fit a CU where two
+// 64 KB ones did), which outweighs re-reading B twice as often.
 constexpr int kMmiKc = 256;
-constexpr int kMmiPieces = kMmiKc / 16;                   // per row
-constexpr int kMmiSlotU4 = 64 * kMmiPieces;               // uint4 per operand per slot
-constexpr int kMmiLoads = 2 * (kMmiSlotU4 / 64) / 4;      // DMA loads per thread per chunk
+constexpr int kMmiPieces = kMmiKc / 16;  // per row
 
-template <bool LDS_EPI>
+template <bool LDS_EPI, int TM>
 __global__ __launch_bounds__(256) void k_mmi_lds(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
     const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
     int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o,
     const uint8_t *__restrict__ pad) {
-  // one array: the A ring (slots 0-1) and the B ring (slots 2-3), which the
-  // LDS epilogue reuses whole
-  __shared__ uint4 smem[4][kMmiSlotU4];
-  uint4 (*sA)[kMmiSlotU4] = smem;
-  uint4 (*sB)[kMmiSlotU4] = smem + 2;
+  constexpr int TI = TM / 32;                      // 16-row blocks per wave
+  constexpr int kSA = TM * kMmiPieces;             // uint4 per A slot
+  constexpr int kSB = 64 * kMmiPieces;             // uint4 per B slot
+  constexpr int kLoads = (kSA + kSB) / 64 / 4;     // DMA loads per thread per chunk
+  static_assert((kSA / 64) % 4 == 0 && (kSB / 64) % 4 == 0, "whole DMA rounds per wave");
+  // one array: the A ring (two slots of kSA) then the B ring (two of kSB),
+  // which the LDS epilogue reuses whole
+  __shared__ uint4 smem[2 * (kSA + kSB)];
+  uint4 *sA0 = smem, *sB0 = smem + 2 * kSA;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t bz = blockIdx.z;
   const uint8_t *Ab = A + bz * a_bstride;
   const int8_t *Bb = Bt + bz * b_bstride;
-  const int64_t m0 = (int64_t)blockIdx.y * 64 + wm * 32;
+  const int64_t m0 = (int64_t)blockIdx.y * TM + wm * (TM / 2);
   const int64_t n0 = (int64_t)blockIdx.x * 64 + wn * 32;
-  const int64_t mt0 = (int64_t)blockIdx.y * 64, nt0 = (int64_t)blockIdx.x * 64;
+  const int64_t mt0 = (int64_t)blockIdx.y * TM, nt0 = (int64_t)blockIdx.x * 64;
   const int r16 = lane & 15, q = lane >> 4;
   const uint32_t flip = a_signed ? 0u : 0x80808080u;
   const uint8_t *apad = pad + (a_signed ? 0 : 1024);
   const int nchunks = (int)((kpad + kMmiKc - 1) / kMmiKc);
 
   // DMA of chunk c into slot s: instruction i of a wave fills LDS slots
-  // [64 i, 64 i + 64) of each operand.
+  // [64 i, 64 i + 64) of an operand.
   auto issue = [&](int c, int s) {
     const int64_t k0 = (int64_t)c * kMmiKc;
 #pragma unroll
-    for (int u = 0; u < kMmiSlotU4 / 64 / 4; u++) {
+    for (int u = 0; u < kSA / 64 / 4; u++) {
       const int i = wave + 4 * u;
       const int slot = i * 64 + lane;
       const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
-      const int pc = cs_ ^ (r & 15);
-      const int64_t kk = k0 + (int64_t)pc * 16;
+      const int64_t kk = k0 + (int64_t)(cs_ ^ (r & 15)) * 16;
       const int64_t arow = mt0 + r;
       const uint8_t *ga = (arow < M && kk < K) ? Ab + arow * K + kk : apad;
+      dma16(ga, sA0 + s * kSA + i * 64);
+    }
+#pragma unroll
+    for (int u = 0; u < kSB / 64 / 4; u++) {
+      const int i = wave + 4 * u;
+      const int slot = i * 64 + lane;
+      const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
+      const int64_t kk = k0 + (int64_t)(cs_ ^ (r & 15)) * 16;
       int64_t bcol = nt0 + r;
       if (bcol >= N) bcol = N - 1;
       const int8_t *gb = kk < kpad ? Bb + bcol * kpad + kk : (const int8_t *)pad;
-      uint4 *da = &sA[s][i * 64];
-      uint4 *db = &sB[s][i * 64];
-      dma16(ga, da);
-      dma16(gb, db);
+      dma16(gb, sB0 + s * kSB + i * 64);
     }
   };
 
-  int4v acc[2][2];
+  int4v acc[TI][2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TI; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = (int4v){0, 0, 0, 0};
-  int rsum[2] = {0, 0};
+  int rsum[TI];
+#pragma unroll
+  for (int i = 0; i < TI; i++) rsum[i] = 0;
   // issued before the first chunk, so the chunk waits below cover them too
   MmiEpiIn ein;
-  mmi_epi_load(ein, bz, M, N, m0, n0, lane, colsum, cs_bstride, ecol, azp, azp_len, o, pad);
+  mmi_epi_load<TI>(ein, bz, M, N, m0, n0, lane, colsum, cs_bstride, ecol, azp, azp_len, o, pad);
 
   issue(0, 0);
   if (nchunks > 1) issue(1, 1);
   for (int c = 0; c < nchunks; c++) {
     const int s = c & 1;
     if (c + 1 < nchunks)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kMmiLoads));
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoads));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __builtin_amdgcn_s_barrier();
+    const uint4 *sA = sA0 + s * kSA, *sB = sB0 + s * kSB;
     const int64_t kc = kpad - (int64_t)c * kMmiKc < kMmiKc ? kpad - (int64_t)c * kMmiKc
                                                             : kMmiKc;  // multiple of 64
     for (int st = 0; st < kc / 64; st++) {
-      int4v av[2], bv[2];
+      int4v av[TI], bv[2];
 #pragma unroll
-      for (int t = 0; t < 2; t++) {
-        const int ra = wm * 32 + t * 16 + r16;
-        const uint4 x = sA[s][ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
+      for (int t = 0; t < TI; t++) {
+        const int ra = wm * (TM / 2) + t * 16 + r16;
+        const uint4 x = sA[ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
         uint32_t w[4] = {x.x ^ flip, x.y ^ flip, x.z ^ flip, x.w ^ flip};
 #pragma unroll
         for (int d = 0; d < 4; d++)
           rsum[t] = __builtin_amdgcn_sdot4((int)w[d], 0x01010101, rsum[t], false);
         av[t] = (int4v){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      }
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
         const int rb = wn * 32 + t * 16 + r16;
-        const uint4 y = sB[s][rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
+        const uint4 y = sB[rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
         bv[t] = (int4v){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
       }
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < TI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
@@ -673,15 +694,14 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
     }
   }
   if constexpr (LDS_EPI) {
+    static_assert(4 * 2 * 16 * TI * 33 * 4 <= (int)sizeof(smem), "epilogue tiles fit the ring");
     __syncthreads();  // the ring is free: it holds the output tiles now
-    mmi_epilogue_lds(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o,
-                     (uint32_t *)&smem[0][0] + wave * 2 * 32 * 33);
+    mmi_epilogue_lds<TI>(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o,
+                         (uint32_t *)smem + wave * 2 * 16 * TI * 33);
   } else {
-    mmi_epilogue(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o);
+    mmi_epilogue<TI>(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o);
   }
 }
-
-
 
 int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, int a_signed,
                           int64_t a_batch, int64_t m, const int32_t *d_azp, int64_t azp_len,
@@ -695,8 +715,18 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
   const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
   if (fast && ctx->d_pad) {
-    auto kern = (!o.yq && !o.trans) ? k_mmi_lds<true> : k_mmi_lds<false>;
-    return launch(ctx, kKernMmi, kern, grid, dim3(256), 0, (const uint8_t *)d_a, a_signed,
+    // 32-row tiles when 64-row ones would leave fewer than three workgroups
+    // per CU (tuning override: MMNB_MMI_TM)
+    const int64_t tiles64 = (int64_t)grid.x * grid.y * grid.z;
+    const int tm = ctx->mmi_tm ? ctx->mmi_tm : (tiles64 < 3 * (int64_t)ctx->cu_count ? 32 : 64);
+    const bool le = !o.yq && !o.trans;
+    auto kern = le ? k_mmi_lds<true, 64> : k_mmi_lds<false, 64>;
+    dim3 g = grid;
+    if (tm == 32) {
+      kern = le ? k_mmi_lds<true, 32> : k_mmi_lds<false, 32>;
+      g.y = (unsigned)((m + 31) / 32);
+    }
+    return launch(ctx, kKernMmi, kern, g, dim3(256), 0, (const uint8_t *)d_a, a_signed,
                   a_batch == 1 ? (int64_t)0 : m * k, m, k, (const int8_t *)p->d_bt,
                   p->batch == 1 ? (int64_t)0 : n * p->kpad, p->kpad,
                   (const int32_t *)p->d_colsum, p->batch == 1 ? (int64_t)0 : n,

@@ -97,6 +97,8 @@ struct mmnb_ctx {
   int gemm_ksplit = 0;
   // Stream capture in progress (no synchronisation or allocation allowed).
   bool capturing = false;
+  // MatMulInteger row tile (32 or 64; 0 = by shape), from MMNB_MMI_TM.
+  int mmi_tm = 0;
   // Device address of this device's fixed workspace for
   // mmnb_matmul_nbits_dev_noalloc (set by noalloc_setup at init).
   void *noalloc_ws = nullptr;

@@ -117,6 +117,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v == 1 || v == 2 || v == 4 || v == 8) ctx->gemm_ksplit = v;
   }
+  if (const char *r = std::getenv("MMNB_MMI_TM")) {
+    const int v = std::atoi(r);
+    if (v == 32 || v == 64) ctx->mmi_tm = v;
+  }
   if (const char *r = std::getenv("MMNB_GEMV_CG")) {
     const int v = std::atoi(r);
     if (v >= 1 && v <= 8) ctx->gemv_cg = v;
