@@ -410,8 +410,10 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
     for (int e = 0; e < 32; e++) av[e] = av[e] * inv * gv[e];
   }
   // ---- arithmetic: exact (q - 8) / 16 per weight (dq_nibbles), unscaled
-  // below; column by column (scheduling barriers), so that column r waits
-  // only for its own weights
+  // below; column by column, so that column r waits only for its own
+  // weights.  The empty asm pins each column's sum in its place: without it
+  // the compiler sinks the FMAs of every column but the first to the end,
+  // keeping all 8R dequantised values live (270 VGPRs at R = 8).
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -426,6 +428,7 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
     }
     const float sc = cv ? sraw[r] : 0.0f;
     acc[r] = sc * d;
+    asm volatile("" : "+v"(acc[r]));
     __builtin_amdgcn_sched_barrier(0);
   }
   // ---- reductions: 32 lanes of a half-wave, then the waves
