@@ -694,6 +694,10 @@ def main():
                                              args.steps, args.warmup, seed=3)
             print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['kernel_gbs']:.0f} GB/s kernel",
                   file=sys.stderr, flush=True)
+            out["c1_gemv"] = bench_gemv(ctx, lib, ops, synth, 1, 1024, 1024, 32, True, 20, 3,
+                                        seed=5)
+            print(f"# C1 GEMV M=1 K=N=1024 bs32+zp: {out['c1_gemv']['ms_per_call'] * 1e3:.2f} us "
+                  f"per call, {out['c1_gemv']['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
             out["gemv_large"] = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128,
                                            False, 20, 3, seed=4)
             print(f"# GEMV K=N=16384: {out['gemv_large']['kernel_gbs']:.0f} GB/s kernel",
