@@ -658,20 +658,22 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 // (split of kDecKS keys, KV head), serving every query head of that KV
 // group, so each cached key and value is read once per layer and the read
 // is shared by many CUs (one CU alone streams only a few tens of GB/s of
-// dependent loads).  The workgroup issues its K / V tile first
-// (unconditional float4 loads: a conditional load would end in a full
-// vmcnt wait), forms the group's q heads and the new k (per-head RMSNorm,
-// rotary at pos) meanwhile, scores its keys (8 lanes per key, DPP
-// reduction) and writes a partial (max, sum, o[hd]) per query head.  The
-// last split of a KV head to finish (counter, reset by it) merges the
-// partials.  Partials and counters go through agent-scope atomics, which
-// are coherent across XCDs without an L2 flush.  The split holding position
-// pos uses the new k / v directly and also writes them into the cache; no
-// workgroup reads an entry written in the same launch.
+// dependent loads).  The workgroup first issues the loads its per-head
+// RMSNorm needs (q heads, new k and v, gammas, rotary row), then its K / V
+// tile (unconditional loads: a conditional load would end in a full vmcnt
+// wait), so the norms run while the tile is in flight.  Each wave then owns
+// 8 keys: scores (8 lanes per key, DPP reduction), a softmax over its keys
+// (the 8 scores read out with readlane, so wave-uniform) and p.v with no
+// LDS round trip; one barrier later the 4 waves' (max, sum, o) are merged
+// into the split's partial per query head.  The last split of a KV head to
+// finish (counter, reset by it) merges the partials.  Partials and counters
+// go through agent-scope atomics.  The split holding position pos uses the
+// new k / v directly and also writes them into the cache; no workgroup
+// reads an entry written in the same launch.
 constexpr int kDecKS = 32;          // keys per split
+constexpr int kDecKW = kDecKS / 4;  // keys per wave
 constexpr int kDecMaxGroup = 4;     // query heads per KV head
-constexpr int kDecMaxLen = 8192;    // cache length (merge weights kept in LDS)
-constexpr int kDecMaxSplits = kDecMaxLen / kDecKS;
+constexpr int kDecMaxLen = 8192;    // longest cache of a decoder session
 
 // Sum over each aligned group of 8 lanes (DPP within a row).
 __device__ __forceinline__ float lane8_sum(float v) {
@@ -679,6 +681,34 @@ __device__ __forceinline__ float lane8_sum(float v) {
   v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
   v = dpp_add<0x141>(v);  // row_half_mirror: lanes 0-7 <-> 7-0 of each half row
   return v;
+}
+
+// v + (v moved by the DPP control CTRL) for a double (both halves move).
+template <int CTRL>
+__device__ __forceinline__ double dpp_add_d(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF,
+                                                            false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL,
+                                                            0xF, 0xF, false);
+  return v + __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sum over the whole wave, wave-uniform: 16-lane sums by DPP, then the four
+// rows read out with readlane.
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v = dpp_add_d<0xB1>(v);
+  v = dpp_add_d<0x4E>(v);
+  v = dpp_add_d<0x141>(v);
+  v = dpp_add_d<0x140>(v);  // row_mirror
+  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
 
 // Operands of one layer's decode attention.  Partials live at
@@ -698,37 +728,51 @@ struct DecAttnArgs {
 };
 
 // One split of kDecKS keys of KV head kh at position pos: the group's q
-// heads and the new k (per-head RMSNorm, rotary at pos), scores (8 lanes per
-// key, DPP reduction), a split-local softmax, o = sum p v, and the partial
-// (max, sum, o) of every query head of the group.  The split holding pos also
-// writes the new k / v into the cache.  COH: qkv was written in the same
-// launch and the cache row is read by other workgroups of the same launch
-// (coherent loads / stores, see ld_act).  Whole workgroup, 256 threads.
-template <int HD, bool COH>
+// heads and the new k (per-head RMSNorm in double, rotary at pos), scores,
+// a softmax and o = sum p v per wave of kDecKW keys, then the split's
+// partial (max, sum, o) of every query head of the group.  The split
+// holding pos also writes the new k / v into the cache.  Whole workgroup,
+// 256 threads (4 waves).
+template <int HD>
 __device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int kh) {
-  constexpr int kDpk = HD / 8;  // dims per K lane (a multiple of 4)
-  constexpr int kHr = HD / 2;
+  constexpr int kDpk = HD / 8;  // K dims per lane (a multiple of 4)
+  constexpr int kHr = HD / 2;   // rotary half; norm lanes hold dims l, l + kHr
   __shared__ __align__(16) float sq[kDecMaxGroup][HD];
   __shared__ __align__(16) float skn[HD];
-  __shared__ float svn[HD];
-  __shared__ float shx[kDecMaxGroup + 1][HD];
-  __shared__ double shd[kDecMaxGroup + 1][4];
-  __shared__ __align__(16) float ssc[kDecMaxGroup][kDecKS];
-  __shared__ float sred[kDecMaxGroup][2][kAttnMaxHd];
-  __shared__ __align__(16) float sp[kDecMaxGroup][kDecKS];
-  __shared__ float smx[kDecMaxGroup], sl[kDecMaxGroup];
+  __shared__ __align__(16) float svn[HD];
+  __shared__ __align__(16) float so[4][kDecMaxGroup][HD];
+  __shared__ float sm[4][kDecMaxGroup], sl[4][kDecMaxGroup];
   const int nh = a.nh, kvh = a.kvh, group = nh / kvh;
-  const int t = threadIdx.x, w = t >> 6, ln = t & 63;
-  const int d = t & (kAttnMaxHd - 1), half = t >> 7;  // V layout: dim, key half
-  const int jk = t >> 3, p8 = t & 7;                  // K layout: key, dim slice
+  const int t = threadIdx.x, w = t >> 6, l = t & 63;
+  const int jk = t >> 3, p8 = t & 7;  // K layout: key, dim slice
   const int L = pos + 1;
   const int nsplit = (L + kDecKS - 1) / kDecKS;
   const int j0 = split * kDecKS;
   const float *Kb = a.ck + (int64_t)kh * a.cap * HD;
   const float *Vb = a.cv + (int64_t)kh * a.cap * HD;
-  const bool lo = t < HD;
-  const int dc = lo ? t : HD - 1;
-  // ---- loads (rows >= pos are read from row 0 and replaced or dropped)
+  // ---- loads, in the order they are used.  Norm rows: wave w takes q head
+  // min(w, group - 1) of the group (kept if w < group) and every wave the
+  // new k (kept by wave 0), so that no load or norm sits behind a branch;
+  // lane l < kHr holds dims l and l + kHr, so the rotary pair is in one lane.
+  const int lc = l < kHr ? l : 0;
+  float x0[2], x1[2], g0[2], g1[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const float *xr = a.qkv + (i == 0 ? kh * group + min(w, group - 1) : nh + kh) * HD;
+    const float *gr = i == 0 ? a.qn : a.kn;
+    x0[i] = xr[lc];
+    x1[i] = xr[lc + kHr];
+    g0[i] = gr[lc];
+    g1[i] = gr[lc + kHr];
+  }
+  const int lv = 2 * l < HD ? l : 0;  // V layout: dims 2 lv, 2 lv + 1
+  const float2 xv = *(const float2 *)(a.qkv + (nh + kvh + kh) * HD + 2 * lv);
+  const double cs = (double)a.cos[(int64_t)pos * kHr + lc];
+  const double sn = (double)a.sin[(int64_t)pos * kHr + lc];
+  // the norm's loads go out first (a wait for one of them waits for every
+  // load issued before it)
+  __builtin_amdgcn_sched_barrier(0);
+  // K / V tile (rows >= pos are read from row 0 and replaced or dropped)
   float kreg[kDpk];
   {
     const int j = j0 + jk;
@@ -742,196 +786,171 @@ __device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int k
       kreg[e + 3] = v4.w;
     }
   }
-  const int dv = d < HD ? d : HD - 1;
-  float vreg[kDecKS / 2];
+  float2 vreg[kDecKW];
 #pragma unroll
-  for (int u = 0; u < kDecKS / 2; u++) {
-    const int j = j0 + half * (kDecKS / 2) + u;
-    vreg[u] = Vb[(int64_t)(j < pos ? j : 0) * HD + dv];
+  for (int u = 0; u < kDecKW; u++) {
+    const int j = j0 + w * kDecKW + u;
+    vreg[u] = *(const float2 *)(Vb + (int64_t)(j < pos ? j : 0) * HD + 2 * lv);
   }
-  float xq[kDecMaxGroup];
+  // ---- per-head RMSNorm (double sums, wave-local) and rotary at pos
 #pragma unroll
-  for (int g = 0; g < kDecMaxGroup; g++)
-    xq[g] = ld_act<COH>(a.qkv + (kh * group + (g < group ? g : 0)) * HD + dc);
-  const float xk = ld_act<COH>(a.qkv + (nh + kh) * HD + dc);
-  const float xv = ld_act<COH>(a.qkv + (nh + kvh + kh) * HD + dc);
-  const float gq = a.qn[dc], gk = a.kn[dc];
-  const int pi = dc < kHr ? dc : dc - kHr;
-  const double cs = (double)a.cos[(int64_t)pos * kHr + pi];
-  const double sn = (double)a.sin[(int64_t)pos * kHr + pi];
-  // ---- per-head RMSNorm of the group's q heads and of k (double sums,
-  // one block reduction for all of them), then rotary at pos
-  {
-    double ss[kDecMaxGroup + 1];
-#pragma unroll
-    for (int g = 0; g <= kDecMaxGroup; g++) {
-      const float x = g < kDecMaxGroup ? xq[g] : xk;
-      ss[g] = lo ? (double)x * (double)x : 0.0;
+  for (int i = 0; i < 2; i++) {
+    const double ss = l < kHr ? (double)x0[i] * x0[i] + (double)x1[i] * x1[i] : 0.0;
+    const double inv = 1.0 / sqrt(wave_sum_d(ss) / (double)HD + (double)a.eps);
+    const float y0 = (float)((double)x0[i] * inv * (double)g0[i]);
+    const float y1 = (float)((double)x1[i] * inv * (double)g1[i]);
+    const float r0 = (float)((double)y0 * cs - (double)y1 * sn);
+    const float r1 = (float)((double)y1 * cs + (double)y0 * sn);
+    if (l < kHr && (i == 0 ? w < group : w == 0)) {
+      float *dst = i == 0 ? sq[w] : skn;
+      dst[l] = r0;
+      dst[l + kHr] = r1;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-      for (int g = 0; g <= kDecMaxGroup; g++)
-        if (g < group || g == kDecMaxGroup) ss[g] += __shfl_xor(ss[g], off, 64);
-    }
-    if (ln == 0) {
-#pragma unroll
-      for (int g = 0; g <= kDecMaxGroup; g++) shd[g][w] = ss[g];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g <= kDecMaxGroup; g++) {
-      const double tot = shd[g][0] + shd[g][1] + shd[g][2] + shd[g][3];
-      const double inv = 1.0 / sqrt(tot / (double)HD + (double)a.eps);
-      const float x = g < kDecMaxGroup ? xq[g] : xk;
-      const float gam = g < kDecMaxGroup ? gq : gk;
-      if (lo) shx[g][t] = (float)((double)x * inv * (double)gam);
-    }
-    __syncthreads();
-    if (lo) {
-#pragma unroll
-      for (int g = 0; g <= kDecMaxGroup; g++) {
-        const double x0 = shx[g][pi], x1 = shx[g][pi + kHr];
-        const float r = (float)(t < kHr ? x0 * cs - x1 * sn : x1 * cs + x0 * sn);
-        if (g < kDecMaxGroup) sq[g][t] = r; else skn[t] = r;
-      }
-      svn[t] = xv;
-    }
-    __syncthreads();
   }
-  // ---- scores of this split's keys for each query head of the group
-  {
-    const int j = j0 + jk;
-    if (j == pos) {
+  if (w == 3 && 2 * l < HD) *(float2 *)(svn + 2 * l) = xv;
+  __syncthreads();
+  // ---- scores of this wave's keys, for each query head of the group
+  const int j = j0 + jk;
+  if (j == pos) {
 #pragma unroll
-      for (int e = 0; e < kDpk; e++) kreg[e] = skn[p8 * kDpk + e];
-    }
+    for (int e = 0; e < kDpk; e++) kreg[e] = skn[p8 * kDpk + e];
+  }
+  float sc[kDecMaxGroup];
 #pragma unroll
-    for (int g = 0; g < kDecMaxGroup; g++) {
-      if (g < group) {
-        float dot = 0.0f;
+  for (int g = 0; g < kDecMaxGroup; g++) {
+    sc[g] = -INFINITY;
+    if (g < group) {
+      float dot = 0.0f;
 #pragma unroll
-        for (int e = 0; e < kDpk; e++) dot = fmaf(sq[g][p8 * kDpk + e], kreg[e], dot);
-        dot = lane8_sum(dot);
-        if (p8 == 0) ssc[g][jk] = j < L ? dot * a.scale : -INFINITY;
+      for (int e = 0; e < kDpk; e += 4) {
+        const float4 q4 = *(const float4 *)(&sq[g][p8 * kDpk + e]);
+        dot = fmaf(q4.x, kreg[e], dot);
+        dot = fmaf(q4.y, kreg[e + 1], dot);
+        dot = fmaf(q4.z, kreg[e + 2], dot);
+        dot = fmaf(q4.w, kreg[e + 3], dot);
       }
+      dot = lane8_sum(dot);
+      sc[g] = j < L ? dot * a.scale : -INFINITY;
     }
   }
   // values of keys past pos are dropped here (their probability is 0, but
   // the row they were read from may hold anything)
-  const float vnew = svn[dv];
+  {
+    const float2 vnew = *(const float2 *)(svn + 2 * lv);
 #pragma unroll
-  for (int u = 0; u < kDecKS / 2; u++) {
-    const int j = j0 + half * (kDecKS / 2) + u;
-    vreg[u] = j < pos ? vreg[u] : (j == pos ? vnew : 0.0f);
-  }
-  __syncthreads();
-  // ---- split-local softmax, one thread per (head, key): max and sum over
-  // the split's keys by shuffles within 32-lane groups, p to LDS
-  if (t < group * kDecKS) {
-    const int g = t / kDecKS, i = t % kDecKS;
-    const float sc = ssc[g][i];
-    float mx = sc;
-#pragma unroll
-    for (int off = kDecKS / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kDecKS));
-    const float p = expf(sc - mx);
-    float ls = p;
-#pragma unroll
-    for (int off = kDecKS / 2; off > 0; off >>= 1) ls += __shfl_xor(ls, off, kDecKS);
-    sp[g][i] = p;
-    if (i == 0) {
-      smx[g] = mx;
-      sl[g] = ls;
+    for (int u = 0; u < kDecKW; u++) {
+      const int jv = j0 + w * kDecKW + u;
+      if (jv >= pos) vreg[u] = jv == pos ? vnew : make_float2(0.0f, 0.0f);
     }
   }
-  __syncthreads();
-  // ---- o = sum_j p_j v_j over the split, thread (dim, key half) per head
+  // ---- softmax over the wave's keys (scores read out of lanes 8u, so
+  // wave-uniform) and o = sum_u p_u v_u; a wave whose keys are all past pos
+  // contributes max -inf and nothing else
 #pragma unroll
   for (int g = 0; g < kDecMaxGroup; g++) {
     if (g < group) {
-      float acc = 0.0f;
+      float s[kDecKW];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < kDecKS / 2; u++) acc = fmaf(sp[g][half * (kDecKS / 2) + u], vreg[u], acc);
-      sred[g][half][d] = acc;
+      for (int u = 0; u < kDecKW; u++) {
+        s[u] = __builtin_bit_cast(float,
+                                  __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc[g]), 8 * u));
+        mx = fmaxf(mx, s[u]);
+      }
+      float ls = 0.0f, o0 = 0.0f, o1 = 0.0f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int u = 0; u < kDecKW; u++) {
+          const float pu = expf(s[u] - mx);
+          ls += pu;
+          o0 = fmaf(pu, vreg[u].x, o0);
+          o1 = fmaf(pu, vreg[u].y, o1);
+        }
+      }
+      if (2 * l < HD) *(float2 *)(&so[w][g][2 * l]) = make_float2(o0, o1);
+      if (l == 0) {
+        sm[w][g] = mx;
+        sl[w][g] = ls;
+      }
     }
   }
   __syncthreads();
-  if (lo) {
-    for (int g = 0; g < group; g++) {
-      float *pp = a.part + ((int64_t)(kh * group + g) * a.nsmax + split) * (HD + 2);
-      if (t == 0) {
-        st_act<true>(pp, smx[g]);
-        st_act<true>(pp + 1, sl[g]);
+  // ---- the split's partial: thread (head g, dim pair dp) merges the waves
+  {
+    const int g = t / kHr, dp = t % kHr;
+    if (g < group) {
+      const float M = fmaxf(fmaxf(sm[0][g], sm[1][g]), fmaxf(sm[2][g], sm[3][g]));
+      float ls = 0.0f, o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < 4; ww++) {
+        const float wt = expf(sm[ww][g] - M);  // 0 for a wave with max -inf
+        const float2 ov = *(const float2 *)(&so[ww][g][2 * dp]);
+        ls = fmaf(wt, sl[ww][g], ls);
+        o0 = fmaf(wt, ov.x, o0);
+        o1 = fmaf(wt, ov.y, o1);
       }
-      st_act<true>(pp + 2 + t, sred[g][0][t] + sred[g][1][t]);
+      float *pp = a.part + ((int64_t)(kh * group + g) * a.nsmax + split) * (HD + 2);
+      if (dp == 0) {
+        st_act<true>(pp, M);
+        st_act<true>(pp + 1, ls);
+      }
+      st_act<true>(pp + 2 + 2 * dp, o0);
+      st_act<true>(pp + 3 + 2 * dp, o1);
     }
   }
   // the split holding position pos writes the new k / v into the cache
   // (issued late: an outstanding store would hold up every vmcnt wait above)
-  if (split == nsplit - 1 && lo) {
-    st_act<COH>(a.ck + ((int64_t)kh * a.cap + pos) * HD + t, skn[t]);
-    st_act<COH>(a.cv + ((int64_t)kh * a.cap + pos) * HD + t, xv);
+  if (split == nsplit - 1 && t < HD) {
+    a.ck[((int64_t)kh * a.cap + pos) * HD + t] = skn[t];
+    a.cv[((int64_t)kh * a.cap + pos) * HD + t] = svn[t];
   }
 }
 
 // Merges the nsplit partials of KV head kh into out (every query head of the
-// group), one memory round trip for up to 16 splits: each thread (head g,
-// dim) loads its dimension of the splits while the splits' (max, sum) go to
-// LDS; then the weights exp(m_s - M) and the sums.  Whole workgroup.
-template <int HD, bool COH>
+// group).  Each thread (head g, dim) loads the (max, sum, o[dim]) of 16
+// splits at once (one memory round trip for caches up to 16 * kDecKS; the
+// (max, sum) addresses are the same across the head's threads) and forms
+// the weights exp(m_s - M) itself, so no barrier is needed; longer caches
+// take further batches of 16, rescaling what is summed so far to the new
+// maximum.  Whole workgroup.
+template <int HD>
 __device__ void dec_attn_merge(const DecAttnArgs &a, int pos, int kh) {
-  __shared__ float sw[kDecMaxGroup][kDecMaxSplits], sls[kDecMaxGroup][kDecMaxSplits];
-  __shared__ float sden[kDecMaxGroup];
   const int group = a.nh / a.kvh, t = threadIdx.x;
   const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
   const float *pg = a.part + (int64_t)kh * group * a.nsmax * (HD + 2);
-  const int gt = t / HD, dt = t % HD;  // this thread's (head, dim) while gt < group
-  const float *p0 = pg + (int64_t)(gt < group ? gt : 0) * a.nsmax * (HD + 2) + 2 + dt;
-  float v[16];
-#pragma unroll
-  for (int u = 0; u < 16; u++) {
-    const int s2 = u < nsplit ? u : nsplit - 1;
-    v[u] = ld_act<true>(p0 + (int64_t)s2 * (HD + 2));
-  }
-  for (int i = t; i < group * nsplit; i += 256) {
-    const int g = i / nsplit, s2 = i % nsplit;
-    const float *pp = pg + ((int64_t)g * a.nsmax + s2) * (HD + 2);
-    sw[g][s2] = ld_act<true>(pp);
-    sls[g][s2] = ld_act<true>(pp + 1);
-  }
-  __syncthreads();
-  if (t < group) {
-    float M = -INFINITY;
-    for (int s2 = 0; s2 < nsplit; s2++) M = fmaxf(M, sw[t][s2]);
-    float den = 0.0f;
-    for (int s2 = 0; s2 < nsplit; s2++) {
-      const float wgt = expf(sw[t][s2] - M);
-      sw[t][s2] = wgt;
-      den = fmaf(wgt, sls[t][s2], den);
-    }
-    sden[t] = den;
-  }
-  __syncthreads();
-  // pairs past the first 256 (group * HD > 256) and splits past the first
-  // 16 (caches longer than 512) load again
   for (int i = t; i < group * HD; i += 256) {
     const int gi = i / HD, di = i % HD;
-    const float *pi0 = pg + (int64_t)gi * a.nsmax * (HD + 2) + 2 + di;
-    float num = 0.0f;
+    const float *ph = pg + (int64_t)gi * a.nsmax * (HD + 2);
+    float M = -INFINITY, den = 0.0f, num = 0.0f;
     for (int s0 = 0; s0 < nsplit; s0 += 16) {
-      if (i != t || s0 != 0) {
+      float mv[16], lv[16], ov[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-          const int s2 = s0 + u < nsplit ? s0 + u : nsplit - 1;
-          v[u] = ld_act<true>(pi0 + (int64_t)s2 * (HD + 2));
-        }
+      for (int u = 0; u < 16; u++) {
+        const float *pp = ph + (int64_t)min(s0 + u, nsplit - 1) * (HD + 2);
+        mv[u] = ld_act<true>(pp);
+        lv[u] = ld_act<true>(pp + 1);
+        ov[u] = ld_act<true>(pp + 2 + di);
       }
+      // every split has a key at or before pos, so its max is finite
+      float Mb = M;
 #pragma unroll
       for (int u = 0; u < 16; u++)
-        if (s0 + u < nsplit) num = fmaf(sw[gi][s0 + u], v[u], num);
+        if (s0 + u < nsplit) Mb = fmaxf(Mb, mv[u]);
+      const float c = expf(M - Mb);  // 0 on the first batch
+      den *= c;
+      num *= c;
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        if (s0 + u < nsplit) {
+          const float wgt = expf(mv[u] - Mb);
+          den = fmaf(wgt, lv[u], den);
+          num = fmaf(wgt, ov[u], num);
+        }
+      }
+      M = Mb;
     }
-    st_act<COH>(a.out + (kh * group + gi) * HD + di, num / sden[gi]);
+    a.out[(kh * group + gi) * HD + di] = num / den;
   }
-  __syncthreads();  // the LDS above may be reused by the caller's next item
 }
 
 // Launch form: grid (splits, KV heads); the last split of a KV head to
@@ -944,20 +963,23 @@ __global__ __launch_bounds__(256) void k_dec_attn(const DecState *__restrict__ s
   const int pos = st->pos;
   const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
   if (split >= nsplit) return;  // whole workgroup
-  dec_attn_partial<HD, false>(a, pos, split, kh);
+  dec_attn_partial<HD>(a, pos, split, kh);
   // ---- publish: the barrier orders every thread's partial stores before
-  // thread 0's count; its release (agent scope) pairs with the last split's
-  // acquire, and that workgroup's barrier extends it to the merge's loads.
+  // thread 0's count; its release (agent scope) pairs with the acquire fence
+  // of the last split, which reads the count the others' releases wrote, and
+  // that workgroup's barrier extends it to the merge's loads.  Only the last
+  // split acquires (an agent-scope acquire invalidates this XCD's L2).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev =
-        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&counters[kh], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == nsplit - 1;
+    if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!s_last) return;
-  dec_attn_merge<HD, false>(a, pos, kh);
+  dec_attn_merge<HD>(a, pos, kh);
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -1438,14 +1438,17 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     }
     // Ordering: the workgroup barrier orders every thread's partial stores
     // before thread 0's count, whose release (agent scope) pairs with the
-    // acquire of the last slice's count, which the barrier below extends to
-    // that workgroup's loads.
+    // acquire fence of the last slice (which read the count the others'
+    // releases wrote); the barrier below extends it to that workgroup's
+    // loads.  Only the last slice acquires (an agent-scope acquire
+    // invalidates this XCD's L2).
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
       const int prev =
-          __hip_atomic_fetch_add(&tile_cnt[tile], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(&tile_cnt[tile], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       s_last = prev == ksplit - 1;
+      if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!s_last) return;  // whole workgroup

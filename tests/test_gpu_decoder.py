@@ -276,10 +276,19 @@ SMALL = G.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64,
                         intermediate=512, vocab=1000, block=64, max_len=64)
 QWEN_HEADS = G.DecoderConfig(layers=2, hidden=1024, heads=16, kv_heads=8, head_dim=128,
                              intermediate=3072, vocab=2048, block=128, max_len=96)
+# four query heads per KV head, head sizes 32 and 96; the first decodes past
+# 16 splits of 32 keys (the decode attention's merge then takes its partials
+# in two batches)
+LONG_G4 = G.DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=2, head_dim=32,
+                          intermediate=512, vocab=500, block=64, max_len=640)
+HD96_G4 = G.DecoderConfig(layers=1, hidden=256, heads=4, kv_heads=1, head_dim=96,
+                          intermediate=512, vocab=500, block=64, max_len=64)
 
 
-@pytest.mark.parametrize("cfg,prompt_len,steps", [(SMALL, 20, 12), (QWEN_HEADS, 48, 8)],
-                         ids=["small", "qwen_heads"])
+@pytest.mark.parametrize("cfg,prompt_len,steps",
+                         [(SMALL, 20, 12), (QWEN_HEADS, 48, 8), (LONG_G4, 600, 8),
+                          (HD96_G4, 30, 6)],
+                         ids=["small", "qwen_heads", "long_cache_group4_hd32", "hd96_group4"])
 def test_decoder_vs_oracle(ctx, cfg, prompt_len, steps):
     w = G.random_weights(cfg, seed=5)
     rng = np.random.default_rng(9)
