@@ -882,29 +882,41 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
 // perm = {0,4,1,5,2,6,3,7} (the order the weight dequantisation produces).
 // Rows >= M and k >= K are zero.
 //
-// One launch: a workgroup owns kPrepRows consecutive rows (so each store
-// fills a contiguous run of a unit: lanes rl .. rl+kPrepRows-1), finds each
-// row's maximum over K, then converts.  Thread t covers k = 16t .. 16t+15 of
-// every 4096-k chunk (one 16-k step: both 8-k halves); the first chunk stays
-// in registers between the two passes, so K <= 4096 reads A once.
+// One launch.  A 128-byte line of a unit holds one half (16 B) of 8
+// consecutive rows, so rows go in groups of 8 whose lines one XCD writes,
+// and its L2 merges the 16-byte pieces of a line before write-back: a
+// workgroup owns half a group (4 rows), and workgroups b and b + 8 of each
+// 16 take the two halves (workgroups are dealt to the 8 XCDs round robin,
+// so both land on one XCD; the mapping only matters for speed).  Two waves
+// per row, each covering half of every 4096-k chunk; lane l reads 8
+// consecutive k (two float4) at 8 l + 512 i, i = 0..3, so a load instruction
+// covers 2 KB of the row.  The row's maximum over K (first chunk kept in
+// registers, so K <= 4096 reads A once), then the conversion.  Measured
+// against one workgroup of 8 rows (fewer, wider workgroups: 11.3 against
+// 8.2 us at M = 512) and the earlier 2-row workgroups with 16-k lanes
+// (same at M <= 512, 21.5 against 17.5 us at M = 2048, K = 4096).
 // ---------------------------------------------------------------------------
-constexpr int kPrepRows = 2;
+constexpr int kPrepRows = 4;
+constexpr int kPrepChunk = 4096;  // k per pass of a row's two waves
 
-__global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int64_t lda,
-                                                int64_t M, int64_t K, int64_t segsp,
-                                                int *__restrict__ row_exp,
-                                                uint4 *__restrict__ out,
-                                                int *__restrict__ clear, int nclear) {
+__global__ __launch_bounds__(128 * kPrepRows) void k_prep_a(
+    const float *__restrict__ A, int64_t lda, int64_t M, int64_t K, int64_t segsp,
+    int *__restrict__ row_exp, uint4 *__restrict__ out, int *__restrict__ clear, int nclear) {
   // the GEMM's K-slice counters when they live in a caller's workspace:
   // zeroed here, before the GEMM (the next launch on the stream) counts in
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i < nclear; i += blockDim.x) clear[i] = 0;
-  __shared__ float wmax[kPrepRows][4];
+  __shared__ float wmax[kPrepRows][2];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int64_t r0 = (int64_t)blockIdx.x * kPrepRows;
+  const int r = wave >> 1, hk = wave & 1;
+  const int b = blockIdx.x;
+  const int64_t r0 = b / 16 < (int)gridDim.x / 16
+                         ? (int64_t)(b / 16 * 8 + b % 8) * 8 + 4 * ((b / 8) & 1)
+                         : (int64_t)b * 4;
+  const int64_t row = r0 + r;
   const int64_t kp = segsp * kSegK;  // padded K
   const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
-  auto load8 = [&](int64_t row, int64_t k0, float *v) {
+  auto load8 = [&](int64_t k0, float *v) {
     const float *ar = A + row * lda + k0;
     if (row < M && vec && k0 + 8 <= K) {
       const float4 x0 = *(const float4 *)ar;
@@ -916,59 +928,55 @@ __global__ __launch_bounds__(256) void k_prep_a(const float *__restrict__ A, int
       for (int e = 0; e < 8; e++) v[e] = (row < M && k0 + e < K) ? ar[e] : 0.0f;
     }
   };
-  // ---- row maxima (first chunk kept)
-  float keep[kPrepRows][16];
-  float mx[kPrepRows];
+  const int kl = (kPrepChunk / 2) * hk + 8 * lane;  // + 512 i within a chunk
+  // ---- the row's maximum (first chunk kept)
+  float keep[4][8];
 #pragma unroll
-  for (int r = 0; r < kPrepRows; r++) {
-    load8(r0 + r, 16 * t, &keep[r][0]);
-    load8(r0 + r, 16 * t + 8, &keep[r][8]);
-  }
+  for (int i = 0; i < 4; i++) load8(kl + 512 * i, keep[i]);
+  float mx = 0.0f;
 #pragma unroll
-  for (int r = 0; r < kPrepRows; r++) {
-    mx[r] = 0.0f;
+  for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int e = 0; e < 16; e++) mx[r] = fmaxf(mx[r], fabsf(keep[r][e]));
-    for (int64_t k0 = 16 * t + 4096; k0 < K; k0 += 4096) {
-      float v[16];
-      load8(r0 + r, k0, &v[0]);
-      load8(r0 + r, k0 + 8, &v[8]);
+    for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(keep[i][e]));
+  for (int64_t k0 = kPrepChunk; k0 < K; k0 += kPrepChunk) {
 #pragma unroll
-      for (int e = 0; e < 16; e++) mx[r] = fmaxf(mx[r], fabsf(v[e]));
+    for (int i = 0; i < 4; i++) {
+      float v[8];
+      load8(k0 + kl + 512 * i, v);
+#pragma unroll
+      for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[e]));
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off, 64));
-    if (lane == 0) wmax[r][wave] = mx[r];
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) wmax[r][hk] = mx;
   __syncthreads();
-  int ex[kPrepRows];
+  const int ex = prep_a_exponent(fmaxf(wmax[r][0], wmax[r][1]));
+  if (t == 128 * r && row < M) row_exp[row] = ex;
+  // ---- convert: 8 k (one half of a 16-k step) per lane and i
+  for (int64_t k0 = 0; k0 < kp; k0 += kPrepChunk) {
 #pragma unroll
-  for (int r = 0; r < kPrepRows; r++) {
-    const float m_ = fmaxf(fmaxf(wmax[r][0], wmax[r][1]), fmaxf(wmax[r][2], wmax[r][3]));
-    ex[r] = prep_a_exponent(m_);
-    if (t == 0 && r0 + r < M) row_exp[r0 + r] = ex[r];
-  }
-  // ---- convert: thread t writes, per 4096-k chunk, step j = t%4 of segment
-  // s = chunk*64 + t/4, both halves g, both parts, for its rows
-  for (int64_t k0 = 16 * t; k0 < kp; k0 += 4096) {
-    float v[kPrepRows][16];
+    for (int i = 0; i < 4; i++) {
+      const int64_t kk = k0 + kl + 512 * i;
+      if (kk < kp) {  // kp is a multiple of 64: the 8 k lie inside
+        float v[8];
+        if (k0 == 0) {
 #pragma unroll
-    for (int r = 0; r < kPrepRows; r++) {
-      if (k0 < 4096) {
-#pragma unroll
-        for (int e = 0; e < 16; e++) v[r][e] = keep[r][e];
-      } else {
-        load8(r0 + r, k0, &v[r][0]);
-        load8(r0 + r, k0 + 8, &v[r][8]);
+          for (int e = 0; e < 8; e++) v[e] = keep[i][e];
+        } else {
+          load8(kk, v);
+        }
+        prep_a_store8(out, segsp, row, kk & ~(int64_t)15, (int)((kk >> 3) & 1), v, ex);
       }
     }
-    // the rows' pieces of one half are adjacent (rl, rl+1): store them
-    // back to back
-#pragma unroll
-    for (int g = 0; g < 2; g++)
-#pragma unroll
-      for (int r = 0; r < kPrepRows; r++) prep_a_store8(out, segsp, r0 + r, k0, g, &v[r][8 * g], ex[r]);
   }
+}
+
+static int launch_prep_a(mmnb_ctx *ctx, const float *d_a, int64_t lda, int64_t m, int64_t k,
+                         int64_t mpad, int64_t segsp, int *d_exp, uint4 *d_ap, int *clear,
+                         int nclear) {
+  return launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(mpad / kPrepRows)),
+                dim3(128 * kPrepRows), 0, d_a, lda, m, k, segsp, d_exp, d_ap, clear, nclear);
 }
 
 // ---------------------------------------------------------------------------
@@ -1613,9 +1621,8 @@ static int launch_gemm(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
   if ((rc = scratch_get(ctx, 2, pl.ap_bytes, &d_ap))) return rc;
   if ((rc = scratch_get(ctx, 3, (size_t)pl.mpad * 4, &d_exp))) return rc;
   if ((rc = gemm_ctx_part(ctx, pl, &d_part))) return rc;
-  if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(pl.mpad / kPrepRows)), dim3(256), 0,
-                    d_a, lda, m, p->k, pl.segsp, (int *)d_exp, (uint4 *)d_ap, (int *)nullptr,
-                    0)))
+  if ((rc = launch_prep_a(ctx, d_a, lda, m, p->k, pl.mpad, pl.segsp, (int *)d_exp,
+                           (uint4 *)d_ap, nullptr, 0)))
     return rc;
   return gemm_run(ctx, p, m, pl, d_ap, d_exp, d_y, d_part, ctx->d_gemm_cnt);
 }
@@ -1671,9 +1678,8 @@ int launch_matmul_nbits_ws(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, 
   char *b = (char *)ws;
   int *d_cnt = (int *)(b + o_cnt);
   const int nclear = pl.ksplit > 1 ? (int)pl.tiles : 0;
-  if ((rc = launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(pl.mpad / kPrepRows)), dim3(256), 0,
-                    d_a, lda, m, p->k, pl.segsp, (int *)(b + o_exp), (uint4 *)(b + o_ap), d_cnt,
-                    nclear)))
+  if ((rc = launch_prep_a(ctx, d_a, lda, m, p->k, pl.mpad, pl.segsp, (int *)(b + o_exp),
+                           (uint4 *)(b + o_ap), d_cnt, nclear)))
     return rc;
   return gemm_run(ctx, p, m, pl, b + o_ap, b + o_exp, d_y,
                   pl.ksplit > 1 ? (void *)(b + o_part) : nullptr, d_cnt);
