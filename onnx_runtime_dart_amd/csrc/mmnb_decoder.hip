@@ -1201,7 +1201,7 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
   d->cfg = c;
   d->layers.resize((size_t)c.layers);
   d->lm = lm_head;
-  d->nkeys = dec_gemv_blocks(ctx, c.vocab);
+  d->nkeys = dec_gemv_blocks(ctx, c.vocab, c.hidden);
   const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim,
                 I = c.intermediate, Lmax = c.max_len;
   const int64_t QKV = (nh + 2 * kvh) * hd;
@@ -1223,7 +1223,7 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
       (rc = A((size_t)(nh * nsplit * (hd + 2)) * 4, (void **)&d->part)) ||
       (rc = A((size_t)kvh * 4, (void **)&d->counters)) ||
       (rc = A(sizeof(DecState), (void **)&d->state)) ||
-      (rc = A((size_t)dec_gemv_blocks(ctx, c.vocab) * 8, (void **)&d->keys)) ||
+      (rc = A((size_t)dec_gemv_blocks(ctx, c.vocab, c.hidden) * 8, (void **)&d->keys)) ||
       (rc = A((size_t)Lmax * 4, (void **)&d->out_tokens)) ||
       (rc = A((size_t)Lmax * 8, (void **)&d->tok))) {
     mmnb_decoder_free(d);

@@ -228,12 +228,12 @@ inline int set_device(mmnb_ctx *ctx) {
 //   kDecSwiglu:  columns are gate/up interleaved, y[j] = silu(v[2j]) * v[2j+1];
 //   kDecArgmax:  y[n] = v and workgroup b stores d_argmax[b] = the greatest
 //                (orderable value << 32 | ~index) key of its columns, for
-//                dec_gemv_blocks(ctx, n) workgroups.
+//                dec_gemv_blocks(ctx, n, k) workgroups.
 enum DecEpilogue { kDecPlain = 0, kDecResidual = 1, kDecSwiglu = 2, kDecArgmax = 3 };
 int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
                     const float *norm_gamma, float eps, int epi, const float *resid,
                     float *d_y, unsigned long long *d_argmax);
-int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n);
+int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n, int64_t k);
 
 // Builds a 4-bit MatMulNBits pack (lock held): b_q [n, ceil(k/bs), bs/2]
 // bytes, scales fp32 [n * ceil(k/bs)], zp packed uint4 with the flat index

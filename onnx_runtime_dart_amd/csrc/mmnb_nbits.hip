@@ -472,14 +472,21 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   }
 }
 
-static int dec_gemv_r(const mmnb_ctx *ctx, int64_t n) {
+// Columns per wave half R: the largest that keeps two waves per SIMD slot
+// of the chip (workgroups x waves >= 2 x CUs; nw waves split K).  Measured
+// on the Qwen3-0.6B decode step: o and down (N = 1024, 2-3 waves) at R = 2
+// and q|k|v, gate/up (N = 4096, 6144, one wave) at R = 4 beat every other
+// pairing by 0.8-4%.
+static int dec_gemv_r(const mmnb_ctx *ctx, int64_t n, int nw) {
   int R = 8;
-  while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  while (R > 1 && (n + 2 * R - 1) / (2 * R) * nw < 2 * (int64_t)ctx->cu_count) R >>= 1;
   return R;
 }
 
-int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n) {
-  const int R = dec_gemv_r(ctx, n);
+static int dec_gemv_waves(int64_t k) { return (int)((k / 32 + 31) / 32); }
+
+int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n, int64_t k) {
+  const int R = dec_gemv_r(ctx, n, dec_gemv_waves(k));
   return (n + 2 * R - 1) / (2 * R);
 }
 
@@ -493,7 +500,7 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
   const int C = (int)(p->col_bytes / 16);
   const int nw = (C + 31) / 32;
   const int64_t n = p->n;
-  const int R = dec_gemv_r(ctx, n);
+  const int R = dec_gemv_r(ctx, n, dec_gemv_waves(p->k));
   const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
   const dim3 block((unsigned)(64 * nw));
   const int bs_log2 = ilog2(p->block);
