@@ -38,6 +38,34 @@ __device__ __forceinline__ float half_wave_sum(float v) {
   return v + __builtin_bit_cast(float, o);
 }
 
+// The 32 activations of a GEMV chunk -- k = base + 16 j + e, j = 0..3,
+// e = 0..7, ar pointing at k = base -- into every lane of a wave whose two
+// halves (lanes l and l + 32, h = l / 32) work on the same chunk: each half
+// loads two of the four 8-float runs (h = 0 runs 0 and 1, h = 1 runs 2 and 3)
+// and v_permlane32_swap hands each half the other's, so the wave issues half
+// the load instructions for the same values.  Every lane must take part
+// (full exec mask).
+__device__ __forceinline__ void load_chunk32_paired(const float *ar, int h, float *av) {
+  float part[16];
+  const float *ah = ar + 32 * h;
+#pragma unroll
+  for (int jj = 0; jj < 2; jj++) {
+    const float4 x0 = *(const float4 *)(ah + 16 * jj);
+    const float4 x1 = *(const float4 *)(ah + 16 * jj + 4);
+    part[8 * jj + 0] = x0.x; part[8 * jj + 1] = x0.y; part[8 * jj + 2] = x0.z;
+    part[8 * jj + 3] = x0.w; part[8 * jj + 4] = x1.x; part[8 * jj + 5] = x1.y;
+    part[8 * jj + 6] = x1.z; part[8 * jj + 7] = x1.w;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const unsigned u = __builtin_bit_cast(unsigned, part[e]);
+    // [0]: lanes 0-31's value in every lane, [1]: lanes 32-63's
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    av[e] = __builtin_bit_cast(float, (unsigned)sw[0]);
+    av[16 + e] = __builtin_bit_cast(float, (unsigned)sw[1]);
+  }
+}
+
 // ---- Exact weight dequantisation for the fp32 FMA kernels.
 //
 // A weight dword w holds 8 nibbles q_e (e = 0..7; byte b holds e = 2b in its

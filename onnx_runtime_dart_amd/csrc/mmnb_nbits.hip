@@ -164,7 +164,10 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, int zp, uint32_t magic) 
 // j = 0..3, nibble e = 0..7.  A workgroup owns 2R columns and all of K:
 //   wave w, lane l: half h = l/32 picks one column of each pair, t = l%32;
 //   the lane owns chunk c = 32w + t (+ 32 nw per extra iteration) of the R
-//   columns 2r + h, r = 0..R-1.
+//   columns 2r + h, r = 0..R-1.  Both halves need the same activations: each
+//   loads half of them and a lane swap completes the other half
+//   (load_chunk32_paired; against every lane loading all 32, the headline
+//   K = N = 4096 call went from 4.69 to 4.59 us).
 // Up to 4 waves split K (one pass covers K <= 4096; longer K iterates:
 // 16-wave workgroups covering K = 16384 in one pass measured 20% slower).
 // Per iteration a lane issues all of its loads -- its 32 activations, the scales (and zero
@@ -215,13 +218,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     const float *ar = A + s * kSegK + 8 * g;
     if constexpr (FAST) {
       // rows hold k64 values: every 8-float run of a chunk is inside the row
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float4 x0 = *(const float4 *)(ar + 16 * j);
-        const float4 x1 = *(const float4 *)(ar + 16 * j + 4);
-        av[8 * j + 0] = x0.x; av[8 * j + 1] = x0.y; av[8 * j + 2] = x0.z; av[8 * j + 3] = x0.w;
-        av[8 * j + 4] = x1.x; av[8 * j + 5] = x1.y; av[8 * j + 6] = x1.z; av[8 * j + 7] = x1.w;
-      }
+      load_chunk32_paired(ar, h, av);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -364,26 +361,8 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   const int s = cc >> 1, g = cc & 1;
   // ---- loads: activations (and gamma), scales, then weights
   float av[32], gv[32];
-  {
-    const float *xr = X + s * kSegK + 8 * g;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float4 x0 = *(const float4 *)(xr + 16 * j);
-      const float4 x1 = *(const float4 *)(xr + 16 * j + 4);
-      av[8 * j + 0] = x0.x; av[8 * j + 1] = x0.y; av[8 * j + 2] = x0.z; av[8 * j + 3] = x0.w;
-      av[8 * j + 4] = x1.x; av[8 * j + 5] = x1.y; av[8 * j + 6] = x1.z; av[8 * j + 7] = x1.w;
-    }
-    if constexpr (NORM) {
-      const float *gr = gamma + s * kSegK + 8 * g;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float4 x0 = *(const float4 *)(gr + 16 * j);
-        const float4 x1 = *(const float4 *)(gr + 16 * j + 4);
-        gv[8 * j + 0] = x0.x; gv[8 * j + 1] = x0.y; gv[8 * j + 2] = x0.z; gv[8 * j + 3] = x0.w;
-        gv[8 * j + 4] = x1.x; gv[8 * j + 5] = x1.y; gv[8 * j + 6] = x1.z; gv[8 * j + 7] = x1.w;
-      }
-    }
-  }
+  load_chunk32_paired(X + s * kSegK + 8 * g, h, av);
+  if constexpr (NORM) load_chunk32_paired(gamma + s * kSegK + 8 * g, h, gv);
   const int blk = (s * kSegK) >> bs_log2;
   float sraw[R];
 #pragma unroll
