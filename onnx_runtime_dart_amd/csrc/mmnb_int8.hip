@@ -565,8 +565,11 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 
 // MatMulInteger with LDS staging by direct global->LDS DMA
 // (global_load_lds_dwordx4, 16 B per lane, no VGPR round trip).  Workgroup
-// tile TM x 64 (TM = 64 or 32), 4 waves in 2 x 2, wave tile (TM/2) x 32 of
-// 16 x 16 MFMA tiles, K steps of 64 as k_mmi_mfma.  K moves in chunks of
+// tile TM x TN, WM x (TN/32) waves, wave tile (TM/WM) x 32 of 16 x 16 MFMA
+// tiles, K steps of 64 as k_mmi_mfma.  The launcher uses 32 x 64 and 64 x 64
+// on 2 x 2 waves; 64 x 128 on 4 x 4 or 2 x 4 waves, 32 x 128, 64 x 64 on 4 x 2
+// and 128 x 64 were all parity-green and 1-10% slower at [512,1024] x
+// [1024,3072].  K moves in chunks of
 // kMmiKc bytes through a two-slot ring: the next chunk is in flight while the
 // current one is multiplied (every thread issues the same number of DMA
 // loads per chunk, so "chunk c has landed" is vmcnt <= that number while
@@ -583,31 +586,34 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 constexpr int kMmiKc = 256;
 constexpr int kMmiPieces = kMmiKc / 16;  // per row
 
-template <bool LDS_EPI, int TM>
-__global__ __launch_bounds__(256) void k_mmi_lds(
+template <bool LDS_EPI, int TM, int TN, int WM>
+__global__ __launch_bounds__(64 * WM * (TN / 32)) void k_mmi_lds(
     const uint8_t *__restrict__ A, int a_signed, int64_t a_bstride, int64_t M, int64_t K,
     const int8_t *__restrict__ Bt, int64_t b_bstride, int64_t kpad,
     const int32_t *__restrict__ colsum, int64_t cs_bstride, const int32_t *__restrict__ ecol,
     int64_t N, const int32_t *__restrict__ azp, int64_t azp_len, MmiEpi o,
     const uint8_t *__restrict__ pad) {
-  constexpr int TI = TM / 32;                      // 16-row blocks per wave
+  constexpr int WN = TN / 32;                      // waves across the tile's columns
+  constexpr int NW = WM * WN;                      // waves per workgroup
+  constexpr int TI = TM / (16 * WM);               // 16-row blocks per wave
   constexpr int kSA = TM * kMmiPieces;             // uint4 per A slot
-  constexpr int kSB = 64 * kMmiPieces;             // uint4 per B slot
-  constexpr int kLoads = (kSA + kSB) / 64 / 4;     // DMA loads per thread per chunk
-  static_assert((kSA / 64) % 4 == 0 && (kSB / 64) % 4 == 0, "whole DMA rounds per wave");
+  constexpr int kSB = TN * kMmiPieces;             // uint4 per B slot
+  constexpr int kLoads = (kSA + kSB) / 64 / NW;    // DMA loads per thread per chunk
+  static_assert(TI >= 1 && TM == 16 * TI * WM, "wave rows");
+  static_assert((kSA / 64) % NW == 0 && (kSB / 64) % NW == 0, "whole DMA rounds per wave");
   // one array: the A ring (two slots of kSA) then the B ring (two of kSB),
   // which the LDS epilogue reuses whole
   __shared__ uint4 smem[2 * (kSA + kSB)];
   uint4 *sA0 = smem, *sB0 = smem + 2 * kSA;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int64_t bz = blockIdx.z;
   const uint8_t *Ab = A + bz * a_bstride;
   const int8_t *Bb = Bt + bz * b_bstride;
-  const int64_t m0 = (int64_t)blockIdx.y * TM + wm * (TM / 2);
-  const int64_t n0 = (int64_t)blockIdx.x * 64 + wn * 32;
-  const int64_t mt0 = (int64_t)blockIdx.y * TM, nt0 = (int64_t)blockIdx.x * 64;
+  const int64_t m0 = (int64_t)blockIdx.y * TM + wm * (16 * TI);
+  const int64_t n0 = (int64_t)blockIdx.x * TN + wn * 32;
+  const int64_t mt0 = (int64_t)blockIdx.y * TM, nt0 = (int64_t)blockIdx.x * TN;
   const int r16 = lane & 15, q = lane >> 4;
   const uint32_t flip = a_signed ? 0u : 0x80808080u;
   const uint8_t *apad = pad + (a_signed ? 0 : 1024);
@@ -618,8 +624,8 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
   auto issue = [&](int c, int s) {
     const int64_t k0 = (int64_t)c * kMmiKc;
 #pragma unroll
-    for (int u = 0; u < kSA / 64 / 4; u++) {
-      const int i = wave + 4 * u;
+    for (int u = 0; u < kSA / 64 / NW; u++) {
+      const int i = wave + NW * u;
       const int slot = i * 64 + lane;
       const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
       const int64_t kk = k0 + (int64_t)(cs_ ^ (r & 15)) * 16;
@@ -628,8 +634,8 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
       dma16(ga, sA0 + s * kSA + i * 64);
     }
 #pragma unroll
-    for (int u = 0; u < kSB / 64 / 4; u++) {
-      const int i = wave + 4 * u;
+    for (int u = 0; u < kSB / 64 / NW; u++) {
+      const int i = wave + NW * u;
       const int slot = i * 64 + lane;
       const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
       const int64_t kk = k0 + (int64_t)(cs_ ^ (r & 15)) * 16;
@@ -668,7 +674,7 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
       int4v av[TI], bv[2];
 #pragma unroll
       for (int t = 0; t < TI; t++) {
-        const int ra = wm * (TM / 2) + t * 16 + r16;
+        const int ra = wm * (16 * TI) + t * 16 + r16;
         const uint4 x = sA[ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
         uint32_t w[4] = {x.x ^ flip, x.y ^ flip, x.z ^ flip, x.w ^ flip};
 #pragma unroll
@@ -694,7 +700,7 @@ __global__ __launch_bounds__(256) void k_mmi_lds(
     }
   }
   if constexpr (LDS_EPI) {
-    static_assert(4 * 2 * 16 * TI * 33 * 4 <= (int)sizeof(smem), "epilogue tiles fit the ring");
+    static_assert(NW * 2 * 16 * TI * 33 * 4 <= (int)sizeof(smem), "epilogue tiles fit the ring");
     __syncthreads();  // the ring is free: it holds the output tiles now
     mmi_epilogue_lds<TI>(acc, rsum, ein, a_signed, bz, M, K, N, m0, n0, lane, azp_len, o,
                          (uint32_t *)smem + wave * 2 * 16 * TI * 33);
@@ -720,10 +726,10 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
     const int64_t tiles64 = (int64_t)grid.x * grid.y * grid.z;
     const int tm = ctx->mmi_tm ? ctx->mmi_tm : (tiles64 < 3 * (int64_t)ctx->cu_count ? 32 : 64);
     const bool le = !o.yq && !o.trans;
-    auto kern = le ? k_mmi_lds<true, 64> : k_mmi_lds<false, 64>;
+    auto kern = le ? k_mmi_lds<true, 64, 64, 2> : k_mmi_lds<false, 64, 64, 2>;
     dim3 g = grid;
     if (tm == 32) {
-      kern = le ? k_mmi_lds<true, 32> : k_mmi_lds<false, 32>;
+      kern = le ? k_mmi_lds<true, 32, 64, 2> : k_mmi_lds<false, 32, 64, 2>;
       g.y = (unsigned)((m + 31) / 32);
     }
     return launch(ctx, kKernMmi, kern, g, dim3(256), 0, (const uint8_t *)d_a, a_signed,
