@@ -458,10 +458,13 @@ def test_decoder_full_size_properties(ctx, full_weights):
         toks = dec.decode(64)
         last = dec.logits()
         assert np.all(np.isfinite(last))
-        # rerun: identical greedy tokens
+        # rerun: identical greedy tokens and the same logits to the bit (the
+        # decode attention's cross-workgroup merge and the prefill GEMM's K
+        # slices sum in a fixed order)
         dec.reset()
         assert dec.prefill(prompt) == t0
         np.testing.assert_array_equal(dec.decode(64), toks)
+        np.testing.assert_array_equal(dec.logits().view(np.uint32), last.view(np.uint32))
         # the last step saw prompt + [t0] + toks[:63]; a prefill of that
         # sequence (GEMM path, row attention) must give the same logits
         dec.reset()
