@@ -620,12 +620,23 @@ struct DecState {
 
 __global__ __launch_bounds__(256) void k_dec_begin(DecState *__restrict__ st,
                                                    const float *__restrict__ table, int64_t H,
-                                                   int64_t vocab, float *__restrict__ x) {
+                                                   int64_t vocab, float *__restrict__ x,
+                                                   const float *__restrict__ cos,
+                                                   const float *__restrict__ sin, int half,
+                                                   int rows, float *__restrict__ rot) {
   // the token comes from the previous step's argmax, always in range; the
   // clamp only keeps a corrupted state from reading outside the table
   int64_t tok = st->token;
   tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
   for (int64_t k = threadIdx.x; k < H; k += blockDim.x) x[k] = table[tok * H + k];
+  // the step's rotary row (cos | sin at pos), so that the attention's loads
+  // do not wait for the position
+  int pos = st->pos;
+  pos = pos < 0 ? 0 : (pos >= rows ? rows - 1 : pos);
+  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    rot[i] = cos[(int64_t)pos * half + i];
+    rot[half + i] = sin[(int64_t)pos * half + i];
+  }
 }
 
 // Greedy token: the maximum of the lm_head workgroups' keys (one workgroup).
@@ -718,7 +729,7 @@ struct DecAttnArgs {
   int nh, kvh;
   const float *qn, *kn;
   float eps;
-  const float *cos, *sin;
+  const float *rot;  // cos | sin of the step's position (HD/2 each)
   float *ck, *cv;
   int64_t cap;
   float scale;
@@ -734,7 +745,7 @@ struct DecAttnArgs {
 // holding pos also writes the new k / v into the cache.  Whole workgroup,
 // 256 threads (4 waves).
 template <int HD>
-__device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int kh) {
+__device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, int kh) {
   constexpr int kDpk = HD / 8;  // K dims per lane (a multiple of 4)
   constexpr int kHr = HD / 2;   // rotary half; norm lanes hold dims l, l + kHr
   __shared__ __align__(16) float sq[kDecMaxGroup][HD];
@@ -745,8 +756,6 @@ __device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int k
   const int nh = a.nh, kvh = a.kvh, group = nh / kvh;
   const int t = threadIdx.x, w = t >> 6, l = t & 63;
   const int jk = t >> 3, p8 = t & 7;  // K layout: key, dim slice
-  const int L = pos + 1;
-  const int nsplit = (L + kDecKS - 1) / kDecKS;
   const int j0 = split * kDecKS;
   const float *Kb = a.ck + (int64_t)kh * a.cap * HD;
   const float *Vb = a.cv + (int64_t)kh * a.cap * HD;
@@ -767,16 +776,17 @@ __device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int k
   }
   const int lv = 2 * l < HD ? l : 0;  // V layout: dims 2 lv, 2 lv + 1
   const float2 xv = *(const float2 *)(a.qkv + (nh + kvh + kh) * HD + 2 * lv);
-  const double cs = (double)a.cos[(int64_t)pos * kHr + lc];
-  const double sn = (double)a.sin[(int64_t)pos * kHr + lc];
+  const double cs = (double)a.rot[lc];
+  const double sn = (double)a.rot[kHr + lc];
   // the norm's loads go out first (a wait for one of them waits for every
   // load issued before it)
   __builtin_amdgcn_sched_barrier(0);
-  // K / V tile (rows >= pos are read from row 0 and replaced or dropped)
+  // K / V tile: addresses independent of pos (rows are clamped to the
+  // cache; rows >= pos are replaced or dropped below)
   float kreg[kDpk];
   {
     const int j = j0 + jk;
-    const float *kr = Kb + (int64_t)(j < pos ? j : 0) * HD + p8 * kDpk;
+    const float *kr = Kb + (int64_t)(j < a.cap ? j : a.cap - 1) * HD + p8 * kDpk;
 #pragma unroll
     for (int e = 0; e < kDpk; e += 4) {
       const float4 v4 = *(const float4 *)(kr + e);
@@ -790,7 +800,17 @@ __device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int k
 #pragma unroll
   for (int u = 0; u < kDecKW; u++) {
     const int j = j0 + w * kDecKW + u;
-    vreg[u] = *(const float2 *)(Vb + (int64_t)(j < pos ? j : 0) * HD + 2 * lv);
+    vreg[u] = *(const float2 *)(Vb + (int64_t)(j < a.cap ? j : a.cap - 1) * HD + 2 * lv);
+  }
+  // the position is first used here, after every load is out (a use
+  // before them would hold them until it arrives); splits past it leave
+  int pos = pos_in;
+  asm volatile("" : "+v"(pos));
+  const int L = pos + 1;
+  const int nsplit = (L + kDecKS - 1) / kDecKS;
+  if (split >= nsplit) {
+    asm volatile("" ::"v"(kreg[0]), "v"(vreg[0].x), "v"(x0[0]), "v"(xv.x));
+    return false;
   }
   // ---- per-head RMSNorm (double sums, wave-local) and rotary at pos
 #pragma unroll
@@ -904,6 +924,7 @@ __device__ void dec_attn_partial(const DecAttnArgs &a, int pos, int split, int k
     a.ck[((int64_t)kh * a.cap + pos) * HD + t] = skn[t];
     a.cv[((int64_t)kh * a.cap + pos) * HD + t] = svn[t];
   }
+  return true;
 }
 
 // Merges the nsplit partials of KV head kh into out (every query head of the
@@ -960,10 +981,14 @@ __global__ __launch_bounds__(256) void k_dec_attn(const DecState *__restrict__ s
                                                   DecAttnArgs a, int *counters) {
   __shared__ int s_last;
   const int split = blockIdx.x, kh = blockIdx.y;
-  const int pos = st->pos;
+  // the position through the vector memory path, used only once the
+  // partial's loads are out: a scalar load would join the kernel-argument
+  // loads' wait, in front of every other load
+  const int pos_v = __hip_atomic_load(const_cast<int *>(&st->pos), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+  if (!dec_attn_partial<HD>(a, pos_v, split, kh)) return;  // whole workgroup
+  const int pos = __builtin_amdgcn_readfirstlane(pos_v);
   const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
-  if (split >= nsplit) return;  // whole workgroup
-  dec_attn_partial<HD>(a, pos, split, kh);
   // ---- publish: the barrier orders every thread's partial stores before
   // thread 0's count; its release (agent scope) pairs with the acquire fence
   // of the last split, which reads the count the others' releases wrote, and
@@ -1133,6 +1158,7 @@ struct mmnb_decoder {
   float *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr,
         *gu = nullptr, *act = nullptr, *tmp = nullptr, *logits = nullptr;
   float *cache_k = nullptr, *cache_v = nullptr, *cos = nullptr, *sin = nullptr;
+  float *rot = nullptr;     // the decode step's rotary row: cos | sin, hd/2 each
   float *part = nullptr;    // attention partials [heads, splits, hd + 2]
   int *counters = nullptr;  // per KV head: attention splits finished
   DecState *state = nullptr;
@@ -1221,6 +1247,7 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
       (rc = A((size_t)(c.layers * kvh * Lmax * hd) * 4, (void **)&d->cache_k)) ||
       (rc = A((size_t)(c.layers * kvh * Lmax * hd) * 4, (void **)&d->cache_v)) ||
       (rc = A((size_t)(nh * nsplit * (hd + 2)) * 4, (void **)&d->part)) ||
+      (rc = A((size_t)hd * 4, (void **)&d->rot)) ||
       (rc = A((size_t)kvh * 4, (void **)&d->counters)) ||
       (rc = A(sizeof(DecState), (void **)&d->state)) ||
       (rc = A((size_t)dec_gemv_blocks(ctx, c.vocab, c.hidden) * 8, (void **)&d->keys)) ||
@@ -1429,8 +1456,8 @@ static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float 
   const dim3 grid((unsigned)((c.max_len + kDecKS - 1) / kDecKS), (unsigned)c.kv_heads);
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
   DecAttnArgs args{(const float *)d->qkv, (int)c.heads, (int)c.kv_heads, (const float *)L.qn,
-                   (const float *)L.kn, c.eps, (const float *)d->cos, (const float *)d->sin,
-                   ck, cv, c.max_len, scale, d->part, (int)grid.x, d->attn};
+                   (const float *)L.kn, c.eps, (const float *)d->rot, ck, cv, c.max_len, scale,
+                   d->part, (int)grid.x, d->attn};
 #define MMNB_DEC_ATTN(HD)                                                                      \
   launch(ctx, kKernDecAttn, k_dec_attn<HD>, grid, dim3(256), 0, (const DecState *)d->state,   \
          args, d->counters)
@@ -1451,7 +1478,8 @@ static int dec_record_step(mmnb_decoder *d) {
   const float eps = c.eps;
   int rc;
   if ((rc = launch(ctx, kKernDecOps, k_dec_begin, dim3(1), dim3(256), 0, d->state,
-                   (const float *)d->embed, H, c.vocab, d->x)))
+                   (const float *)d->embed, H, c.vocab, d->x, (const float *)d->cos,
+                   (const float *)d->sin, (int)(c.head_dim / 2), (int)Lmax, d->rot)))
     return rc;
   for (int64_t li = 0; li < c.layers; li++) {
     const mmnb_decoder::Layer &L = d->layers[(size_t)li];
