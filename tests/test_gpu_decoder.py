@@ -283,12 +283,18 @@ LONG_G4 = G.DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=2, head_dim=32
                           intermediate=512, vocab=500, block=64, max_len=640)
 HD96_G4 = G.DecoderConfig(layers=1, hidden=256, heads=4, kv_heads=1, head_dim=96,
                           intermediate=512, vocab=500, block=64, max_len=64)
+# one and three query heads per KV head
+MHA_G1 = G.DecoderConfig(layers=1, hidden=256, heads=4, kv_heads=4, head_dim=64,
+                         intermediate=512, vocab=500, block=64, max_len=80)
+G3 = G.DecoderConfig(layers=2, hidden=256, heads=6, kv_heads=2, head_dim=64,
+                     intermediate=512, vocab=500, block=64, max_len=80)
 
 
 @pytest.mark.parametrize("cfg,prompt_len,steps",
                          [(SMALL, 20, 12), (QWEN_HEADS, 48, 8), (LONG_G4, 600, 8),
-                          (HD96_G4, 30, 6)],
-                         ids=["small", "qwen_heads", "long_cache_group4_hd32", "hd96_group4"])
+                          (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
+                         ids=["small", "qwen_heads", "long_cache_group4_hd32", "hd96_group4",
+                              "mha_group1", "group3"])
 def test_decoder_vs_oracle(ctx, cfg, prompt_len, steps):
     w = G.random_weights(cfg, seed=5)
     rng = np.random.default_rng(9)
