@@ -100,6 +100,21 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
   __shared__ float2 s[kDqlThreads / 64];
   __shared__ float s_scale;
   __shared__ int s_zp;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)y) & 3) == 0);
+  const int64_t n4 = (vec && n >= 4) ? n >> 2 : 0;
+  const float4 *x4 = (const float4 *)x;
+  // the thread's first batch of x is loaded before the scale is known (it
+  // does not depend on it), so its round trip overlaps the partials' one
+  float4 v[kDqlUnroll];
+  if (n4 > 0) {  // workgroup-uniform
+#pragma unroll
+    for (int u = 0; u < kDqlUnroll; u++) {
+      const int64_t i = tid + u * stride;
+      v[u] = x4[i < n4 ? i : n4 - 1];
+    }
+  }
   float mn = 0.0f, mx = 0.0f;
   for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
     const float2 p = part[i];
@@ -136,22 +151,17 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
   __syncthreads();
   const float scale = s_scale;
   const int zp = s_zp;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)y) & 3) == 0);
-  int64_t done = 0;
-  if (vec && n >= 4) {
-    const int64_t n4 = n >> 2;
-    const float4 *x4 = (const float4 *)x;
+  if (n4 > 0) {
     uint32_t *y4 = (uint32_t *)y;
     // kDqlUnroll loads in flight per thread (clamped indices; only the
     // in-range results are stored)
     for (int64_t base = tid; base < n4; base += stride * kDqlUnroll) {
-      float4 v[kDqlUnroll];
+      if (base != tid) {
 #pragma unroll
-      for (int u = 0; u < kDqlUnroll; u++) {
-        const int64_t i = base + u * stride;
-        v[u] = x4[i < n4 ? i : n4 - 1];
+        for (int u = 0; u < kDqlUnroll; u++) {
+          const int64_t i = base + u * stride;
+          v[u] = x4[i < n4 ? i : n4 - 1];
+        }
       }
 #pragma unroll
       for (int u = 0; u < kDqlUnroll; u++) {
@@ -163,9 +173,8 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
         if (i < n4) y4[i] = b;
       }
     }
-    done = n4 << 2;
   }
-  for (int64_t i = done + tid; i < n; i += stride) y[i] = dql_q(x[i], scale, zp);
+  for (int64_t i = (n4 << 2) + tid; i < n; i += stride) y[i] = dql_q(x[i], scale, zp);
 }
 
 int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *d_scale,
