@@ -27,7 +27,10 @@ namespace mmnb {
 // ---------------------------------------------------------------------------
 constexpr int kDqlThreads = 256;
 constexpr int kDqlMaxBlocks = 1024;
-constexpr int kDqlUnroll = 4;  // 16-byte loads a thread issues before using any
+// 16-byte loads a thread issues before using any: 2 gives twice the
+// workgroups of 4 at the same bytes (at [512,1024] 512 against 256; the two
+// launches took 5.65 against 6.2 us, and 5.9 at 1, 7.6 at 8)
+constexpr int kDqlUnroll = 2;
 
 // Per-block min/max partials.  Each thread issues kDqlUnroll float4 loads
 // (indices clamped into range: a repeated element changes neither extreme)
