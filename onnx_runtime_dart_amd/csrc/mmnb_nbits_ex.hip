@@ -81,14 +81,20 @@ __global__ __launch_bounds__(256) void k_nbits_correct(float *__restrict__ Y, in
 
 // The same correction for few rows, with the block sums of row m formed in
 // LDS by the workgroup itself (one launch instead of two; every column
-// workgroup re-reads its row, which is cheap for M <= 8).
+// workgroup re-reads its row, which is cheap for M <= 8).  A workgroup takes
+// 64 columns; its 4 waves split the blocks (wave w: b = w, w + 4, ...) with
+// eight loads of corr in flight per lane, then add their partial sums in a
+// fixed order through LDS (a single chain over all blocks waited on every
+// load in turn).
 constexpr int kFusedMaxBlocks = 8192;
+constexpr int kCorrCols = 64;
 
 __global__ __launch_bounds__(256) void k_nbits_correct_rows(
     float *__restrict__ Y, int64_t N, const float *__restrict__ bias,
     const float *__restrict__ corr, int64_t nb, const float *__restrict__ A, int64_t lda,
     int64_t ka, int64_t bs) {
   __shared__ float sas[kFusedMaxBlocks];
+  __shared__ float spart[4][kCorrCols];
   const int64_t m = blockIdx.y;
   const int w = threadIdx.x >> 6, ln = threadIdx.x & 63;
   if (corr) {
@@ -101,12 +107,27 @@ __global__ __launch_bounds__(256) void k_nbits_correct_rows(
     }
     __syncthreads();
   }
-  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
-  float v = bias ? bias[n] : 0.0f;
-  if (corr)
-    for (int64_t b = 0; b < nb; b++) v = fmaf(corr[b * N + n], sas[b], v);
-  Y[m * N + n] += v;
+  const int64_t n = (int64_t)blockIdx.x * kCorrCols + ln;
+  const int64_t nc = n < N ? n : N - 1;
+  float v = 0.0f;
+  if (corr) {
+    int64_t b = w;
+    for (; b + 28 < nb; b += 32) {
+      float c[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) c[u] = corr[(b + 4 * u) * N + nc];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v = fmaf(c[u], sas[b + 4 * u], v);
+    }
+    for (; b < nb; b += 4) v = fmaf(corr[b * N + nc], sas[b], v);
+  }
+  spart[w][ln] = v;
+  __syncthreads();
+  if (w == 0 && n < N) {
+    float t = bias ? bias[n] : 0.0f;
+    t += ((spart[0][ln] + spart[1][ln]) + spart[2][ln]) + spart[3][ln];
+    Y[m * N + n] += t;
+  }
 }
 
 int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
@@ -130,7 +151,8 @@ int run_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_
   if ((rc = launch_matmul_nbits(ctx, p, a2, lda2, m, d_y))) return rc;
   if (m <= 8 && p->corr_nb <= kFusedMaxBlocks)
     return launch(ctx, kKernNbitsEx, k_nbits_correct_rows,
-                  dim3((unsigned)((p->n + 255) / 256), (unsigned)m), dim3(256), 0, d_y, p->n,
+                  dim3((unsigned)((p->n + kCorrCols - 1) / kCorrCols), (unsigned)m), dim3(256), 0,
+                  d_y, p->n,
                   (const float *)p->d_bias, (const float *)p->d_corr, p->corr_nb, a2, lda2, ka,
                   p->block);
   const float *d_asum = nullptr;
