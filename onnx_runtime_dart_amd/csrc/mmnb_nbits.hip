@@ -1038,6 +1038,10 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   const int tx = (L % per_group) / rows_in_group;
   const int rb0 = ty * 2;
   const int n0 = tx * kBN;
+  // the exponent of tile row `lane`, loaded now (it is ready long before the
+  // epilogue, which takes it from this lane by a shuffle instead of a memory
+  // round trip after the K loop)
+  const int rexp = row_exp[min(rb0 * 32 + lane, M - 1)];
 
   // DMA sources.  Activations: thread's unit pieces idx = tid + 256 i
   // (unit idx/64 = row block (idx/64)/8, step*2+part (idx/64)%8); the
@@ -1472,15 +1476,17 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   if (grp > 0) return;
   // 32x32 f32 accumulator layout: lane l holds column l%32, rows
   // (r/4)*8 + (l/32)*4 + r%4 for r = 0..15.
+  // (every lane takes part in the shuffles: the column test is on the store)
 #pragma unroll
   for (int cb = 0; cb < CB; cb++) {
-    if (!colok[cb]) continue;
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int row = (rb0 + rb) * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-        if (row < M) Y[(size_t)row * N + col[cb]] = ldexpf(acc[rb][cb][r], -row_exp[row]);
+        const int tr = rb * 32 + (r >> 2) * 8 + g * 4 + (r & 3);  // row in the tile
+        const int row = rb0 * 32 + tr;
+        const int ex = __shfl(rexp, tr, 64);
+        if (colok[cb] && row < M) Y[(size_t)row * N + col[cb]] = ldexpf(acc[rb][cb][r], -ex);
       }
     }
   }
