@@ -367,6 +367,11 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   float sraw[R];
 #pragma unroll
   for (int r = 0; r < R; r++) sraw[r] = S[colr[r] * nb + blk];
+  // the residual of output column col0 + thread, loaded with the rest (a
+  // load under the epilogue's column test would be a round trip of its own);
+  // only this workgroup writes those columns
+  float rres = 0.0f;
+  if constexpr (EPI == kDecResidual) rres = resid[min(col0 + (int)threadIdx.x, N - 1)];
   uint4 wv[R];
 #pragma unroll
   for (int r = 0; r < R; r++)
@@ -427,7 +432,7 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   if constexpr (EPI == kDecPlain) {
     if (i < 2 * R && col < N) Y[col] = v;
   } else if constexpr (EPI == kDecResidual) {
-    if (i < 2 * R && col < N) Y[col] = resid[col] + v;
+    if (i < 2 * R && col < N) Y[col] = rres + v;
   } else if constexpr (EPI == kDecSwiglu) {
     if (i < 2 * R) outv[i] = v;
     __syncthreads();
