@@ -104,29 +104,46 @@ __global__ __launch_bounds__(256) void k_rmsnorm_prep(const float *X, int64_t M,
   const int64_t r = blockIdx.x;
   const bool live = r < M;  // whole workgroup
   const int t = threadIdx.x;
+  const int64_t k0 = 16 * t;
+  // every load first (clamped indices): the row (thread t: k = t + 256 j),
+  // the residual, and the gammas of the conversion's k = 16t .. 16t+15
+  float xr[kPrepMaxDim / 256], ar[kPrepMaxDim / 256], gv[16];
+  const int64_t rr = live ? r : 0;
+#pragma unroll
+  for (int j = 0; j < kPrepMaxDim / 256; j++) {
+    const int64_t k = t + 256 * j;
+    const int64_t kc = k < dim ? k : dim - 1;
+    xr[j] = X[rr * dim + kc];
+    ar[j] = add ? add[rr * dim + kc] : 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; e++) gv[e] = G[k0 + e < dim ? k0 + e : dim - 1];
   double inv = 0.0;
   if (live) {
     double ss = 0.0;
-    for (int64_t k = t; k < dim; k += blockDim.x) {
-      float v = X[r * dim + k];
-      if (add) {
-        v = v + add[r * dim + k];
-        xsum[r * dim + k] = v;
+#pragma unroll
+    for (int j = 0; j < kPrepMaxDim / 256; j++) {
+      const int64_t k = t + 256 * j;
+      if (k < dim) {
+        float v = xr[j];
+        if (add) {
+          v = v + ar[j];
+          xsum[r * dim + k] = v;
+        }
+        srow[k] = v;
+        ss += (double)v * (double)v;
       }
-      srow[k] = v;
-      ss += (double)v * (double)v;
     }
     ss = block_sum_d(ss, sh);  // its barriers also publish srow
     inv = 1.0 / sqrt(ss / (double)dim + (double)eps);
   }
-  const int64_t k0 = 16 * t;
   float v[16];
   float mx = 0.0f;
 #pragma unroll
   for (int e = 0; e < 16; e++) {
     const int64_t k = k0 + e;
     const bool ok = live && k < dim;
-    const float gk = G[ok ? k : 0];
+    const float gk = gv[e];
     const float y = (float)((double)srow[k] * inv * (double)gk);
     v[e] = ok ? y : 0.0f;
     mx = fmaxf(mx, fabsf(v[e]));
