@@ -645,14 +645,29 @@ __global__ __launch_bounds__(256) void k_dec_begin(DecState *__restrict__ st,
   // clamp only keeps a corrupted state from reading outside the table
   int64_t tok = st->token;
   tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
-  for (int64_t k = threadIdx.x; k < H; k += blockDim.x) x[k] = table[tok * H + k];
-  // the step's rotary row (cos | sin at pos), so that the attention's loads
-  // do not wait for the position
+  // the step's rotary row (cos | sin at pos; half <= 64 < blockDim), so that
+  // the attention's loads do not wait for the position; loaded first
   int pos = st->pos;
   pos = pos < 0 ? 0 : (pos >= rows ? rows - 1 : pos);
-  for (int i = threadIdx.x; i < half; i += blockDim.x) {
-    rot[i] = cos[(int64_t)pos * half + i];
-    rot[half + i] = sin[(int64_t)pos * half + i];
+  const int ic = (int)threadIdx.x < half ? (int)threadIdx.x : 0;
+  const float cv = cos[(int64_t)pos * half + ic], sv = sin[(int64_t)pos * half + ic];
+  // four loads in flight per thread (a plain loop waited for each in turn)
+  for (int64_t k0 = threadIdx.x; k0 < H; k0 += 4 * (int64_t)blockDim.x) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int64_t k = k0 + u * (int64_t)blockDim.x;
+      v[u] = table[tok * H + (k < H ? k : H - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int64_t k = k0 + u * (int64_t)blockDim.x;
+      if (k < H) x[k] = v[u];
+    }
+  }
+  if ((int)threadIdx.x < half) {
+    rot[threadIdx.x] = cv;
+    rot[half + threadIdx.x] = sv;
   }
 }
 
@@ -662,8 +677,20 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
                                                   int nkeys, int32_t *__restrict__ out_tokens,
                                                   int out_cap) {
   __shared__ unsigned long long sk[16];
+  const int step = st->step, pos = st->pos;  // read now, not after the reduction
   unsigned long long best = 0ull;
-  for (int i = threadIdx.x; i < nkeys; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+  // eight keys in flight per thread (clamped: a repeated key leaves the
+  // maximum alone); a plain loop waited for every key in turn
+  for (int i0 = threadIdx.x; i0 < nkeys; i0 += 8 * (int)blockDim.x) {
+    unsigned long long k8[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = i0 + u * (int)blockDim.x;
+      k8[u] = keys[i < nkeys ? i : nkeys - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) best = k8[u] > best ? k8[u] : best;
+  }
   for (int off = 32; off > 0; off >>= 1) {
     const unsigned long long o = __shfl_xor(best, off, 64);
     best = o > best ? o : best;
@@ -676,9 +703,9 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
     st->argmax = key;
     const int tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
     st->token = tok;
-    if (st->step >= 0 && st->step < out_cap) out_tokens[st->step] = tok;
-    st->step += 1;
-    st->pos += 1;
+    if (step >= 0 && step < out_cap) out_tokens[step] = tok;
+    st->step = step + 1;
+    st->pos = pos + 1;
   }
 }
 

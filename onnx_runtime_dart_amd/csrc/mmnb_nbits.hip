@@ -1456,23 +1456,30 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     __syncthreads();
     if (!s_last) return;  // whole workgroup
     if (grp == 0) {
-      // one round trip per slice: all of a slice's values, then the adds
-      for (int sl = 0; sl < ksplit; sl++) {
-        float t[2][CB][16];
-        const float *q = pt + (size_t)sl * kPart + tid;
+      // one round trip per two slices (ksplit is even): both slices' values,
+      // then the adds in slice order
+      for (int sl = 0; sl < ksplit; sl += 2) {
+        float t[2][2][CB][16];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const float *q = pt + (size_t)(sl + h) * kPart + tid;
+#pragma unroll
+          for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int cb = 0; cb < CB; cb++)
+#pragma unroll
+              for (int r = 0; r < 16; r++)
+                t[h][rb][cb][r] = ld_act<true>(q + ((rb * CB + cb) * 16 + r) * 256);
+        }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)
 #pragma unroll
           for (int cb = 0; cb < CB; cb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) t[rb][cb][r] = ld_act<true>(q + ((rb * CB + cb) * 16 + r) * 256);
-#pragma unroll
-        for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-          for (int cb = 0; cb < CB; cb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-              acc[rb][cb][r] = sl == 0 ? t[rb][cb][r] : acc[rb][cb][r] + t[rb][cb][r];
+            for (int r = 0; r < 16; r++) {
+              const float a = sl == 0 ? t[0][rb][cb][r] : acc[rb][cb][r] + t[0][rb][cb][r];
+              acc[rb][cb][r] = a + t[1][rb][cb][r];
+            }
       }
     }
     if (threadIdx.x == 0)
