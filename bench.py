@@ -255,7 +255,10 @@ def bench_qlinear(ctx, lib, ops, reps=200):
     """QLinearMatMul at the int8 chain's shape ([512,1024] u8 x [1024,3072]
     i8 -> u8) and a ResNet-50 layer-1 3x3 convolution (1x64x56x56 u8,
     64x64x3x3 i8, pad 1) as ConvInteger (int32 out) and QLinearConv
-    (per-channel scales, bias, u8 out).  Kernel times from dispatch events."""
+    (per-channel scales, bias, u8 out).  Kernel times from dispatch events
+    (each includes the dispatch's own start-up, ~4 us for an empty kernel);
+    QLinearMatMul and ConvInteger also back to back in graphs of 20 calls
+    (QLinearConv uploads its per-channel parameters and is not captured)."""
     out = {}
     rng = np.random.default_rng(7)
     m, k, n = 512, 1024, 3072
@@ -277,6 +280,7 @@ def bench_qlinear(ctx, lib, ops, reps=200):
     nbytes = m * k + k * n + m * n
     out["qlinear_matmul"] = {
         "m": m, "k": k, "n": n, "kernels_us": per, "us_per_call": tot,
+        "back_to_back_us": _graph_us(ctx, qmm, 50, 5),
         "gbs": nbytes / (tot * 1e-6) / 1e9, "hbm_frac": nbytes / (tot * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "tops": 2.0 * m * k * n / (tot * 1e-6) / 1e12}
     for bf in (da, dz, dq):
@@ -317,6 +321,8 @@ def bench_qlinear(ctx, lib, ops, reps=200):
         out[name] = {"shape": "x 1x64x56x56 u8, w 64x64x3x3 i8, pad 1", "kernels_us": per,
                      "us_per_call": tot, "tops": ops_ / (tot * 1e-6) / 1e12,
                      "gbs": nbytes / (tot * 1e-6) / 1e9}
+        if fn is conv:
+            out[name]["back_to_back_us"] = _graph_us(ctx, conv, 50, 5)
     for bf in (dx, dy32, dy8):
         bf.free()
     cp.free()

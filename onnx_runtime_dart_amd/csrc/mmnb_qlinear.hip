@@ -21,25 +21,43 @@ using namespace mmnb;
 namespace mmnb {
 
 // One image: x [C][H][W] bytes -> out [groups][oh*ow][cg*kh*kw].  Grid
-// (output positions, 256-wide chunks of a row, groups); 32-bit index
-// arithmetic (the host checks the sizes); the source index is clamped so
-// every load is in bounds.
+// (items / 256, groups); 32-bit index arithmetic (the host checks that
+// groups * oh*ow * cg*kh*kw fits); the source index is clamped so every load
+// is in bounds.
 __global__ __launch_bounds__(256) void k_im2col(const uint8_t *__restrict__ x, int H, int W,
                                                 int cg, int kh, int kw, int ow, int sh, int sw,
                                                 int ph, int pw, int dh, int dw, uint32_t zp,
-                                                uint8_t *__restrict__ out) {
-  const int kcn = cg * kh * kw;
-  const int kc = blockIdx.y * blockDim.x + threadIdx.x;
-  if (kc >= kcn) return;
-  const int p = blockIdx.x, g = blockIdx.z;
-  const int khw = kh * kw;
-  const int c = kc / khw, r = kc - c * khw;
-  const int ky = r / kw, kx = r - ky * kw;
+                                                int items, int per, uint8_t *__restrict__ out) {
+  // the group's output [P][kcn] is contiguous: thread item i owns bytes
+  // per*i .. per*i + per - 1 of it (per = 4 when kcn % 4 == 0, one 32-bit
+  // store; else 1), all of whose source bytes are loaded before any store
+  const unsigned item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= (unsigned)items) return;
+  const int g = blockIdx.y;
+  const int kcn = cg * kh * kw, khw = kh * kw;
+  const int e0 = (int)item * per;
+  const int p = e0 / kcn, kc0 = e0 - p * kcn;
   const int oy = p / ow, ox = p - oy * ow;
-  const int iy = oy * sh - ph + ky * dh, ix = ox * sw - pw + kx * dw;
-  const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W;
-  const uint8_t v = x[((size_t)(g * cg + c) * H + (in ? iy : 0)) * W + (in ? ix : 0)];
-  out[((size_t)g * gridDim.x + p) * kcn + kc] = in ? v : (uint8_t)zp;
+  uint32_t v[4];
+  bool in[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int kc = kc0 + (u < per ? u : 0);
+    const int c = kc / khw, r = kc - c * khw;
+    const int ky = r / kw, kx = r - ky * kw;
+    const int iy = oy * sh - ph + ky * dh, ix = ox * sw - pw + kx * dw;
+    in[u] = iy >= 0 && iy < H && ix >= 0 && ix < W;
+    v[u] = x[((size_t)(g * cg + c) * H + (in[u] ? iy : 0)) * W + (in[u] ? ix : 0)];
+  }
+  uint8_t *o = out + (size_t)g * items * per + e0;
+  if (per == 4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) word |= (in[u] ? v[u] : zp) << (8 * u);
+    *(uint32_t *)o = word;
+  } else {
+    o[0] = (uint8_t)(in[0] ? v[0] : zp);
+  }
 }
 
 }  // namespace mmnb
@@ -106,12 +124,16 @@ int conv_run(mmnb_ctx *ctx, const mmnb_pack *p, const uint8_t *d_x, int x_signed
   o.azp_is_const = 1;
   o.azp_const = (int32_t)x_zp;
   const uint32_t zbyte = (uint32_t)(x_zp & 0xFF);
-  const dim3 grid((unsigned)P, (unsigned)((kcn + 255) / 256), (unsigned)g);
+  // 4 bytes per thread when the rows are whole dwords (the scratch buffer
+  // is 256-byte aligned, so then every dword is aligned)
+  const int per = kcn % 4 == 0 ? 4 : 1;
+  const int items = (int)(P * kcn / per);
+  const dim3 grid((unsigned)((items + 255) / 256), (unsigned)g);
   for (int64_t b = 0; b < s.n; b++) {
     const uint8_t *xb = d_x + b * s.c * s.h * s.w;
     if ((rc = launch(ctx, kKernIm2col, k_im2col, grid, dim3(256), 0, xb, (int)s.h, (int)s.w,
                      (int)p->conv_cg, (int)p->conv_kh, (int)p->conv_kw, (int)s.ow, s.sh, s.sw,
-                     s.ph, s.pw, s.dh, s.dw, zbyte, (uint8_t *)d_col)))
+                     s.ph, s.pw, s.dh, s.dw, zbyte, items, per, (uint8_t *)d_col)))
       return rc;
     MmiEpi ob = o;
     ob.trans = 1;

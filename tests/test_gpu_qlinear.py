@@ -74,6 +74,9 @@ CONV = [
     (1, 6, 7, 6, 6, 1, 3, 3, [1, 2], [0, 0, 0, 0], [1, 1], False, False),
     (1, 16, 12, 12, 32, 3, 3, 1, [1, 1], [1, 1, 1, 1], [1, 1], False, True),  # K = 144
     (3, 32, 9, 9, 64, 1, 1, 2, [1, 1], [0, 0, 0, 0], [1, 1], False, True),    # K = 16
+    (1, 64, 20, 23, 16, 3, 3, 1, [1, 1], [1, 1, 1, 1], [1, 1], False, True),  # K = 576
+    (1, 8, 15, 31, 8, 3, 3, 2, [2, 2], [1, 2, 1, 0], [1, 1], True, True),
+    (1, 512, 4, 30, 8, 3, 3, 1, [1, 1], [0, 0, 0, 0], [1, 12], False, True),  # K = 4608
 ]
 
 
