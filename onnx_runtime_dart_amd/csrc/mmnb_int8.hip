@@ -299,6 +299,8 @@ int prepare_integer_b(mmnb_ctx *ctx, const uint8_t *d_src, int b_signed, int b_t
 }
 
 typedef int int4v __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Epilogue operands of one lane: A's zero point for each of its 8 rows, and
 // per column (2 of them) the pack's zero-point terms, the fp32 rescale's B
@@ -477,8 +479,12 @@ __device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[TI][2], int 
     if (row >= M) continue;
     const int64_t base = (bz * M + row) * N + n0 + sc0;
     if (vec) {
-      if (o.y) *(uint4 *)(o.y + base) = make_uint4(v[0], v[1], v[2], v[3]);
-      if (o.yf) *(float4 *)(o.yf + base) = make_float4(f[0], f[1], f[2], f[3]);
+      // non-temporal: the outputs are not read again by this kernel (at
+      // [512,1024] x [1024,3072] the kernel went from 8.98 to 8.51 us)
+      if (o.y)
+        __builtin_nontemporal_store((u32x4){v[0], v[1], v[2], v[3]}, (u32x4 *)(o.y + base));
+      if (o.yf)
+        __builtin_nontemporal_store((f32x4){f[0], f[1], f[2], f[3]}, (f32x4 *)(o.yf + base));
     } else {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
@@ -763,7 +769,6 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
 // independent 16-byte non-temporal loads per thread (bounds-checked) whose
 // xor is kept live by a never-taken store.
 // ---------------------------------------------------------------------------
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void k_probe_empty(int *sink, unsigned key) {
   if (threadIdx.x == key) sink[0] = 1;  // key is out of range: never stores
 }
