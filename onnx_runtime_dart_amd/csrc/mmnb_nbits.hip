@@ -854,10 +854,14 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
     iters = (nw + kGemvMaxWaves - 1) / kGemvMaxWaves;
     nw = (C + 32 * iters - 1) / (32 * iters);
   }
-  // columns per workgroup 2R: as many as keep >= 2 workgroups per CU
+  // columns per workgroup 2R.  Timed over R = 1, 2, 4, 8 at (K, N) =
+  // (1024, 1024 / 2048 / 6144), (2048, 2048), (3072, 1024), (4096, 4096),
+  // (4096, 14336), (14336, 4096), (8192, 8192), (16384, 16384) and
+  // (1024, 151936): R = 2 was best up to 8.4 MB of packed weights (within 3%
+  // of R = 1 at (2048, 2048)), R = 4 from 29 MB up (every workgroup reads the
+  // whole activation row from L2, so more workgroups cost more there)
   const int64_t n = p->n;
-  int R = 8;
-  while (R > 1 && (n + 2 * R - 1) / (2 * R) < 2 * (int64_t)ctx->cu_count) R >>= 1;
+  int R = p->col_bytes * n > ((int64_t)16 << 20) ? 4 : 2;
   if (ctx->gemv_r > 0) R = ctx->gemv_r;  // tuning override
   const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
   const dim3 block((unsigned)(64 * nw));
