@@ -355,6 +355,23 @@ __device__ __forceinline__ void mmi_epi_load(MmiEpiIn &in, int64_t bz, int64_t M
   }
 }
 
+// 8-bit requantisation of one exact accumulator v (QLinearMatMul /
+// QLinearConv): mode 1 rounds v * mult through binary32 as the reference's
+// float path does, otherwise (v + bias) * mult_ch in double; then round half
+// to even, add the output zero point and saturate.
+__device__ __forceinline__ uint32_t mmi_requant(uint32_t v, double mch, double bias,
+                                                const MmiEpi &o) {
+  double x;
+  if (o.rq_mode == 1) {
+    x = (double)(float)((double)(int32_t)v * (double)o.rq_mult);
+  } else {
+    x = ((double)(int32_t)v + bias) * mch;
+  }
+  double t = rint(x) + (double)o.yzp;
+  t = t < (double)o.lo ? (double)o.lo : (t > (double)o.hi ? (double)o.hi : t);
+  return (uint32_t)(uint8_t)(int32_t)t;
+}
+
 // Epilogue shared by both MatMulInteger kernels: completes the row sums,
 // applies the exact integer zero-point corrections and stores what `o` asks
 // for (int32, the fused fp32 rescale, 8-bit requantisation).  16x16 i32
@@ -399,17 +416,7 @@ __device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[TI][2], int (&rs
         const int64_t oi = o.trans ? (bz * N + col) * M + row[r] : (bz * M + row[r]) * N + col;
         if (o.y) o.y[oi] = (int32_t)v;
         if (o.yf) o.yf[oi] = (float)(int32_t)v * sj;
-        if (o.yq) {
-          double x;
-          if (o.rq_mode == 1) {
-            x = (double)(float)((double)(int32_t)v * (double)o.rq_mult);
-          } else {
-            x = ((double)(int32_t)v + bias) * mch;
-          }
-          double t = rint(x) + (double)o.yzp;
-          t = t < (double)o.lo ? (double)o.lo : (t > (double)o.hi ? (double)o.hi : t);
-          o.yq[oi] = (uint8_t)(int32_t)t;
-        }
+        if (o.yq) o.yq[oi] = (uint8_t)mmi_requant(v, mch, bias, o);
       }
     }
   }
@@ -420,8 +427,10 @@ __device__ __forceinline__ void mmi_epilogue(const int4v (&acc)[TI][2], int (&rs
 // parked in `tiles` (two (16 TI) x 33 arrays: int32 and fp32; 4224 TI bytes
 // per wave) and stored back as 16 bytes per lane, 8 full 128-byte rows per
 // instruction (the MFMA layout would write 64-byte row pieces 16 columns
-// wide).  The caller's LDS must be free of other readers (a barrier after
-// the K loop).
+// wide).  With the 8-bit output (only: the launcher sends y / yf with yq
+// to mmi_epilogue) the requantised bytes go through the int32 tile and each
+// lane stores 8 of them.  The caller's LDS must be free of other readers (a
+// barrier after the K loop).
 template <int TI = 2>
 __device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[TI][2], int (&rsum)[TI],
                                                  const MmiEpiIn &ein, int a_signed, int64_t bz,
@@ -449,18 +458,47 @@ __device__ __forceinline__ void mmi_epilogue_lds(const int4v (&acc)[TI][2], int 
     for (int j = 0; j < 2; j++) {
       const uint32_t e = (uint32_t)ein.e[j], csum = (uint32_t)ein.cs[j];
       const float sj = ein.as * ein.bs[j];
+      const double mch = ein.mch[j], bias = (double)ein.bias[j];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const uint32_t c = (uint32_t)cm[r];
         const uint32_t v = (uint32_t)acc[i][j][r] + e * (uint32_t)rs[r] + c * csum +
                            (uint32_t)K * c * e;
         const int at = (i * 16 + q * 4 + r) * 33 + j * 16 + r16;
-        ti[at] = v;
-        tf[at] = (float)(int32_t)v * sj;
+        if (o.yq) {
+          ti[at] = mmi_requant(v, mch, bias, o);
+        } else {
+          ti[at] = v;
+          tf[at] = (float)(int32_t)v * sj;
+        }
       }
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS writes, read back by its own lanes
+  if (o.yq) {
+    // lane l -> row 16 pass + l/4, columns 8 (l % 4) .. +7
+    const int c8 = (lane & 3) * 8;
+    const bool vq = n0 + 32 <= N && (N & 7) == 0 && (((uintptr_t)o.yq) & 7) == 0;
+#pragma unroll
+    for (int pass = 0; pass < TI; pass++) {
+      const int rr = pass * 16 + (lane >> 2);
+      const int64_t row = m0 + rr;
+      uint32_t b[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) b[u] = ti[rr * 33 + c8 + u];
+      if (row >= M) continue;
+      const int64_t base = (bz * M + row) * N + n0 + c8;
+      if (vq) {
+        *(uint2 *)(o.yq + base) = make_uint2(b[0] | b[1] << 8 | b[2] << 16 | b[3] << 24,
+                                             b[4] | b[5] << 8 | b[6] << 16 | b[7] << 24);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+          if (n0 + c8 + u < N) o.yq[base + u] = (uint8_t)b[u];
+      }
+    }
+    return;
+  }
   // ---- stores: lane l -> row 8 pass + l/8, columns 4 (l % 8) .. +3
   const int sc0 = (lane & 7) * 4;
   const bool vec = n0 + 32 <= N && (N & 3) == 0 &&
@@ -743,7 +781,8 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
     // per CU (tuning override: MMNB_MMI_TM)
     const int64_t tiles64 = (int64_t)grid.x * grid.y * grid.z;
     const int tm = ctx->mmi_tm ? ctx->mmi_tm : (tiles64 < 3 * (int64_t)ctx->cu_count ? 32 : 64);
-    const bool le = !o.yq && !o.trans;
+    // the LDS epilogue: row-major outputs, the 8-bit one only on its own
+    const bool le = !o.trans && (!o.yq || (!o.y && !o.yf));
     auto kern = le ? k_mmi_lds<true, 64, 64, 2> : k_mmi_lds<false, 64, 64, 2>;
     dim3 g = grid;
     if (tm == 32) {
