@@ -895,35 +895,34 @@ static int launch_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int6
 // One launch.  A 128-byte line of a unit holds one half (16 B) of 8
 // consecutive rows, so rows go in groups of 8 whose lines one XCD writes,
 // and its L2 merges the 16-byte pieces of a line before write-back: a
-// workgroup owns half a group (4 rows), and workgroups b and b + 8 of each
-// 16 take the two halves (workgroups are dealt to the 8 XCDs round robin,
-// so both land on one XCD; the mapping only matters for speed).  Two waves
-// per row, each covering half of every 4096-k chunk; lane l reads 8
-// consecutive k (two float4) at 8 l + 512 i, i = 0..3, so a load instruction
-// covers 2 KB of the row.  The row's maximum over K (first chunk kept in
+// workgroup owns one row, and the 8 workgroups of a group are b, b + 8, ...,
+// b + 56 of each 64 (workgroups are dealt to the 8 XCDs round robin, so all
+// 8 land on one XCD; the mapping only matters for speed).  Eight waves per
+// row, each covering 512 k of every 4096-k chunk; lane l reads 8 consecutive
+// k (two float4) at 8 l.  The row's maximum over K (first chunk kept in
 // registers, so K <= 4096 reads A once), then the conversion.  Measured
-// against one workgroup of 8 rows (fewer, wider workgroups: 11.3 against
-// 8.2 us at M = 512) and the earlier 2-row workgroups with 16-k lanes
-// (same at M <= 512, 21.5 against 17.5 us at M = 2048, K = 4096).
+// against 4 rows per workgroup with two waves per row (K = N = 4096, bs32 +
+// zp, prep per call 6.8 / 7.3 / 8.7 / 18.6 us at M = 128 / 256 / 512 / 2048,
+// against 5.0 / 5.7 / 7.2 / 16.6 us here; 2 rows with four waves per row
+// fell in between), one workgroup of 8 rows (11.3 against 8.2 us at M = 512)
+// and 2-row workgroups with 16-k lanes (21.5 against 17.5 us at M = 2048).
 // ---------------------------------------------------------------------------
-constexpr int kPrepRows = 4;
-constexpr int kPrepChunk = 4096;  // k per pass of a row's two waves
+constexpr int kPrepWaves = 8;     // waves per row (one row per workgroup)
+constexpr int kPrepChunk = 4096;  // k per pass of a row's waves
 
-__global__ __launch_bounds__(128 * kPrepRows) void k_prep_a(
+__global__ __launch_bounds__(64 * kPrepWaves) void k_prep_a(
     const float *__restrict__ A, int64_t lda, int64_t M, int64_t K, int64_t segsp,
     int *__restrict__ row_exp, uint4 *__restrict__ out, int *__restrict__ clear, int nclear) {
   // the GEMM's K-slice counters when they live in a caller's workspace:
   // zeroed here, before the GEMM (the next launch on the stream) counts in
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i < nclear; i += blockDim.x) clear[i] = 0;
-  __shared__ float wmax[kPrepRows][2];
+  __shared__ float wmax[kPrepWaves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int r = wave >> 1, hk = wave & 1;
   const int b = blockIdx.x;
-  const int64_t r0 = b / 16 < (int)gridDim.x / 16
-                         ? (int64_t)(b / 16 * 8 + b % 8) * 8 + 4 * ((b / 8) & 1)
-                         : (int64_t)b * 4;
-  const int64_t row = r0 + r;
+  const int64_t row = b / 64 < (int)gridDim.x / 64
+                          ? (int64_t)(b / 64 * 8 + b % 8) * 8 + (b % 64) / 8
+                          : (int64_t)b;
   const int64_t kp = segsp * kSegK;  // padded K
   const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
   auto load8 = [&](int64_t k0, float *v) {
@@ -938,46 +937,50 @@ __global__ __launch_bounds__(128 * kPrepRows) void k_prep_a(
       for (int e = 0; e < 8; e++) v[e] = (row < M && k0 + e < K) ? ar[e] : 0.0f;
     }
   };
-  const int kl = (kPrepChunk / 2) * hk + 8 * lane;  // + 512 i within a chunk
+  const int kl = (kPrepChunk / kPrepWaves) * wave + 8 * lane;
   // ---- the row's maximum (first chunk kept)
-  float keep[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; i++) load8(kl + 512 * i, keep[i]);
+  float keep[8];
+  load8(kl, keep);
   float mx = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(keep[e]));
+  int64_t k0 = kPrepChunk;
+  for (; k0 + 3 * kPrepChunk < K; k0 += 4 * kPrepChunk) {  // four loads in flight
+    float v[4][8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(keep[i][e]));
-  for (int64_t k0 = kPrepChunk; k0 < K; k0 += kPrepChunk) {
+    for (int u = 0; u < 4; u++) load8(k0 + u * kPrepChunk + kl, v[u]);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float v[8];
-      load8(k0 + kl + 512 * i, v);
+    for (int u = 0; u < 4; u++)
 #pragma unroll
-      for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[e]));
-    }
+      for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[u][e]));
+  }
+  for (; k0 < K; k0 += kPrepChunk) {
+    float v[8];
+    load8(k0 + kl, v);
+#pragma unroll
+    for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[e]));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (lane == 0) wmax[r][hk] = mx;
+  if (lane == 0) wmax[wave] = mx;
   __syncthreads();
-  const int ex = prep_a_exponent(fmaxf(wmax[r][0], wmax[r][1]));
-  if (t == 128 * r && row < M) row_exp[row] = ex;
-  // ---- convert: 8 k (one half of a 16-k step) per lane and i
+  float rm = wmax[0];
+#pragma unroll
+  for (int w = 1; w < kPrepWaves; w++) rm = fmaxf(rm, wmax[w]);
+  const int ex = prep_a_exponent(rm);
+  if (t == 0 && row < M) row_exp[row] = ex;
+  // ---- convert: 8 k (one half of a 16-k step) per lane and chunk
   for (int64_t k0 = 0; k0 < kp; k0 += kPrepChunk) {
+    const int64_t kk = k0 + kl;
+    if (kk < kp) {  // kp is a multiple of 64: the 8 k lie inside
+      float v[8];
+      if (k0 == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int64_t kk = k0 + kl + 512 * i;
-      if (kk < kp) {  // kp is a multiple of 64: the 8 k lie inside
-        float v[8];
-        if (k0 == 0) {
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = keep[i][e];
-        } else {
-          load8(kk, v);
-        }
-        prep_a_store8(out, segsp, row, kk & ~(int64_t)15, (int)((kk >> 3) & 1), v, ex);
+        for (int e = 0; e < 8; e++) v[e] = keep[e];
+      } else {
+        load8(kk, v);
       }
+      prep_a_store8(out, segsp, row, kk & ~(int64_t)15, (int)((kk >> 3) & 1), v, ex);
     }
   }
 }
@@ -985,8 +988,8 @@ __global__ __launch_bounds__(128 * kPrepRows) void k_prep_a(
 static int launch_prep_a(mmnb_ctx *ctx, const float *d_a, int64_t lda, int64_t m, int64_t k,
                          int64_t mpad, int64_t segsp, int *d_exp, uint4 *d_ap, int *clear,
                          int nclear) {
-  return launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)(mpad / kPrepRows)),
-                dim3(128 * kPrepRows), 0, d_a, lda, m, k, segsp, d_exp, d_ap, clear, nclear);
+  return launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)mpad), dim3(64 * kPrepWaves), 0, d_a,
+                lda, m, k, segsp, d_exp, d_ap, clear, nclear);
 }
 
 // ---------------------------------------------------------------------------
