@@ -48,6 +48,9 @@ MFMA_FP16_PEAK_TFLOPS = 2500.0
 MFMA_FP32_PEAK_TFLOPS = 157.3
 INT8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 320 * 1024 * 1024
+HOST_CPU_SHARE = 16  # host cores the GPU box allots to one GPU's jobs
+TRAFFIC_SOURCE = ("committed rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) of the same "
+                  "workload, profiles/traffic.json; not measured in this run")
 
 
 def mmnb_bytes(m, k, n, bs, zp):
@@ -68,13 +71,17 @@ def make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed):
     return packs
 
 
-def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup, min_calls=32):
+def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup, min_calls=32, min_dispatches=200):
     """One step = one call on each pack.  Each HIP graph holds enough whole
     steps for at least min_calls calls (one step for the headline's 38
     packs), so the gap between graph launches is amortised like the gap
     between kernels; `steps` steps are timed (rounded up to whole graphs).
-    Returns (timed steps, ms per step, ms per call, dispatch-event kernel
-    durations per name)."""
+    Then two eager passes with start/end timestamps taken by each dispatch
+    (the per-kernel durations a kernel tracer reports): `queued`, at least
+    min_dispatches calls enqueued without waiting, and `isolated`,
+    min_dispatches calls each launched after the previous one finished.
+    Returns (timed steps, ms per step, ms per call, queued, isolated), the
+    last two as {kernel: per-dispatch durations in ms}."""
     P = len(packs)
     per_graph = max(1, -(-min_calls // P))  # steps per graph
 
@@ -100,43 +107,64 @@ def time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup, min_calls=32):
     ctx.synchronize()
     total_ms = ctx.event_elapsed_ms(0, 1)
     ctx.graph_destroy(g)
-    # per-dispatch event durations, for reference (they include a fixed
-    # dispatch cost that back-to-back launches do not pay)
-    nk = min(steps * P, 2048)
+    # eager pass: one dispatch per call, each timed by its own start/end
+    # timestamps (these include a fixed per-dispatch cost that back-to-back
+    # graph launches do not pay)
+    nk = max(min_dispatches, min(steps * P, 2048))
     ctx.kernel_timing(True, max_launches=4 * nk)
     done = 0
     while done < nk:
         issue_round()
         done += P
     kt = ctx.kernel_timing_read()
+    queued = {name: ctx.kernel_timing_samples(name) for name in kt}
     ctx.kernel_timing(False)
-    return steps, total_ms / steps, total_ms / (steps * P), kt
+    # isolated pass: each call launched on an idle GPU (the host waits for the
+    # previous one to finish), the regime a kernel tracer puts every dispatch in
+    ctx.kernel_timing(True, max_launches=4 * min_dispatches)
+    for i in range(min_dispatches):
+        lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, packs[i % P].handle, da.ptr, m,
+                                                dy.ptr))
+        ctx.synchronize()
+    kt = ctx.kernel_timing_read()
+    isolated = {name: ctx.kernel_timing_samples(name) for name in kt}
+    ctx.kernel_timing(False)
+    return steps, total_ms / steps, total_ms / (steps * P), queued, isolated
 
 
-def kernel_avg_ms(kt, name):
-    c, tot, lo, hi = kt[name]
-    return tot / c
+def dispatch_stats(ms):
+    """Median / mean / min / max (µs) and count of per-dispatch durations."""
+    us = np.asarray(ms, np.float64) * 1e3
+    return {"count": int(us.size), "median_us": float(np.median(us)),
+            "mean_us": float(us.mean()), "min_us": float(us.min()), "max_us": float(us.max())}
 
 
 def bench_gemv(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup, seed=1):
+    """GB/s of one GEMV shape over rotated weight packs.  `gbs` / `sustained_*`
+    are the back-to-back rate (graph replays: timed region / calls);
+    `dispatch` holds the per-dispatch durations of the GEMV kernel launched on
+    an idle GPU (median over 200 isolated launches), the figure a kernel trace
+    reproduces; `queued_dispatch` the same kernel's durations when launches
+    are enqueued without waiting."""
     per_call = mmnb_bytes(m, k, n, bs, zp)
     count = max(2, int(np.ceil(ROTATE_BYTES / (k * n // 2 + n * ((k + bs - 1) // bs) * 4))))
     packs = make_packs(ctx, ops, synth, m, k, n, bs, zp, count, seed)
     a = synth.activations(m, k, seed)
     da = ctx.to_device(a)
     dy = ctx.alloc(m * n * 4)
-    n_steps, ms_step, ms_call, kt = time_mmnb(ctx, lib, packs, da, m, dy, steps, warmup)
-    kname = "k_gemv_valu" if "k_gemv_valu" in kt else sorted(kt)[0]
-    ev_ms = kernel_avg_ms(kt, kname)
+    n_steps, ms_step, ms_call, queued, isolated = time_mmnb(ctx, lib, packs, da, m, dy, steps,
+                                                            warmup)
+    kname = "k_gemv_valu" if "k_gemv_valu" in isolated else sorted(isolated)[0]
+    disp = dispatch_stats(isolated[kname])
     res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "packs": count,
            "bytes_per_call": per_call, "bytes_per_step": per_call * count,
            "steps": n_steps, "calls": n_steps * count, "ms_per_step": ms_step,
            "ms_per_call": ms_call, "gbs": per_call / (ms_call * 1e-3) / 1e9, "kernel": kname,
-           "kernel_ms": ms_call, "kernel_gbs": per_call / (ms_call * 1e-3) / 1e9,
-           "dispatch_event_us": ev_ms * 1e3,
-           "kernels": {k_: {"count": v[0], "avg_us": v[1] / v[0] * 1e3,
-                            "min_us": v[2] * 1e3, "max_us": v[3] * 1e3}
-                       for k_, v in kt.items()}}
+           "sustained_us": ms_call * 1e3, "sustained_gbs": per_call / (ms_call * 1e-3) / 1e9,
+           "dispatch": disp,
+           "dispatch_gbs": per_call / (disp["median_us"] * 1e-6) / 1e9,
+           "queued_dispatch": dispatch_stats(queued[kname]),
+           "kernels": {k_: dispatch_stats(v) for k_, v in isolated.items()}}
     da.free()
     dy.free()
     for p in packs:
@@ -145,29 +173,45 @@ def bench_gemv(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup, seed=1):
 
 
 def bench_gemm(ctx, lib, ops, synth, m, k, n, bs, zp, steps, warmup):
+    """Prefill MatMulNBits: the op back to back (graph replays: `k_prep_a` +
+    the GEMM per call) and per-dispatch medians of each kernel over 200
+    isolated calls (each launched on an idle GPU).  The roofline is the GEMM kernel's median dispatch, the
+    figure a kernel trace reproduces; `op` adds the prep kernel's median
+    (what a caller dispatching the op eagerly sees) and the back-to-back
+    rate."""
     p = synth.mmnb_problem(m, k, n, bs, zp, seed=2, outlier_frac=0.01)
     pack = ops.pack_nbits(p.b_q, p.scales, p.zero_points, k=k, n=n, bits=4, block_size=bs,
                           ctx=ctx)
     da = ctx.to_device(p.a)
     dy = ctx.alloc(m * n * 4)
-    n_steps, _, ms_step, kt = time_mmnb(ctx, lib, [pack], da, m, dy, steps, warmup)
+    n_steps, _, ms_step, queued, isolated = time_mmnb(ctx, lib, [pack], da, m, dy, steps,
+                                                      warmup)
     flops = 2.0 * m * k * n
-    gk = kernel_avg_ms(kt, "k_gemm_mfma")
-    # k_prep_a: the activation prep launch (row exponents and hi/lo split)
-    pk = kt["k_prep_a"][1] / kt["k_gemm_mfma"][0] if "k_prep_a" in kt else 0.0
-    achieved = flops / (gk * 1e-3) / 1e12
+    g = dispatch_stats(isolated["k_gemm_mfma"])
+    pr = dispatch_stats(isolated["k_prep_a"]) if "k_prep_a" in isolated else None
+    achieved = flops / (g["median_us"] * 1e-6) / 1e12
+    op_us = g["median_us"] + (pr["median_us"] if pr else 0.0)
     res = {"m": m, "k": k, "n": n, "block": bs, "zero_points": zp, "steps": n_steps,
            "ms_per_call": ms_step, "tflops": flops / (ms_step * 1e-3) / 1e12,
-           "gemm_kernel_us": gk * 1e3, "prep_kernel_us": pk * 1e3,
+           "gemm_dispatch": g, "prep_dispatch": pr,
+           "gemm_queued_dispatch": dispatch_stats(queued["k_gemm_mfma"]),
+           "op": {"dispatch_us": op_us, "dispatch_tflops": flops / (op_us * 1e-6) / 1e12,
+                  "sustained_us": ms_step * 1e3,
+                  "sustained_tflops": flops / (ms_step * 1e-3) / 1e12},
            "roofline": {"bound": "mfma", "achieved": achieved,
                         "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": achieved / MFMA_FP16_PEAK_TFLOPS,
+                        "kernel": "k_gemm_mfma", "kernel_median_us": g["median_us"],
+                        "dispatches": g["count"],
                         "mfma_passes": 2,
                         "mfma_utilisation": 2 * achieved / MFMA_FP16_PEAK_TFLOPS,
-                        "vs_fp32_mfma_peak": achieved / MFMA_FP32_PEAK_TFLOPS,
-                        "traffic": (measured_traffic("gemm_m512_k4096_n4096_bs32_zp")
-                                    if (m, k, n, bs, zp) == (512, 4096, 4096, 32, True)
-                                    else None)}}
+                        "vs_fp32_mfma_peak": achieved / MFMA_FP32_PEAK_TFLOPS}}
+    if (m, k, n, bs, zp) == (512, 4096, 4096, 32, True):
+        tr = measured_traffic("gemm_m512_k4096_n4096_bs32_zp")
+        res["roofline"]["traffic"] = tr
+        res["roofline"]["traffic_source"] = TRAFFIC_SOURCE if tr else None
+    else:
+        res["roofline"]["traffic"] = None
     da.free()
     dy.free()
     pack.free()
@@ -509,7 +553,12 @@ def cpu_baseline(synth, budget_s):
     (DynamicQuantizeLinear -> MatMulInteger -> rescale, one thread)."""
     from oracle import refcpu
 
-    threads = min(16, refcpu.host_threads())
+    # The GPU box gives each GPU's jobs a share of 16 host cores, whatever the
+    # machine's own count: the multi-threaded legs use that share (or fewer
+    # if fewer CPUs are allowed to this process), and both counts are stated.
+    nproc = os.cpu_count() or 1
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    threads = min(HOST_CPU_SHARE, allowed, refcpu.host_threads())
     # headline: M=1 K=N=4096 block 128, symmetric
     m, k, n, bs = 1, 4096, 4096, 128
     p = synth.mmnb_problem(m, k, n, bs, False, seed=1, scale_range=(0.002, 0.02))
@@ -566,6 +615,8 @@ def cpu_baseline(synth, budget_s):
         "value": 2.0 * 512 * 1024 * 3072 / mean / 1e12, "unit": "TOP/s", "cores": 1,
         "min_ms": lo * 1e3, "mean_ms": mean * 1e3, "calls": cnt}
     out["legs"] = legs
+    out["host"] = {"nproc": nproc, "cpus_allowed": allowed, "cpu_share_per_gpu": HOST_CPU_SHARE,
+                   "threads_used_by_multithreaded_legs": threads}
     return out
 
 
@@ -588,7 +639,7 @@ def profile_pass(ctx, lib, ops, synth, kind):
         r = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128, False, 40, 3, seed=4)
         what = (f"GEMV K=N=16384 block 128: {r['calls']} graph-replayed calls "
                 f"({r['ms_per_call'] * 1e3:.2f} us per call) and the eager timing pass "
-                f"({r['dispatch_event_us']:.2f} us per dispatch)")
+                f"({r['dispatch']['median_us']:.2f} us median per dispatch)")
         print(f"# profile pass: {what}", file=sys.stderr, flush=True)
         return
     elif kind == "gemm":
@@ -670,9 +721,11 @@ def main():
 
     head = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 128, False, args.steps,
                       args.warmup)
-    print(f"# headline GEMV: {head['gbs']:.0f} GB/s, {head['ms_per_call'] * 1e3:.2f} us per "
-          f"call ({head['packs']} calls per step), dispatch event "
-          f"{head['dispatch_event_us']:.2f} us", file=sys.stderr, flush=True)
+    hd = head["dispatch"]
+    print(f"# headline GEMV: {head['gbs']:.0f} GB/s back to back, {head['ms_per_call'] * 1e3:.2f} "
+          f"us per call ({head['packs']} calls per step); per dispatch median "
+          f"{hd['median_us']:.3f} us over {hd['count']} = {head['dispatch_gbs']:.0f} GB/s",
+          file=sys.stderr, flush=True)
     out = {
         "metric": "int4 MatMulNBits GB/s (M=1) & TFLOPS (M=512), % of HBM/MFMA roofline",
         "value": round(head["gbs"], 1),
@@ -692,20 +745,31 @@ def main():
                    "m": 1, "k": 4096, "n": 4096, "block_size": 128, "zero_points": False,
                    "calls_per_step": head["packs"], "bytes_per_call": head["bytes_per_call"],
                    "bytes_per_step": head["bytes_per_step"], "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1),
+        "roofline": {"bound": "hbm", "achieved": round(head["dispatch_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "frac": round(head["dispatch_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("gemv_m1_k4096_n4096_bs128"),
+                     "traffic_source": TRAFFIC_SOURCE,
                      "kernel": head["kernel"],
-                     "kernel_avg_us": round(head["ms_per_call"] * 1e3, 3),
-                     "launches_timed": head["calls"],
-                     "dispatch_event_us": round(head["dispatch_event_us"], 3)},
+                     "timing": "median of per-dispatch start/end timestamps (the durations a "
+                               "rocprofv3 kernel trace reports) over 200 launches, each on an "
+                               "idle GPU",
+                     "kernel_median_us": round(hd["median_us"], 3),
+                     "kernel_mean_us": round(hd["mean_us"], 3),
+                     "dispatches": hd["count"],
+                     "queued_median_us": round(head["queued_dispatch"]["median_us"], 3),
+                     "sustained": {"timing": "graph replays back to back: timed region / "
+                                             "launches (the same region as value)",
+                                   "us_per_launch": round(head["sustained_us"], 3),
+                                   "achieved": round(head["sustained_gbs"], 1),
+                                   "frac": round(head["sustained_gbs"] / HBM_PEAK_GBS, 4),
+                                   "launches": head["calls"]}},
     }
     if not args.quick:
         try:
             out["gemv_bs32_zp"] = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 32, True,
                                              args.steps, args.warmup, seed=3)
-            print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['kernel_gbs']:.0f} GB/s kernel",
+            print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['sustained_gbs']:.0f} GB/s back to back",
                   file=sys.stderr, flush=True)
             out["c1_gemv"] = bench_gemv(ctx, lib, ops, synth, 1, 1024, 1024, 32, True, 20, 3,
                                         seed=5)
@@ -713,12 +777,13 @@ def main():
                   f"per call, {out['c1_gemv']['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
             out["gemv_large"] = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128,
                                            False, 20, 3, seed=4)
-            print(f"# GEMV K=N=16384: {out['gemv_large']['kernel_gbs']:.0f} GB/s kernel",
+            print(f"# GEMV K=N=16384: {out['gemv_large']['sustained_gbs']:.0f} GB/s back to back",
                   file=sys.stderr, flush=True)
             out["gemm"] = bench_gemm(ctx, lib, ops, synth, 512, 4096, 4096, 32, True,
                                      200, 20)
-            print(f"# GEMM M=512: {out['gemm']['tflops']:.1f} TFLOP/s op, kernel "
-                  f"{out['gemm']['roofline']['achieved']:.1f}", file=sys.stderr, flush=True)
+            print(f"# GEMM M=512: {out['gemm']['tflops']:.1f} TFLOP/s op back to back, kernel "
+                  f"median dispatch {out['gemm']['roofline']['achieved']:.1f}",
+                  file=sys.stderr, flush=True)
             out["int8"] = bench_int8(ctx, lib, ops, synth, 20, 3)
             print(f"# int8 chain: {out['int8']['ms_per_chain'] * 1e3:.1f} us "
                   f"(fused, no int32 output: {out['int8']['fused']['ms_per_chain'] * 1e3:.1f} us;"
@@ -728,8 +793,8 @@ def main():
             for m in (1, 4, 8):
                 for (k, n) in synth.DECODE_PROJECTIONS:
                     r = bench_gemv(ctx, lib, ops, synth, m, k, n, 128, False, 10, 2)
-                    sweep.append({kk: r[kk] for kk in ("m", "k", "n", "gbs", "kernel_gbs",
-                                                       "kernel_ms", "bytes_per_call")})
+                    sweep.append({kk: r[kk] for kk in ("m", "k", "n", "gbs", "sustained_us",
+                                                       "dispatch_gbs", "bytes_per_call")})
             out["decode_sweep"] = sweep
             print("# decode sweep done", file=sys.stderr, flush=True)
             out["qlinear"] = bench_qlinear(ctx, lib, ops)

@@ -170,7 +170,11 @@ int mmnb_pack_nbits_ex(mmnb_ctx *ctx, const mmnb_nbits_desc *desc, mmnb_pack **o
 /* y = saturate(roundEven(x / scale) + zp), scale = fl32((max(0,x) -
  * min(0,x)) / 255.0) in double, zp = roundEven(clamp(fl32(-min/scale))).
  * Host buffers, synchronous; zero_point is returned as int64 like
- * Tensor.scalarInt.
+ * Tensor.scalarInt.  Input the reference rejects -- scale != 0 and some x
+ * NaN or infinite, where its _roundEven calls toInt() on a non-finite
+ * quotient (onnx_ops.dart:2490-2497, :2574-2576) -- returns
+ * MMNB_ERR_UNSUPPORTED (outputs unspecified).  NaN among zeros (scale 0)
+ * rounds nothing and returns zp everywhere, as the reference does.
  * Replaces: opDynamicQuantizeLinear (lib/src/onnx_ops.dart:2556-2583),
  * _dispatch arm 'DynamicQuantizeLinear' (lib/src/onnx_graph.dart:1561-1562). */
 int mmnb_dynamic_quantize_linear(mmnb_ctx *ctx, const float *x, int64_t n,
@@ -179,7 +183,11 @@ int mmnb_dynamic_quantize_linear(mmnb_ctx *ctx, const float *x, int64_t n,
 
 /* Device-buffer form: d_scale (1 float) and d_zero_point (1 int32) are
  * written on the device, so a following MatMulInteger can consume them
- * without a host round trip. */
+ * without a host round trip.  It runs asynchronously and cannot report the
+ * input the host form rejects: for that input it writes a NaN scale (never
+ * produced otherwise) and defined bytes (NaN quantises to 0), so a NaN
+ * *d_scale is the device-side error marker.  mmnb_dynamic_matmul_dev passes
+ * that NaN scale on: its fp32 results are then NaN. */
 int mmnb_dynamic_quantize_linear_dev(mmnb_ctx *ctx, const float *d_x,
                                      int64_t n, uint8_t *d_y, float *d_scale,
                                      int32_t *d_zero_point);
@@ -488,6 +496,15 @@ int mmnb_kernel_timing(mmnb_ctx *ctx, int enable, int max_launches);
  * (see mmnb_kernel_name); waits for the recorded launches to finish. */
 int mmnb_kernel_timing_read(mmnb_ctx *ctx, int kernel_id, int64_t *count,
                             double *total_ms, double *min_ms, double *max_ms);
+
+/* Each recorded duration (ms) of kernel `kernel_id`, in launch order: up to
+ * `cap` of them into ms_out, and the number recorded into *count (which may
+ * exceed cap).  These are the dispatch's own start/end timestamps, the
+ * per-kernel durations a kernel tracer reports, so medians taken from them
+ * can be checked against a rocprofv3 kernel trace.  Waits for the recorded
+ * launches to finish. */
+int mmnb_kernel_timing_samples(mmnb_ctx *ctx, int kernel_id, float *ms_out, int64_t cap,
+                               int64_t *count);
 
 /* Name of kernel id 0.. (NULL past the last id). */
 const char *mmnb_kernel_name(int kernel_id);

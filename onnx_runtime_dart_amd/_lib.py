@@ -84,6 +84,7 @@ SIGNATURES = {
     "mmnb_kernel_timing": (_int, [_vp, _int, _int]),
     "mmnb_kernel_timing_read": (_int, [_vp, _int, _P(_i64), _P(ctypes.c_double),
                                        _P(ctypes.c_double), _P(ctypes.c_double)]),
+    "mmnb_kernel_timing_samples": (_int, [_vp, _int, _P(ctypes.c_float), _i64, _P(_i64)]),
     "mmnb_kernel_name": (ctypes.c_char_p, [_int]),
     "mmnb_probe_empty": (_int, [_vp, _int]),
     "mmnb_probe_stream_read": (_int, [_vp, _vp, _sz]),
@@ -247,6 +248,26 @@ class Context:
             if c.value:
                 out[name.decode()] = (c.value, t.value, lo.value, hi.value)
             kid += 1
+        return out
+
+    def kernel_timing_samples(self, name):
+        """Every recorded duration (ms) of kernel `name`, in launch order, as a
+        float32 array (empty if it was not launched while timing was on)."""
+        kid = 0
+        while True:
+            kn = self.lib.mmnb_kernel_name(kid)
+            if kn is None:
+                raise KeyError(name)
+            if kn.decode() == name:
+                break
+            kid += 1
+        c = ctypes.c_int64()
+        check(self.lib.mmnb_kernel_timing_samples(self.handle, kid, None, 0, ctypes.byref(c)))
+        out = np.zeros(c.value, np.float32)
+        if c.value:
+            check(self.lib.mmnb_kernel_timing_samples(
+                self.handle, kid, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), c.value,
+                ctypes.byref(c)))
         return out
 
     def graph_begin(self):

@@ -26,7 +26,8 @@ CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libmmnb.so"
 SOURCES = ["mmnb_runtime.hip", "mmnb_nbits.hip", "mmnb_int8.hip", "mmnb_decoder.hip",
-           "mmnb_qlinear.hip", "mmnb_nbits_ex.hip", "mmnb_model.hip", "mmnb_noalloc.hip"]
+           "mmnb_qlinear.hip", "mmnb_nbits_ex.hip", "mmnb_model.hip", "mmnb_noalloc.hip",
+           "mmnb_nbits_any.hip"]
 HOST_SOURCES = ["mmnb_host.cpp"]
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

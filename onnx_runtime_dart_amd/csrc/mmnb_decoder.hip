@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_prep(const float *X, int64_t M,
     const float gk = gv[e];
     const float y = (float)((double)srow[k] * inv * (double)gk);
     v[e] = ok ? y : 0.0f;
-    mx = fmaxf(mx, fabsf(v[e]));
+    mx = fmaxf(mx, finite_abs(v[e]));
   }
   const int ex = prep_row_exponent(mx, wmx);
   if (t == 0 && live) row_exp[r] = ex;
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void k_swiglu_prep(const float *__restrict__ g
     const float g = gu[i], u = gu[i + 1];
     const float sig = (float)(1.0 / (1.0 + exp(-(double)g)));
     v[e] = ok ? (g * sig) * u : 0.0f;
-    mx = fmaxf(mx, fabsf(v[e]));
+    mx = fmaxf(mx, finite_abs(v[e]));
   }
   const int ex = prep_row_exponent(mx, wmx);
   if (t == 0 && live) row_exp[r] = ex;
@@ -1259,7 +1259,8 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
     return fail(MMNB_ERR_UNSUPPORTED,
                 "decoder: needs head_dim <= 128 (a multiple of 32) and hidden, heads*head_dim, "
                 "intermediate multiples of 64 and <= 4096");
-  if (lm_head->kind != kPackNBits || lm_head->ext || lm_head->k != c.hidden || lm_head->n != c.vocab ||
+  if (lm_head->kind != kPackNBits || lm_head->ext || lm_head->generic || lm_head->k != c.hidden ||
+      lm_head->n != c.vocab ||
       lm_head->ctx != ctx)
     return fail(MMNB_ERR_ARG, "decoder: lm_head pack shape");
   CtxLock lk(ctx);
@@ -1336,7 +1337,8 @@ int mmnb_decoder_set_layer(mmnb_decoder *d, int64_t layer, const float *ln1, con
   const int64_t H = c.hidden, hd = c.head_dim, nh = c.heads, kvh = c.kv_heads,
                 I = c.intermediate;
   auto ok = [&](const mmnb_pack *p, int64_t k, int64_t n) {
-    return p->kind == kPackNBits && !p->ext && p->ctx == d->ctx && p->k == k && p->n == n;
+    return p->kind == kPackNBits && !p->ext && !p->generic && p->ctx == d->ctx && p->k == k &&
+           p->n == n;
   };
   if (!ok(qkv, H, (nh + 2 * kvh) * hd) || !ok(o, nh * hd, H) || !ok(gate_up, H, 2 * I) ||
       !ok(down, I, H))

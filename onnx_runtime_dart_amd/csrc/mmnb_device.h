@@ -133,7 +133,8 @@ __device__ __forceinline__ float snib16_f32(uint32_t v) {
 __device__ __forceinline__ uint32_t dq8_const(int z) { return (uint32_t)(128 - 8 * z) * 0x01010101u; }
 
 // Scale S of the dequantised values: 1/16 (zero point 8) or 8 (explicit
-// zero points); the kernels multiply their sums by 1 / S.
+// zero points); the kernels multiply each block's scale by 1 / S (exact for
+// normal scales), so no sum is S times larger or smaller than the result.
 template <bool HAS_ZP>
 constexpr float dq_unscale() { return HAS_ZP ? 0.125f : 16.0f; }
 
@@ -200,8 +201,16 @@ __device__ __forceinline__ void st_act(float *p, float v) {
 // one 1 KB unit per (32-row block, 64-k segment s, 16-k step j, part hi|lo),
 // lane l holding row l%32, k = 64s + 16j + 8(l/32) + {0,4,1,5,2,6,3,7}.
 
-// The row exponent e_m for a row whose largest magnitude is mx (0 for an
-// all-zero or non-finite row).
+// |v| for finite v, 0 for NaN and infinities: rows are scaled by their
+// largest FINITE magnitude, so the finite elements of a row that also holds
+// an infinity or a NaN keep their precision and stay within fp16's range.
+__device__ __forceinline__ float finite_abs(float v) {
+  const float a = fabsf(v);
+  return a < INFINITY ? a : 0.0f;
+}
+
+// The row exponent e_m for a row whose largest finite magnitude is mx (0 for
+// an all-zero row).
 __device__ __forceinline__ int prep_a_exponent(float mx) {
   return (mx > 0.0f && mx < INFINITY) ? 13 - ilogbf(mx) : 0;
 }
@@ -225,7 +234,11 @@ __device__ __forceinline__ void prep_a_store8(uint4 *__restrict__ out, int64_t s
     const float x = ldexpf(v[e], ex);
     const _Float16 h = (_Float16)x;
     hi[e] = h;
-    lo[e] = (_Float16)(x - (float)h);
+    // a NaN or infinite element keeps hi = x and lo = 0 (x - hi would be
+    // NaN for an infinity): each product hi * w is then the reference's
+    // a * w, +-inf, or NaN where w == 0, and the sums follow IEEE as its do
+    const float d = x - (float)h;
+    lo[e] = (_Float16)(d == d ? d : 0.0f);
   }
   const prep_h8 hv = {hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
   const prep_h8 lv = {lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};

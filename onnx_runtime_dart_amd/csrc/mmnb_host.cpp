@@ -66,10 +66,16 @@ int nbits_prepare(const mmnb_nbits_desc *d, NbitsHost *out) {
   if (k <= 0 || n <= 0) return fail(MMNB_ERR_ARG, "MatMulNBits: K and N must be positive");
   if (k > INT32_MAX / 2 || n > INT32_MAX)
     return fail(MMNB_ERR_UNSUPPORTED, "MatMulNBits: K or N too large for the kernels");
-  if (bs < 16 || bs > 65536 || (bs & (bs - 1)) != 0)
+  // any even block size for the reference's own form (bits 4, uint8 zero
+  // points, no g_idx / bias); the extensions need a power of two >= 16
+  if (bs < 2 || (bs & 1) || bs > (int64_t(1) << 30))
     return fail(MMNB_ERR_UNSUPPORTED,
-                "MatMulNBits: block_size must be a power of two in [16, 65536], got " +
+                "MatMulNBits: block_size must be even and at most 2^30, got " +
                     std::to_string(bs));
+  const bool native_block = bs >= 16 && (bs & (bs - 1)) == 0;
+  if (bits == 8 && !native_block)
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "MatMulNBits: bits=8 needs a power-of-two block_size >= 16");
   const int64_t nb = (k + bs - 1) / bs;
   const int64_t blob = bs * bits / 8;
   int64_t nnb, need_b;
@@ -152,6 +158,10 @@ int nbits_prepare(const mmnb_nbits_desc *d, NbitsHost *out) {
       });
     }
   }
+  if (!native_block && (!zf.empty() || !out->bias.empty() || !perm.empty()))
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "MatMulNBits: g_idx, bias and float zero points need a power-of-two "
+                "block_size >= 16");
   // ---- the virtual 4-bit weight
   const uint8_t *B = d->b_q;
   const int64_t kp = nb * bs;

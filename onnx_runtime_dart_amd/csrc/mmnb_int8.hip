@@ -24,6 +24,13 @@ namespace mmnb {
 //           innocuous for division at these precisions), so __fdiv_rn gives
 //           the same bits.  rint is round-half-even, as _roundEven
 //           (onnx_ops.dart:2490-2497) for finite input.
+// Non-finite input: the reference throws (toInt() of a NaN / infinite
+// quotient in _roundEven) whenever scale != 0 and some x is NaN or infinite;
+// an infinity makes mn or mx infinite, a NaN is flagged by pass 1.  Then the
+// scale is written as NaN, the marker the host entry point turns into
+// MMNB_ERR_UNSUPPORTED, and every quantised byte is defined (NaN -> 0).  With
+// scale == 0 (NaN among zeros) the reference rounds nothing and returns zp
+// everywhere, and so do the kernels.
 // ---------------------------------------------------------------------------
 constexpr int kDqlThreads = 256;
 constexpr int kDqlMaxBlocks = 1024;
@@ -38,8 +45,10 @@ constexpr int kDqlUnroll = 2;
 // kDqlUnroll loads instead of one per load.
 __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restrict__ x,
                                                             int64_t n,
-                                                            float2 *__restrict__ part) {
+                                                            float2 *__restrict__ part,
+                                                            int *__restrict__ part_nan) {
   float mn = 0.0f, mx = 0.0f;
+  bool nan = false;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const bool vec = (((uintptr_t)x) & 15) == 0;
@@ -60,6 +69,8 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restr
         mn = v[u].y < mn ? v[u].y : mn; mx = v[u].y > mx ? v[u].y : mx;
         mn = v[u].z < mn ? v[u].z : mn; mx = v[u].z > mx ? v[u].z : mx;
         mn = v[u].w < mn ? v[u].w : mn; mx = v[u].w > mx ? v[u].w : mx;
+        nan |= (v[u].x != v[u].x) | (v[u].y != v[u].y) | (v[u].z != v[u].z) |
+               (v[u].w != v[u].w);
       }
     }
     done = n4 << 2;
@@ -68,22 +79,31 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restr
     const float v = x[i];
     mn = v < mn ? v : mn;
     mx = v > mx ? v : mx;
+    nan |= v != v;
   }
+  const bool wave_nan = __any(nan);
   for (int off = 32; off > 0; off >>= 1) {
     const float a = __shfl_xor(mn, off, 64), b = __shfl_xor(mx, off, 64);
     mn = a < mn ? a : mn;
     mx = b > mx ? b : mx;
   }
   __shared__ float2 s[kDqlThreads / 64];
+  __shared__ int s_nan[kDqlThreads / 64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) s[wave] = make_float2(mn, mx);
+  if (lane == 0) {
+    s[wave] = make_float2(mn, mx);
+    s_nan[wave] = wave_nan ? 1 : 0;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
+    int any_nan = s_nan[0];
     for (int w = 1; w < kDqlThreads / 64; w++) {
       mn = s[w].x < mn ? s[w].x : mn;
       mx = s[w].y > mx ? s[w].y : mx;
+      any_nan |= s_nan[w];
     }
     part[blockIdx.x] = make_float2(mn, mx);
+    part_nan[blockIdx.x] = any_nan;
   }
 }
 
@@ -91,16 +111,18 @@ __device__ __forceinline__ uint8_t dql_q(float v, float scale, int zp) {
   if (scale == 0.0f) return (uint8_t)zp;
   const float r = rintf(__fdiv_rn(v, scale));
   // r is an integral float; clamp before converting (|r| <= ~2^8 for finite
-  // in-contract input, but saturate defensively).
+  // in-contract input; NaN, reached only out of contract, goes to 0).
   float q = r + (float)zp;
-  q = q < 0.0f ? 0.0f : (q > 255.0f ? 255.0f : q);
+  q = q >= 0.0f ? (q > 255.0f ? 255.0f : q) : 0.0f;
   return (uint8_t)(int)q;
 }
 
 __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
-    const float *__restrict__ x, int64_t n, const float2 *__restrict__ part, int nparts,
-    uint8_t *__restrict__ y, float *__restrict__ out_scale, int32_t *__restrict__ out_zp) {
+    const float *__restrict__ x, int64_t n, const float2 *__restrict__ part,
+    const int *__restrict__ part_nan, int nparts, uint8_t *__restrict__ y,
+    float *__restrict__ out_scale, int32_t *__restrict__ out_zp) {
   __shared__ float2 s[kDqlThreads / 64];
+  __shared__ int s_nan[kDqlThreads / 64];
   __shared__ float s_scale;
   __shared__ int s_zp;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -119,30 +141,41 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
     }
   }
   float mn = 0.0f, mx = 0.0f;
+  bool nan = false;
   for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
     const float2 p = part[i];
     mn = p.x < mn ? p.x : mn;
     mx = p.y > mx ? p.y : mx;
+    nan |= part_nan[i] != 0;
   }
   for (int off = 32; off > 0; off >>= 1) {
     const float a = __shfl_xor(mn, off, 64), b = __shfl_xor(mx, off, 64);
     mn = a < mn ? a : mn;
     mx = b > mx ? b : mx;
   }
+  const bool wave_nan = __any(nan);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) s[wave] = make_float2(mn, mx);
+  if (lane == 0) {
+    s[wave] = make_float2(mn, mx);
+    s_nan[wave] = wave_nan ? 1 : 0;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
+    int any_nan = s_nan[0];
     for (int w = 1; w < kDqlThreads / 64; w++) {
       mn = s[w].x < mn ? s[w].x : mn;
       mx = s[w].y > mx ? s[w].y : mx;
+      any_nan |= s_nan[w];
     }
     const double dmn = (double)mn, dmx = (double)mx;
-    const float scale = (float)((dmx - dmn) / 255.0);
+    float scale = (float)((dmx - dmn) / 255.0);
+    // out of contract (the reference throws): NaN scale marks it
+    if (scale != 0.0f && (any_nan || __builtin_isinf(mn) || __builtin_isinf(mx)))
+      scale = __builtin_nanf("");
     const double ds = (double)scale;
     const float zpf = ds == 0.0 ? 0.0f : (float)(-dmn / ds);
     double zc = (double)zpf;
-    zc = zc < 0.0 ? 0.0 : (zc > 255.0 ? 255.0 : zc);
+    zc = zc >= 0.0 ? (zc > 255.0 ? 255.0 : zc) : 0.0;  // NaN (out of contract) -> 0
     const int zp = (int)rint(zc);
     s_scale = scale;
     s_zp = zp;
@@ -184,20 +217,24 @@ int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *
                int32_t *d_zp) {
   void *d_part = nullptr;
   int rc;
-  if ((rc = scratch_get(ctx, 3, sizeof(float2) * kDqlMaxBlocks, &d_part))) return rc;
+  // partials: kDqlMaxBlocks (min, max) pairs, then kDqlMaxBlocks NaN flags
+  if ((rc = scratch_get(ctx, 3, (sizeof(float2) + sizeof(int)) * kDqlMaxBlocks, &d_part)))
+    return rc;
+  int *d_part_nan = (int *)((float2 *)d_part + kDqlMaxBlocks);
   // one batch of kDqlUnroll float4 per thread when the grid allows
   const int64_t per_block = (int64_t)kDqlThreads * kDqlUnroll * 4;
   int64_t blocks = (n + per_block - 1) / per_block;
   if (blocks < 1) blocks = 1;
   if (blocks > kDqlMaxBlocks) blocks = kDqlMaxBlocks;
   if ((rc = launch(ctx, kKernDqlMinmax, k_dql_minmax, dim3((unsigned)blocks), dim3(kDqlThreads),
-                    0, d_x, n, (float2 *)d_part)))
+                    0, d_x, n, (float2 *)d_part, d_part_nan)))
     return rc;
   int64_t qblocks = (n + per_block - 1) / per_block;
   if (qblocks < 1) qblocks = 1;
   if (qblocks > 4096) qblocks = 4096;
   return launch(ctx, kKernDqlQuant, k_dql_quant, dim3((unsigned)qblocks), dim3(kDqlThreads), 0,
-                d_x, n, (const float2 *)d_part, (int)blocks, d_y, d_scale, d_zp);
+                d_x, n, (const float2 *)d_part, (const int *)d_part_nan, (int)blocks, d_y,
+                d_scale, d_zp);
 }
 
 // ---------------------------------------------------------------------------

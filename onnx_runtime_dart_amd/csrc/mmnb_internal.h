@@ -121,6 +121,10 @@ struct mmnb_pack {
   uint32_t *d_zt = nullptr;
   int64_t ldsz = 0;
   bool has_zp = false;
+  // Block size the fast kernels cannot take (even, not a multiple of 16): the
+  // reference's bytes [n][n_blocks][block/2] (col_bytes per column), scales
+  // and flat zero points as they are, for k_nbits_generic; k64 = k.
+  bool generic = false;
   // --- MatMulNBits beyond the reference's 4-bit form (mmnb_pack_nbits_ex):
   // the kernels run on a 4-bit "virtual" weight of k rows (k, n_blocks, d_w,
   // d_scales, d_zp above); A is first gathered into [m, k64] when d_asrc is
@@ -177,7 +181,8 @@ enum KernelId {
   kKernDecGemvLm = 15,   // decode MatMulNBits, RMSNorm + argmax (lm_head)
   kKernIm2col = 16,      // convolution input rows for the MatMulInteger kernels
   kKernNbitsEx = 17,     // extended MatMulNBits: A gather, block sums, correction
-  kKernCount = 18
+  kKernNbitsAny = 18,    // MatMulNBits of a block size the fast kernels do not take
+  kKernCount = 19
 };
 
 // Launch `kern` on the context stream; in timing mode the dispatch records
@@ -238,9 +243,22 @@ int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n, int64_t k);
 // Builds a 4-bit MatMulNBits pack (lock held): b_q [n, ceil(k/bs), bs/2]
 // bytes, scales fp32 [n * ceil(k/bs)], zp packed uint4 with the flat index
 // (or null: every byte zp_fill).
+// bs is a power of two >= 16; src_col (0: ceil(k/bs) * bs/2) is the byte
+// stride of b_q's columns.
 int pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales,
                     const uint8_t *zp, int zp_fill, int64_t k, int64_t n, int64_t bs,
-                    mmnb_pack **out);
+                    mmnb_pack **out, int64_t src_col = 0);
+// The same for any even block size (lock held): power-of-two blocks >= 16
+// as above, other multiples of 16 re-blocked to their largest power-of-two
+// divisor, the rest as a generic pack; odd sizes MMNB_ERR_UNSUPPORTED.
+int pack_nbits_any(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales,
+                   const uint8_t *zp, int zp_fill, int64_t k, int64_t n, int64_t bs,
+                   mmnb_pack **out);
+// Block sizes the fast kernels take as they are (powers of two >= 16).
+bool nbits_block_native(int64_t bs);
+// MatMulNBits on a generic pack (no scratch; the reference's order and bits).
+int launch_nbits_generic(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
+                         int64_t m, float *d_y);
 
 // MatMulNBits for any pack (plain or extended): gathers A, runs the kernels
 // and the correction pass as the pack requires.  lda = row stride of A.

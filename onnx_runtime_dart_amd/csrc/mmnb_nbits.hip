@@ -270,7 +270,9 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     for (int r = 0; r < R; r++)
       wv[r] = ld_weights16_u4(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
     __builtin_amdgcn_sched_barrier(0);
-    // ---- arithmetic: exact (q - zp) per weight, scaled by dq_unscale
+    // ---- arithmetic: exact S * (q - zp) per weight (dq_nibbles); the block's
+    // scale carries the 1 / S (dq_unscale, exact for normal scales), so the
+    // sums range like the reference's (q - zp) * scale terms
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const uint32_t wd[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
@@ -287,7 +289,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
 #pragma unroll
           for (int e = 0; e < 8; e++) d = fmaf(av[8 * j + e], qv[e], d);
         }
-        acc[r] = fmaf(inbq[q] ? sraw[r][q] : 0.0f, d, acc[r]);
+        // a lane past the last chunk (or a block past the last one) drops
+        // its d: its activations may be chunk 0's, and 0 * inf would be NaN
+        const float sc = sraw[r][q] * dq_unscale<HAS_ZP>();
+        acc[r] = inbq[q] ? fmaf(sc, d, acc[r]) : acc[r];
       }
       // column by column: the scheduler would otherwise hoist later
       // columns' dequantisation and so wait for every weight load first
@@ -305,7 +310,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     float v = 0.0f;
     for (int ww = 0; ww < nw; ww++) v += red[ww][threadIdx.x];
     const int col = col0 + threadIdx.x;
-    if (col < N) Y[col] = v * dq_unscale<HAS_ZP>();
+    if (col < N) Y[col] = v;
   }
 }
 
@@ -408,8 +413,8 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
 #pragma unroll
     for (int e = 0; e < 32; e++) av[e] = av[e] * inv * gv[e];
   }
-  // ---- arithmetic: exact (q - 8) / 16 per weight (dq_nibbles), unscaled
-  // below; column by column, so that column r waits only for its own
+  // ---- arithmetic: exact (q - 8) / 16 per weight (dq_nibbles), the 16
+  // folded into the block's scale; column by column, so that column r waits only for its own
   // weights.  The empty asm pins each column's sum in its place: without it
   // the compiler sinks the FMAs of every column but the first to the end,
   // keeping all 8R dequantised values live (270 VGPRs at R = 8).
@@ -425,7 +430,7 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
 #pragma unroll
       for (int e = 0; e < 8; e++) d = fmaf(av[8 * j + e], qv[e], d);
     }
-    const float sc = cv ? sraw[r] : 0.0f;
+    const float sc = cv ? sraw[r] * dq_unscale<false>() : 0.0f;
     acc[r] = sc * d;
     asm volatile("" : "+v"(acc[r]));
     __builtin_amdgcn_sched_barrier(0);
@@ -441,7 +446,6 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   const int i = threadIdx.x;
   if (i < 2 * R) {
     for (int ww = 0; ww < nw; ww++) v += red[ww][i];
-    v *= dq_unscale<false>();
   }
   const int col = col0 + i;
   if constexpr (EPI == kDecPlain) {
@@ -492,8 +496,9 @@ int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n, int64_t k) {
 int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
                     const float *norm_gamma, float eps, int epi, const float *resid,
                     float *d_y, unsigned long long *d_argmax) {
-  if (p->has_zp || p->block < 64)
-    return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV: needs block >= 64 and no zero points");
+  if (p->has_zp || p->block < 64 || p->generic)
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "decoder GEMV: needs a power-of-two block >= 64 and no zero points");
   if (p->k % kSegK != 0 || p->k > 4096)
     return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV: K must be a multiple of 64, <= 4096");
   const int C = (int)(p->col_bytes / 16);
@@ -696,7 +701,7 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
         if (((j + 1) % (4 / NBPC)) == 0) {
 #pragma unroll
           for (int r = 0; r < R; r++) {
-            const float sc = ch.inbq[q] ? ch.sraw[r][q] : 0.0f;
+            const float sc = ch.inbq[q] ? ch.sraw[r][q] * dq_unscale<HAS_ZP>() : 0.0f;
 #pragma unroll
             for (int m = 0; m < M; m++) {
               acc[m][r] = fmaf(sc, d[m][r], acc[m][r]);
@@ -728,7 +733,7 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
       float v = 0.0f;
       for (int ww = 0; ww < kw; ww++) v += red[sg * kw + ww][m][cl];
       const int col = gi * (2 * R) + cl;
-      if (gi < groups && col < N) Y[(int64_t)m * N + col] = v * dq_unscale<HAS_ZP>();
+      if (gi < groups && col < N) Y[(int64_t)m * N + col] = v;
     }
     __syncthreads();
   }
@@ -943,7 +948,7 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_prep_a(
   load8(kl, keep);
   float mx = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(keep[e]));
+  for (int e = 0; e < 8; e++) mx = fmaxf(mx, finite_abs(keep[e]));
   int64_t k0 = kPrepChunk;
   for (; k0 + 3 * kPrepChunk < K; k0 += 4 * kPrepChunk) {  // four loads in flight
     float v[4][8];
@@ -952,13 +957,13 @@ __global__ __launch_bounds__(64 * kPrepWaves) void k_prep_a(
 #pragma unroll
     for (int u = 0; u < 4; u++)
 #pragma unroll
-      for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[u][e]));
+      for (int e = 0; e < 8; e++) mx = fmaxf(mx, finite_abs(v[u][e]));
   }
   for (; k0 < K; k0 += kPrepChunk) {
     float v[8];
     load8(k0 + kl, v);
 #pragma unroll
-    for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[e]));
+    for (int e = 0; e < 8; e++) mx = fmaxf(mx, finite_abs(v[e]));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -1683,6 +1688,7 @@ int launch_matmul_nbits_prepared(mmnb_ctx *ctx, const mmnb_pack *p, int64_t m, f
 // kTailPad bytes of slack.  Allocates nothing.
 int launch_matmul_nbits_ws(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                            int64_t m, float *d_y, void *ws, size_t ws_bytes) {
+  if (p->generic) return launch_nbits_generic(ctx, p, d_a, lda, m, d_y);  // no scratch
   // the GEMVs use no scratch (the multi-row one falls back to the GEMM when A
   // does not fit its LDS: that GEMM takes the workspace below)
   if (m == 1 || (m <= 8 && gemv_multi_fits(ctx, p, m)))
@@ -1713,6 +1719,7 @@ int launch_matmul_nbits_ws(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, 
 
 int launch_matmul_nbits(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_a, int64_t lda,
                         int64_t m, float *d_y) {
+  if (p->generic) return launch_nbits_generic(ctx, p, d_a, lda, m, d_y);
   if (m <= 8) return launch_gemv(ctx, p, d_a, lda, m, d_y);
   return launch_gemm(ctx, p, d_a, lda, m, d_y);
 }

@@ -197,9 +197,14 @@ int mmnb_pack_nbits_ex(mmnb_ctx *ctx, const mmnb_nbits_desc *d, mmnb_pack **out)
   {
     CtxLock lk(ctx);
     if ((rc = set_device(ctx))) return rc;
-    if ((rc = pack_nbits_core(ctx, h.vb.data(), h.vs.data(), h.vz.empty() ? nullptr : h.vz.data(),
-                              h.zfill, h.kv, h.n, h.block, &p)))
-      return rc;
+    // the reference's own form takes any even block size (pack_nbits_any);
+    // the extensions run on power-of-two blocks (nbits_prepare checks)
+    const bool plain = h.asrc.empty() && h.corr.empty() && h.bias.empty();
+    const uint8_t *vz = h.vz.empty() ? nullptr : h.vz.data();
+    rc = plain ? pack_nbits_any(ctx, h.vb.data(), h.vs.data(), vz, h.zfill, h.kv, h.n, h.block, &p)
+               : pack_nbits_core(ctx, h.vb.data(), h.vs.data(), vz, h.zfill, h.kv, h.n, h.block,
+                                 &p);
+    if (rc) return rc;
     p->k_in = h.k;
     p->ext = !h.asrc.empty() || !h.corr.empty() || !h.bias.empty();
     if (!h.asrc.empty()) urc = upload(p, h.asrc, &p->d_asrc);

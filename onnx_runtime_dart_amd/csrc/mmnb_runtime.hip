@@ -207,9 +207,9 @@ int mmnb_device_info(mmnb_ctx *ctx, char *name, size_t name_len,
 
 int mmnb::pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales,
                     const uint8_t *zero_points, int zp_fill, int64_t k, int64_t n,
-                    int64_t block_size, mmnb_pack **out) {
+                    int64_t block_size, mmnb_pack **out, int64_t src_col) {
   const int64_t nb = (k + block_size - 1) / block_size;
-  const int64_t src_col = nb * (block_size / 2);
+  if (src_col <= 0) src_col = nb * (block_size / 2);
   const int64_t zp_need = (n * nb + 1) / 2;
   int rc;
   mmnb_pack *p = new (std::nothrow) mmnb_pack();
@@ -283,10 +283,15 @@ int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
                 "MatMulNBits: only bits=4 supported, got " + std::to_string(bits));
   if (k <= 0 || n <= 0)
     return fail(MMNB_ERR_ARG, "MatMulNBits: K and N must be positive");
-  if (block_size < 16 || (block_size & (block_size - 1)) != 0)
+  if (k > INT32_MAX / 2 || n > INT32_MAX)
+    return fail(MMNB_ERR_UNSUPPORTED, "MatMulNBits: K or N too large for the kernels");
+  // any even block size, as the reference (onnx_qlinear_ops.dart:120-121);
+  // an odd one cannot hold its nibbles in block_size ~/ 2 bytes
+  if (block_size < 2 || (block_size & 1))
     return fail(MMNB_ERR_UNSUPPORTED,
-                "MatMulNBits: block_size must be a power of two >= 16, got " +
-                    std::to_string(block_size));
+                "MatMulNBits: block_size must be even, got " + std::to_string(block_size));
+  if (block_size > (int64_t(1) << 30))
+    return fail(MMNB_ERR_UNSUPPORTED, "MatMulNBits: block_size above 2^30");
   const int64_t nb = (k + block_size - 1) / block_size;
   const int64_t src_col = nb * (block_size / 2);
   if (!b_q || b_q_len < n * src_col)
@@ -304,7 +309,7 @@ int mmnb_pack_nbits(mmnb_ctx *ctx, const uint8_t *b_q, int64_t b_q_len,
   CtxLock lk(ctx);
   int rc = set_device(ctx);
   if (rc) return rc;
-  return pack_nbits_core(ctx, b_q, scales, zero_points, 0x88, k, n, block_size, out);
+  return pack_nbits_any(ctx, b_q, scales, zero_points, 0x88, k, n, block_size, out);
 }
 
 static int check_nbits_pack(const mmnb_ctx *ctx, const mmnb_pack *p) {
@@ -400,6 +405,11 @@ int mmnb_dynamic_quantize_linear(mmnb_ctx *ctx, const float *x, int64_t n,
   MMNB_HIP(hipMemcpyAsync(&hs, d_scale, 4, hipMemcpyDeviceToHost, ctx->stream));
   MMNB_HIP(hipMemcpyAsync(&hz, d_zp, 4, hipMemcpyDeviceToHost, ctx->stream));
   MMNB_HIP(hipStreamSynchronize(ctx->stream));
+  // a NaN scale is the kernels' marker for input the reference rejects
+  if (hs != hs)
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "DynamicQuantizeLinear: NaN or infinite input (roundEven of a non-finite "
+                "quotient)");
   *scale = hs;
   *zero_point = hz;
   return MMNB_OK;
@@ -722,7 +732,7 @@ static const char *kKernelNames[kKernCount] = {
     "k_gemv_valu", "k_prep_a", "k_gemm_mfma", "k_dql_minmax",
     "k_dql_quant", "k_mmi_mfma", "k_repack_nbits", "k_prep_int_b", "k_probe_empty",
     "k_probe_read", "k_dec_gemv", "k_dec_attn", "k_dec_ops", "k_dec_gemv_res",
-    "k_dec_gemv_glu", "k_dec_gemv_lm", "k_im2col", "k_nbits_ex"};
+    "k_dec_gemv_glu", "k_dec_gemv_lm", "k_im2col", "k_nbits_ex", "k_nbits_generic"};
 
 const char *mmnb_kernel_name(int kernel_id) {
   if (kernel_id < 0 || kernel_id >= kKernCount) return nullptr;
@@ -775,6 +785,29 @@ int mmnb_kernel_timing_read(mmnb_ctx *ctx, int kernel_id, int64_t *count, double
   if (total_ms) *total_ms = tot;
   if (min_ms) *min_ms = mn;
   if (max_ms) *max_ms = mx;
+  return MMNB_OK;
+}
+
+int mmnb_kernel_timing_samples(mmnb_ctx *ctx, int kernel_id, float *ms_out, int64_t cap,
+                               int64_t *count) {
+  MMNB_GUARD_CTX(ctx);
+  if (cap < 0 || (cap > 0 && !ms_out) || !count)
+    return fail(MMNB_ERR_ARG, "mmnb_kernel_timing_samples: bad output buffer");
+  CtxLock lk(ctx);
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  MMNB_HIP(hipStreamSynchronize(ctx->stream));
+  int64_t c = 0;
+  for (size_t i = 0; i < ctx->tused; i++) {
+    if (ctx->tkid[i] != kernel_id) continue;
+    if (c < cap) {
+      float ms = 0.0f;
+      MMNB_HIP(hipEventElapsedTime(&ms, ctx->tev[2 * i], ctx->tev[2 * i + 1]));
+      ms_out[c] = ms;
+    }
+    c++;
+  }
+  *count = c;
   return MMNB_OK;
 }
 

@@ -434,9 +434,14 @@ static int64_t round_even(double v) {
 /*   y[k]  = clamp(roundEven(fl32(x[k] / scale)) + zp, 0, 255); when       */
 /*           scale == 0 every y is zp.                                     */
 /* Returns the rounding-exact values; zp as int64 like Tensor.scalarInt.    */
+/* Non-finite input: when scale != 0, a NaN or infinite x[k] makes the      */
+/* quotient non-finite (an infinity also makes scale infinite, and          */
+/* inf / inf is NaN), and _roundEven's toInt() throws UnsupportedError:     */
+/* REF_ERR_UNSUPPORTED, outputs unspecified.  When scale == 0 (NaN among    */
+/* zeros) no element is rounded and the reference returns zp everywhere.    */
 /* ------------------------------------------------------------------------ */
-void ref_dql(const float *x, int64_t n, uint8_t *y, float *scale_out,
-             int64_t *zp_out) {
+int ref_dql(const float *x, int64_t n, uint8_t *y, float *scale_out,
+            int64_t *zp_out) {
   double mn = 0.0, mx = 0.0;
   for (int64_t k = 0; k < n; k++) {
     const double v = (double)x[k];
@@ -456,12 +461,14 @@ void ref_dql(const float *x, int64_t n, uint8_t *y, float *scale_out,
       q = zp;
     } else {
       const float r = (float)((double)x[k] / scale);
+      if (!isfinite(r)) return REF_ERR_UNSUPPORTED; /* toInt() of NaN / inf */
       q = round_even((double)r) + zp;
     }
     y[k] = (uint8_t)(q < 0 ? 0 : (q > 255 ? 255 : q));
   }
   *scale_out = scale_f;
   *zp_out = zp;
+  return REF_OK;
 }
 
 /* ------------------------------------------------------------------------ */

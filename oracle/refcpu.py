@@ -23,6 +23,7 @@ _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
+REF_ERR_UNSUPPORTED = -2  # refcpu.c: the reference throws UnsupportedError
 
 
 def build():
@@ -52,7 +53,7 @@ def lib():
         L.ref_matmul_kernel.restype = ctypes.c_int
         L.ref_dql.argtypes = [_f32p, _i64, _u8p, ctypes.POINTER(ctypes.c_float),
                               ctypes.POINTER(ctypes.c_int64)]
-        L.ref_dql.restype = None
+        L.ref_dql.restype = ctypes.c_int
         L.ref_matmul_integer.argtypes = [_u8p, ctypes.c_int, _i64, _i64, _i64,
                                          _u8p, ctypes.c_int, _i64, _i64,
                                          _vp, _i64, _vp, _i64, _i64p]
@@ -146,7 +147,10 @@ def dynamic_quantize_linear(x):
     y = np.zeros(xf.size, dtype=np.uint8)
     sc = ctypes.c_float(0.0)
     zp = ctypes.c_int64(0)
-    lib().ref_dql(xf, xf.size, y, ctypes.byref(sc), ctypes.byref(zp))
+    rc = lib().ref_dql(xf, xf.size, y, ctypes.byref(sc), ctypes.byref(zp))
+    if rc == REF_ERR_UNSUPPORTED:
+        # the reference's _roundEven calls toInt() on a NaN / infinite quotient
+        raise NotImplementedError("DynamicQuantizeLinear: NaN or infinite input")
     return y.reshape(x.shape), np.float32(sc.value), int(zp.value)
 
 

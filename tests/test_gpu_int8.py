@@ -1,5 +1,7 @@
 """GPU parity of DynamicQuantizeLinear and MatMulInteger (+ the fused
 fp32 rescale) against the CPU oracle: bit-exact."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -63,6 +65,34 @@ def test_dql_many_scales_match_double_sequence(ctx):
     for _ in range(40):
         x = (rng.standard_normal(333) * rng.uniform(1e-3, 1e3)).astype(np.float32)
         dql_check(ctx, x)
+
+
+@pytest.mark.parametrize("n", [5, 1000, 70001])
+def test_dql_non_finite_input_is_rejected(ctx, n):
+    # the reference's _roundEven throws on a NaN / infinite quotient
+    # (onnx_ops.dart:2490-2497, :2574-2576): the host entry point returns
+    # MMNB_ERR_UNSUPPORTED (NotImplementedError), like the oracle; the device
+    # form writes a NaN scale as its marker
+    rng = np.random.default_rng(n)
+    for pos, bad in ((0, np.nan), (n - 1, np.inf), (n // 2, -np.inf)):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[pos] = bad
+        with pytest.raises(NotImplementedError):
+            refcpu.dynamic_quantize_linear(x)
+        with pytest.raises(NotImplementedError):
+            ops.op_dynamic_quantize_linear(x, ctx=ctx)
+        dx, dy, dsz = ctx.to_device(x), ctx.alloc(n), ctx.alloc(8)
+        _lib.check(ctx.lib.mmnb_dynamic_quantize_linear_dev(ctx.handle, dx.ptr, n, dy.ptr,
+                                                            dsz.ptr,
+                                                            ctypes.c_void_p(dsz.ptr.value + 4)))
+        ctx.synchronize()
+        assert np.isnan(dsz.numpy(np.float32, (2,))[0])
+        for bf in (dx, dy, dsz):
+            bf.free()
+    # NaN among zeros: scale 0, nothing rounded, zp everywhere (no error)
+    x = np.zeros(n, np.float32)
+    x[n // 3] = np.nan
+    dql_check(ctx, x)
 
 
 def test_dql_empty(ctx):

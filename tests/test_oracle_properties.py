@@ -140,6 +140,43 @@ def test_dequant_closed_forms():
     np.testing.assert_array_equal(w, (q - np.array([[1], [2], [3]])).T.astype(np.float32))
 
 
+@pytest.mark.parametrize("bs", [2, 6, 8, 10, 24, 48, 1000])
+@pytest.mark.parametrize("zp", [False, True])
+def test_dequant_any_even_block_closed_form(bs, zp):
+    # For an even block_size a column's bytes are its k run, two to a byte
+    # (byte blk*bs/2 + j/2 holds k = blk*bs + j, low nibble even), so
+    # W[k, n] = (q[n, k] - zp[n, k // bs]) * scale[n, k // bs] with the
+    # partial last block clipped at K (onnx_qlinear_ops.dart:120-146).
+    rng = np.random.default_rng(bs)
+    k, n = 77, 9
+    nb = -(-k // bs)
+    b = rng.integers(0, 256, (n, nb, bs // 2), dtype=np.uint8)
+    s = rng.uniform(0.01, 2.0, (n, nb)).astype(np.float32)
+    z = rng.integers(0, 256, ((n * nb + 1) // 2,), dtype=np.uint8) if zp else None
+    w = refcpu.dequant(b, s, z, k, n, bs)
+    q = np.stack([b & 0xF, b >> 4], axis=-1).reshape(n, nb * bs)[:, :k].astype(np.int64)
+    blk = np.arange(k) // bs
+    if zp:
+        zi = np.arange(n)[:, None] * nb + blk[None, :]
+        zg = ((z[zi >> 1] >> (4 * (zi & 1))) & 0xF).astype(np.int64)
+    else:
+        zg = 8
+    want = ((q - zg).astype(np.float64) * s[:, blk].astype(np.float64)).astype(np.float32).T
+    np.testing.assert_array_equal(w, want)
+    # and the op is that W through the Dart GEMM order, M = 1 and M > 1
+    for m in (1, 3):
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        np.testing.assert_array_equal(refcpu.matmul_nbits(a, b, s, z, k, n, 4, bs),
+                                      refcpu.matmul_kernel(a, want, m, k, n))
+
+
+def test_odd_block_size_rejected():
+    # blob = bs ~/ 2 bytes cannot hold bs nibbles: the oracle refuses odd sizes
+    with pytest.raises(refcpu.OracleError):
+        refcpu.matmul_nbits(np.zeros((1, 9), np.float32), np.zeros((1, 3, 1), np.uint8),
+                            np.ones(3, np.float32), None, 9, 1, 4, 3)
+
+
 def test_partial_block_ignores_padding_nibbles():
     rng = np.random.default_rng(4)
     k, n, bs = 40, 5, 32
@@ -204,6 +241,19 @@ def test_dql_special_ranges():
     assert zp == 0 and y[-1] == 255
     y, scale, zp = refcpu.dynamic_quantize_linear(np.zeros(0, np.float32))
     assert y.size == 0 and scale == 0.0 and zp == 0
+
+
+def test_dql_non_finite_input_raises_like_the_reference():
+    # _roundEven (onnx_ops.dart:2490-2497) calls toInt() on floor(v); a NaN or
+    # infinite quotient x / scale makes it throw UnsupportedError.  With an
+    # infinity in x the scale is infinite and inf / inf is NaN; a NaN in x
+    # gives a NaN quotient whenever scale != 0.
+    for x in ([1.0, np.nan, -2.0], [np.inf, 1.0], [-np.inf], [0.5, -np.inf, np.nan]):
+        with pytest.raises(NotImplementedError):
+            refcpu.dynamic_quantize_linear(np.array(x, np.float32))
+    # NaN among zeros: scale 0, nothing is rounded, every y is zp = 0
+    y, scale, zp = refcpu.dynamic_quantize_linear(np.array([0.0, np.nan, 0.0], np.float32))
+    assert scale == 0.0 and zp == 0 and not y.any()
 
 
 def test_dql_scale_uses_double_sequence():
