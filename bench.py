@@ -620,6 +620,23 @@ def cpu_baseline(synth, budget_s):
     return out
 
 
+PROFILE_CALLS = 200
+EXTRAS = ["gemv_bs32_zp", "c1_gemv", "gemv_large", "gemm", "int8", "decode_sweep", "qlinear",
+          "nbits_ex", "decoder", "platform"]
+
+
+def profile_calls(ctx, call):
+    """The two eager passes of time_mmnb, for a tracer: PROFILE_CALLS calls
+    each launched on an idle GPU (the host waits after every call), then
+    PROFILE_CALLS calls enqueued without waiting.  No HIP graphs."""
+    for i in range(PROFILE_CALLS):
+        call(i)
+        ctx.synchronize()
+    for i in range(PROFILE_CALLS):
+        call(i)
+    ctx.synchronize()
+
+
 def profile_pass(ctx, lib, ops, synth, kind):
     """Kernels for a rocprofv3 counter run: one operator workload and a copy
     of known size (the calibration reference for FETCH_SIZE / WRITE_SIZE)."""
@@ -629,10 +646,10 @@ def profile_pass(ctx, lib, ops, synth, kind):
         packs = make_packs(ctx, ops, synth, m, k, n, bs, False, count, 1)
         da = ctx.to_device(synth.activations(m, k, 1))
         dy = ctx.alloc(m * n * 4)
-        for i in range(100):
-            lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, packs[i % count].handle, da.ptr,
-                                                    m, dy.ptr))
-        what = f"100 GEMV calls ({mmnb_bytes(m, k, n, bs, False)} algorithmic bytes each)"
+        profile_calls(ctx, lambda i: lib.check(ctx.lib.mmnb_matmul_nbits_dev(
+            ctx.handle, packs[i % count].handle, da.ptr, m, dy.ptr)))
+        what = (f"GEMV calls over {count} rotated packs ({mmnb_bytes(m, k, n, bs, False)} "
+                f"algorithmic bytes each): {PROFILE_CALLS} isolated, then {PROFILE_CALLS} queued")
     elif kind == "gemv_large":
         # eager dispatches with gaps between them, then graph replays back
         # to back: a kernel trace shows the duration of both
@@ -649,9 +666,10 @@ def profile_pass(ctx, lib, ops, synth, kind):
                               block_size=bs, ctx=ctx)
         da = ctx.to_device(p.a)
         dy = ctx.alloc(m * n * 4)
-        for _ in range(20):
-            lib.check(ctx.lib.mmnb_matmul_nbits_dev(ctx.handle, pack.handle, da.ptr, m, dy.ptr))
-        what = "20 GEMM calls (M=512 K=N=4096 block 32, zero points)"
+        profile_calls(ctx, lambda i: lib.check(ctx.lib.mmnb_matmul_nbits_dev(
+            ctx.handle, pack.handle, da.ptr, m, dy.ptr)))
+        what = (f"GEMM calls (M=512 K=N=4096 block 32, zero points; k_prep_a + k_gemm_mfma "
+                f"each): {PROFILE_CALLS} isolated, then {PROFILE_CALLS} queued")
     elif kind == "decoder":
         from onnx_runtime_dart_amd import decoder as G
         cfg = G.QWEN3_0_6B
@@ -691,6 +709,11 @@ def main():
                     help="timed steps (one step = one call on each rotated weight pack)")
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="headline only, no extras")
+    ap.add_argument("--extras", default=",".join(EXTRAS),
+                    help="comma-separated extra workloads after the headline (default: all "
+                         "of " + ",".join(EXTRAS) + ")")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline (the line then carries no cpu_baseline)")
     ap.add_argument("--cpu-budget", type=float, default=16.0,
                     help="seconds of host time for the CPU baseline legs")
     ap.add_argument("--profile", action="store_true",
@@ -699,9 +722,10 @@ def main():
                          "the counter calibration")
     ap.add_argument("--profile-kind", default="gemv",
                     choices=["gemv", "gemv_large", "gemm", "int8", "decoder"],
-                    help="gemv: headline GEMV, 100 calls over the rotated packs; "
-                         "gemv_large: K=N=16384, graph replays and eager dispatches; gemm: "
-                         "M=512 K=N=4096 block 32 with zero points, 20 calls; int8: the "
+                    help="gemv: headline GEMV, 200 isolated then 200 queued calls over the "
+                         "rotated packs; gemv_large: K=N=16384, graph replays and eager "
+                         "dispatches; gemm: M=512 K=N=4096 block 32 with zero points, 200 "
+                         "isolated then 200 queued calls; int8: the "
                          "DQL -> MatMulInteger -> rescale chain, 50 calls; decoder: the "
                          "Qwen3-shaped decoder, 256-token prefill + 64 steps, eager")
     args = ap.parse_args()
@@ -765,30 +789,40 @@ def main():
                                    "frac": round(head["sustained_gbs"] / HBM_PEAK_GBS, 4),
                                    "launches": head["calls"]}},
     }
-    if not args.quick:
-        try:
+    extras = [] if args.quick else [e for e in args.extras.split(",") if e]
+    unknown = [e for e in extras if e not in EXTRAS]
+    if unknown:
+        print(f"unknown extras {unknown}; choose from {EXTRAS}", file=sys.stderr)
+        sys.exit(2)
+    try:
+        if "gemv_bs32_zp" in extras:
             out["gemv_bs32_zp"] = bench_gemv(ctx, lib, ops, synth, 1, 4096, 4096, 32, True,
                                              args.steps, args.warmup, seed=3)
             print(f"# GEMV bs32+zp: {out['gemv_bs32_zp']['sustained_gbs']:.0f} GB/s back to back",
                   file=sys.stderr, flush=True)
+        if "c1_gemv" in extras:
             out["c1_gemv"] = bench_gemv(ctx, lib, ops, synth, 1, 1024, 1024, 32, True, 20, 3,
                                         seed=5)
             print(f"# C1 GEMV M=1 K=N=1024 bs32+zp: {out['c1_gemv']['ms_per_call'] * 1e3:.2f} us "
                   f"per call, {out['c1_gemv']['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+        if "gemv_large" in extras:
             out["gemv_large"] = bench_gemv(ctx, lib, ops, synth, 1, 16384, 16384, 128,
                                            False, 20, 3, seed=4)
             print(f"# GEMV K=N=16384: {out['gemv_large']['sustained_gbs']:.0f} GB/s back to back",
                   file=sys.stderr, flush=True)
+        if "gemm" in extras:
             out["gemm"] = bench_gemm(ctx, lib, ops, synth, 512, 4096, 4096, 32, True,
                                      200, 20)
             print(f"# GEMM M=512: {out['gemm']['tflops']:.1f} TFLOP/s op back to back, kernel "
                   f"median dispatch {out['gemm']['roofline']['achieved']:.1f}",
                   file=sys.stderr, flush=True)
+        if "int8" in extras:
             out["int8"] = bench_int8(ctx, lib, ops, synth, 20, 3)
             print(f"# int8 chain: {out['int8']['ms_per_chain'] * 1e3:.1f} us "
                   f"(fused, no int32 output: {out['int8']['fused']['ms_per_chain'] * 1e3:.1f} us;"
                   f" DQL {out['int8']['dql_us']:.1f} us, MatMulInteger "
                   f"{out['int8']['mmi_us']:.1f} us)", file=sys.stderr, flush=True)
+        if "decode_sweep" in extras:
             sweep = []
             for m in (1, 4, 8):
                 for (k, n) in synth.DECODE_PROJECTIONS:
@@ -797,18 +831,23 @@ def main():
                                                        "dispatch_gbs", "bytes_per_call")})
             out["decode_sweep"] = sweep
             print("# decode sweep done", file=sys.stderr, flush=True)
+        if "qlinear" in extras:
             out["qlinear"] = bench_qlinear(ctx, lib, ops)
             print(f"# qlinear: {json.dumps(out['qlinear'])[:300]}", file=sys.stderr, flush=True)
+        if "nbits_ex" in extras:
             out["nbits_ex"] = bench_nbits_ex(ctx, lib, ops)
             print(f"# nbits_ex: {json.dumps(out['nbits_ex'])[:300]}", file=sys.stderr, flush=True)
+        if "decoder" in extras:
             out["decoder"] = bench_decoder(ctx, lib)
             print(f"# decoder: decode {out['decoder']['decode_tok_s']:.0f} tok/s, prefill "
                   f"{out['decoder']['prefill_tok_s']:.0f} tok/s", file=sys.stderr, flush=True)
+        if "platform" in extras:
             out["platform"] = bench_platform(ctx, lib)
             print(f"# platform: {out['platform']}", file=sys.stderr, flush=True)
-        except Exception as e:  # extras must not hide the headline
-            out["extras_error"] = repr(e)
-    out["cpu_baseline"] = cpu_baseline(synth, args.cpu_budget if not args.quick else 6.0)
+    except Exception as e:  # extras must not hide the headline
+        out["extras_error"] = repr(e)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(synth, args.cpu_budget if not args.quick else 6.0)
     print(json.dumps(out), flush=True)
 
 

@@ -100,8 +100,10 @@ struct mmnb_ctx {
   // MatMulInteger row tile (32 or 64; 0 = by shape), from MMNB_MMI_TM.
   int mmi_tm = 0;
   // Device address of this device's fixed workspace for
-  // mmnb_matmul_nbits_dev_noalloc (set by noalloc_setup at init).
+  // mmnb_matmul_nbits_dev_noalloc (set by noalloc_setup at init), and why it
+  // is null if the lookup failed.
   void *noalloc_ws = nullptr;
+  std::string noalloc_err;
 };
 
 struct mmnb_pack {

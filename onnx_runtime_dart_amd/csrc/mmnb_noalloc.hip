@@ -59,7 +59,8 @@ int mmnb_matmul_nbits_dev_noalloc(mmnb_ctx *ctx, const mmnb_pack *pack, const fl
   if (m < 0) return fail(MMNB_ERR_ARG, "MatMulNBits: negative M");
   if (m == 0) return MMNB_OK;
   if (!d_a || !d_y) return fail(MMNB_ERR_ARG, "MatMulNBits: null buffer");
-  if (!ctx->noalloc_ws) return fail(MMNB_ERR_DEVICE, "no-alloc workspace not set up");
+  if (!ctx->noalloc_ws)
+    return fail(MMNB_ERR_DEVICE, "no-alloc workspace not set up: " + ctx->noalloc_err);
   CtxLock lk(ctx);
   int rc = set_device(ctx);
   if (rc) return rc;

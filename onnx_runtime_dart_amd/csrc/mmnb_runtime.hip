@@ -158,9 +158,13 @@ int mmnb_init(int device, mmnb_ctx **out) {
     delete ctx;
     return check_hip(e, "hipMalloc(pad page, GEMM counters)");
   }
-  if (int rc = noalloc_setup(ctx)) {
-    (void)mmnb_shutdown(ctx);  // no packs yet: releases everything above
-    return rc;
+  // The fixed workspace serves only mmnb_matmul_nbits_dev_noalloc: when it
+  // cannot be resolved the context still opens, and that entry point reports
+  // the reason (kept here) on every call.
+  if (noalloc_setup(ctx) != MMNB_OK) {
+    ctx->noalloc_ws = nullptr;
+    ctx->noalloc_err = mmnb_last_error();
+    (void)hipGetLastError();  // clear the sticky HIP error of the failed lookup
   }
   *out = ctx;
   return MMNB_OK;

@@ -95,3 +95,55 @@ def test_noalloc_rejects_oversized_and_extended(ctx):
         da.free()
         dy.free()
         xp.free()
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    # A fresh context (no scratch ever grown) whose FIRST MatMulNBits calls
+    # are made under HIP graph capture through the no-alloc entry point: a
+    # K-sliced GEMM (tile counters in the workspace, cleared by the prep
+    # kernel) and an M <= 8 call that falls back to the GEMM (rows too long
+    # for the multi-row GEMV's LDS; a GEMM of more than 64 KB of LDS, so a
+    # hipFuncSetAttribute while capturing).  Nothing may allocate during capture; every replay,
+    # with eager work and synchronisations in between, must give the bits of
+    # mmnb_matmul_nbits_dev run outside capture.
+    c = _lib.Context(0)
+    cases = [(100, 4096, 512, 32, True), (5, 8192, 40, 64, True)]
+    packs, bufs = [], []
+    try:
+        for m, k, n, block, zp in cases:
+            p = synth.mmnb_problem(m, k, n, block, zp, seed=k + m)
+            pk = ops.pack_nbits(p.b_q, p.scales, p.zero_points, k=k, n=n, bits=4,
+                                block_size=block, ctx=c)
+            da, dy = c.to_device(p.a), c.alloc(m * n * 4)
+            packs.append(pk)
+            bufs.append((m, n, da, dy))
+        c.synchronize()
+        c.graph_begin()
+        for pk, (m, n, da, dy) in zip(packs, bufs):
+            _lib.check(c.lib.mmnb_matmul_nbits_dev_noalloc(c.handle, pk.handle, da.ptr, m,
+                                                            dy.ptr))
+        g = c.graph_end()
+        try:
+            want = []
+            for pk, (m, n, da, dy) in zip(packs, bufs):
+                want.append(_run(c, c.lib.mmnb_matmul_nbits_dev, pk, da.numpy(np.float32,
+                                                                              (m, pk.k))))
+            for rep in range(3):
+                for (m, n, da, dy) in bufs:
+                    dy.upload(np.full((m, n), np.nan, np.float32))
+                c.graph_launch(g)
+                c.synchronize()
+                for w, (m, n, da, dy) in zip(want, bufs):
+                    np.testing.assert_array_equal(dy.numpy(np.float32, (m, n)), w, err_msg=str(rep))
+                # eager work between replays (the entry points outside the graph)
+                _run(c, c.lib.mmnb_matmul_nbits_dev_noalloc, packs[0],
+                     bufs[0][2].numpy(np.float32, (bufs[0][0], packs[0].k)))
+        finally:
+            c.graph_destroy(g)
+    finally:
+        for (m, n, da, dy) in bufs:
+            da.free()
+            dy.free()
+        for pk in packs:
+            pk.free()
+        c.close()
