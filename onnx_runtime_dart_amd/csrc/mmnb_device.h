@@ -19,6 +19,24 @@ __device__ __forceinline__ void dma16(const void *g, void *lds) {
   __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
 }
 
+// Buffer resource over raw bytes at base (no range limit: callers clamp
+// their offsets; 32-bit data format, so loads return the bytes as stored).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, 0x00020000);
+}
+
+// 16-byte global->LDS DMA through a buffer resource (buffer_load_dwordx4
+// ... lds): lane l's 16 bytes at base + voff + soff land at lds + 16 l (lds
+// wave-uniform).  The compiler counts it on vmcnt only, so LDS reads issued
+// after it keep in-order lgkmcnt waits; after the FLAT form
+// (global_load_lds) it waits for every outstanding LDS read (lgkmcnt(0))
+// before their first use.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                          void *lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                           voff, soff, 0, 0);
+}
+
 // v + (v moved by the DPP control CTRL), every lane.
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {

@@ -117,8 +117,10 @@ struct mmnb_pack {
   uint8_t *d_w = nullptr;
   float *d_scales = nullptr;
   uint8_t *d_zp = nullptr;  // packed uint4; 0x88 filler when the op has none
-  // block-major copies for the prefill GEMM: scales [nb][ldsz], zero points
-  // [nb][ldsz], ldsz = n rounded up to 4 (padding zero)
+  // block-major copies for the prefill GEMM, one allocation of rows
+  // [nb][2][ldsz] (scales, then the zero points as dwords), ldsz = n rounded
+  // up to 4 (padding zero): d_st is the allocation, d_zt = d_st + ldsz inside
+  // it (both with row stride 2 ldsz)
   float *d_st = nullptr;
   uint32_t *d_zt = nullptr;
   int64_t ldsz = 0;

@@ -104,38 +104,39 @@ int repack_nbits_weights(mmnb_ctx *ctx, const uint8_t *d_src, int64_t n, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// Block-major copies of the scales and zero points for the prefill GEMM:
-// st[b][c] = scales[c][b], zt[b][c] = zero-point nibble (c, b) as a dword, so
-// the columns of one quantisation block that a GEMM tile stages are
-// contiguous (coalesced DMA) instead of nb apart.  One thread per (b, c).
+// Block-major copies of the scales and zero points for the prefill GEMM, in
+// one buffer of rows [nb][2][ld]: row 2b holds scales[c][b], row 2b + 1 the
+// zero-point nibble (c, b) as a dword, so the columns of one quantisation
+// block that a GEMM tile stages are contiguous (coalesced DMA) instead of nb
+// apart, and one buffer resource covers both.  One thread per (b, c).
 // ---------------------------------------------------------------------------
 __global__ void k_sz_block_major(const float *__restrict__ S, const uint8_t *__restrict__ Z,
-                                 int64_t n, int64_t nb, int64_t ld, float *__restrict__ st,
-                                 uint32_t *__restrict__ zt) {
+                                 int64_t n, int64_t nb, int64_t ld, uint32_t *__restrict__ stz) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= ld * nb) return;
   const int64_t b = idx / ld, c = idx % ld;
+  uint32_t *row = stz + 2 * b * ld;
   if (c >= n) {  // row padding
-    st[idx] = 0.0f;
-    zt[idx] = 0u;
+    row[c] = 0u;
+    row[ld + c] = 0u;
     return;
   }
   const int64_t zi = c * nb + b;
-  st[idx] = S[zi];
-  zt[idx] = (uint32_t)(Z[zi >> 1] >> (4 * (zi & 1))) & 0xFu;
+  row[c] = __builtin_bit_cast(uint32_t, S[zi]);
+  row[ld + c] = (uint32_t)(Z[zi >> 1] >> (4 * (zi & 1))) & 0xFu;
 }
 
 int build_gemm_sz(mmnb_ctx *ctx, mmnb_pack *p) {
   p->ldsz = (p->n + 3) / 4 * 4;
   const int64_t total = p->ldsz * p->n_blocks;
   int rc;
-  if ((rc = device_alloc((size_t)total * 4, (void **)&p->d_st))) return rc;
-  if ((rc = device_alloc((size_t)total * 4, (void **)&p->d_zt))) return rc;
+  if ((rc = device_alloc((size_t)total * 8, (void **)&p->d_st))) return rc;
+  p->d_zt = (uint32_t *)(p->d_st + p->ldsz);  // inside d_st (not freed on its own)
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
   return launch(ctx, kKernRepack, k_sz_block_major, dim3((unsigned)blocks), dim3(threads), 0,
                 (const float *)p->d_scales, (const uint8_t *)p->d_zp, p->n, p->n_blocks,
-                p->ldsz, p->d_st, p->d_zt);
+                p->ldsz, (uint32_t *)p->d_st);
 }
 
 // (a & mask) | orv in one VALU op.  gfx9 VOP3 takes no literal, so the
@@ -1011,8 +1012,13 @@ static int launch_prep_a(mmnb_ctx *ctx, const float *d_a, int64_t lda, int64_t m
 // Every operand of a 64-k segment -- the prepared activations (16 KB), the
 // packed weights (128*CB columns x 32 B), the tile's scales and zero points
 // (from block-major copies, so one block's columns are contiguous and move
-// as 16 B per lane) -- is copied by global_load_lds into one of NST LDS
-// stages, so NST-1 segments are in flight without a register round trip.
+// as 16 B per lane) -- is copied by buffer_load_dwordx4 ... lds into one of
+// NST LDS stages, so NST-1 segments are in flight without a register round
+// trip.  (The buffer form rather than global_load_lds: after a pending FLAT
+// DMA the compiler waits for every outstanding LDS read before the first
+// MFMA of a matrix phase; with buffer loads it waits per fragment.  M = 512,
+// K = N = 4096 kernel, one box: block 128 39.7 -> 36.5 us, block 32
+// 41.0 -> 40.8 us.)
 // Every thread issues the same number of DMA loads per stage (kL), so "stage
 // s has landed" is vmcnt <= (NST-2)*kL once the next stages are issued; a
 // barrier then publishes the stage to all waves.
@@ -1075,22 +1081,26 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   // round trip after the K loop)
   const int rexp = row_exp[min(rb0 * 32 + lane, M - 1)];
 
-  // DMA sources.  Activations: thread's unit pieces idx = tid + 256 i
-  // (unit idx/64 = row block (idx/64)/8, step*2+part (idx/64)%8); the
-  // prepared buffer holds segsp segments, zero past K.
-  const uint4 *a_base = Ap + (size_t)rb0 * segsp * 8 * 64;
-  int a_off[4];
+  // DMA sources, as buffer resources of the tile's operands with per-lane
+  // byte offsets (the stage's part in the scalar offset).  Activations:
+  // thread's unit pieces idx = tid + 256 i (unit idx/64 = row block
+  // (idx/64)/8, step*2+part (idx/64)%8); the prepared buffer holds segsp
+  // segments of 8 KB per row block, zero past K.
+  const __amdgpu_buffer_rsrc_t a_rs = buf_rsrc(Ap + (size_t)rb0 * segsp * 8 * 64);
+  uint32_t a_off[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int idx = tid + 256 * i;
     const int u = idx >> 6;
-    a_off[i] = ((u >> 3) * segsp * 8 + (u & 7)) * 64 + (idx & 63);
+    a_off[i] = (uint32_t)(((u >> 3) * segsp * 8 + (u & 7)) * 64 + (idx & 63)) * 16u;
   }
-  const uint8_t *w_base[CB];
+  // nibbles: columns n0 .. (clamped to N - 1), 32 bytes per segment
+  const __amdgpu_buffer_rsrc_t w_rs = buf_rsrc(W + (size_t)n0 * col_bytes);
+  uint32_t w_off[CB];
 #pragma unroll
   for (int i = 0; i < CB; i++) {
     const int wcol = min(n0 + 128 * i + (tid >> 1), N - 1);
-    w_base[i] = W + (size_t)wcol * col_bytes + (tid & 1) * 16;
+    w_off[i] = (uint32_t)((wcol - n0) * col_bytes) + (tid & 1) * 16u;
   }
   // Scale / zero-point dword slots of a stage: [0, kSz) scales, [kSz, 2 kSz)
   // zero points, each indexed (block q, column c) as q * kBN + c.  They move
@@ -1098,6 +1108,9 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   // from the block-major copies, whose rows are ldsz = N rounded up to 4
   // apart): wave w loads chunks w, w + 4, ... of the 2 kSz / 256; with fewer
   // chunks than waves the extra waves repeat one (same data, same place).
+  // Both copies live in one buffer of rows [nb][2][ldsz] (ST = its start,
+  // ZT = ST + ldsz): a lane's 16 bytes of block b2 sit at dword
+  // (2 b2 + zp) ldsz + column.
   constexpr int kSzChunks = 2 * kSz / 256;
   int sz_col[kSzI], sz_q[kSzI], sz_chunk[kSzI];
   bool sz_isz[kSzI];
@@ -1107,7 +1120,7 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     int slot = sz_chunk[i] * 256 + 4 * lane;
     sz_isz[i] = slot >= kSz;
     if (sz_isz[i]) slot -= kSz;
-    sz_col[i] = min(n0 + slot % kBN, ldsz - 4);
+    sz_col[i] = min(n0 + slot % kBN, ldsz - 4) + (sz_isz[i] ? ldsz : 0);
     sz_q[i] = slot / kBN;
   }
 
@@ -1128,22 +1141,21 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     uint4 *st = smem + buf * kStageU4;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      __builtin_amdgcn_global_load_lds(a_base + a_off[i] + sa_ * 512, st + 256 * i + 64 * wave,
-                                       16, 0, 0);
+      dma16_buf(a_rs, a_off[i], (uint32_t)sa_ * 8192u, st + 256 * i + 64 * wave);
 #pragma unroll
-    for (int i = 0; i < CB; i++) {
-      const uint8_t *wsrc = w_base[i] + sg * kSegBytes;
-      __builtin_amdgcn_global_load_lds(wsrc, st + 1024 + 256 * i + 64 * wave, 16, 0, 0);
-    }
+    for (int i = 0; i < CB; i++)
+      dma16_buf(w_rs, w_off[i], (uint32_t)sg * kSegBytes, st + 1024 + 256 * i + 64 * wave);
+    // the stage's first block (clamped; a lane's block lies 0 .. NBPS - 1
+    // rows below it) rides in the resource, so offsets stay within a few rows
+    const int blk0 = min((sa_ * kSegK) >> bs_log2, nb - 1);
+    const __amdgpu_buffer_rsrc_t sz_rs = buf_rsrc(ST + (size_t)blk0 * 2 * ldsz);
     uint32_t *sz = (uint32_t *)(st + kSOff);
 #pragma unroll
     for (int i = 0; i < kSzI; i++) {
       const int blk = (sa_ * kSegK + sz_q[i] * (kSegK / NBPS)) >> bs_log2;
       const int b2 = blk < nb ? blk : nb - 1;
-      const size_t zi = (size_t)b2 * ldsz + sz_col[i];
-      const void *src = sz_isz[i] ? (const void *)(ZT + zi) : (const void *)(ST + zi);
-      uint32_t *dst = sz + 256 * sz_chunk[i];
-      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      dma16_buf(sz_rs, (uint32_t)((b2 - blk0) * 2 * ldsz + sz_col[i]) * 4u, 0u,
+                sz + 256 * sz_chunk[i]);
     }
   };
 
@@ -1222,30 +1234,29 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
     };
     auto mphase = [&](const int b) __attribute__((always_inline)) {
       const u4vec *sAv = (const u4vec *)(smem + b * kStageU4);
-      half8_t af[4][2][2];
+      // The 16 MFMAs in a fixed order, and the A fragments read in that same
+      // order, so each MFMA waits only for its own read (LDS reads return in
+      // order; the DMA goes through buffer loads, which the compiler counts
+      // on vmcnt, so it keeps the waits incremental).  MFMA i takes step
+      // J(i), row block RB(i), part H(i): with two or more blocks per stage
+      // steps j and j + 2 (different blocks) go together, so four
+      // accumulators alternate and a dependent MFMA issues four after its
+      // predecessor; with one block, the two row blocks alternate.
+      auto J = [](int i) { return NBPS >= 2 ? i / 8 + 2 * ((i >> 1) & 1) : i / 4; };
+      auto H = [](int i) { return NBPS >= 2 ? (i >> 2) & 1 : (i >> 1) & 1; };
+      half8_t af[16];
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int i = 0; i < 16; i++) {
+        af[i] = __builtin_bit_cast(half8_t, sAv[((i & 1) * 8 + J(i) * 2 + H(i)) * 64 + lane]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-          for (int h = 0; h < 2; h++)
-            af[j][rb][h] = __builtin_bit_cast(half8_t, sAv[(rb * 8 + j * 2 + h) * 64 + lane]);
-      // all 16 reads are issued before the first MFMA (one wait, then the
-      // MFMAs back to back) instead of the scheduler's read-wait-MFMA pairs
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int q = j / kJB;
-        const bool first = (j % kJB) == 0;
-#pragma unroll
-        for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-          for (int cb = 0; cb < CB; cb++) {
-            P[q][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                af[j][rb][0], bq[j][cb], first ? zero16 : P[q][rb][cb], 0, 0, 0);
-            P[q][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j][rb][1], bq[j][cb],
-                                                                  P[q][rb][cb], 0, 0, 0);
-          }
+      for (int i = 0; i < 16; i++) {
+        const int j = J(i), rb = i & 1, q = j / kJB;
+        const bool first = (j % kJB) == 0 && H(i) == 0;
+        P[q][rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bq[j][0],
+                                                             first ? zero16 : P[q][rb][0], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
     // the scheduler may not move any instruction across a phase boundary

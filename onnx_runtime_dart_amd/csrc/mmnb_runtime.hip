@@ -231,8 +231,7 @@ int mmnb::pack_nbits_core(mmnb_ctx *ctx, const uint8_t *b_q, const float *scales
     if (p->d_w) (void)hipFree(p->d_w);
     if (p->d_scales) (void)hipFree(p->d_scales);
     if (p->d_zp) (void)hipFree(p->d_zp);
-    if (p->d_st) (void)hipFree(p->d_st);
-    if (p->d_zt) (void)hipFree(p->d_zt);
+    if (p->d_st) (void)hipFree(p->d_st);  // d_zt lies inside it
     delete p;
     return code;
   };
@@ -622,8 +621,7 @@ int mmnb_pack_free(mmnb_pack *p) {
     if (p->d_w) (void)hipFree(p->d_w);
     if (p->d_scales) (void)hipFree(p->d_scales);
     if (p->d_zp) (void)hipFree(p->d_zp);
-    if (p->d_st) (void)hipFree(p->d_st);
-    if (p->d_zt) (void)hipFree(p->d_zt);
+    if (p->d_st) (void)hipFree(p->d_st);  // d_zt lies inside it
     if (p->d_bt) (void)hipFree(p->d_bt);
     if (p->d_colsum) (void)hipFree(p->d_colsum);
     if (p->d_ecol) (void)hipFree(p->d_ecol);
