@@ -670,8 +670,9 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 // slot).  LDS rows hold kMmiPieces 16-byte pieces; piece c of row r is
 // stored at slot c ^ (r & 15) so the 16 rows an MFMA operand read touches
 // land in 16 different bank groups.  Pieces past K (or rows past M) are read
-// from a constant page whose bytes become zero after the int8 offset.
-// Requires K % 16 == 0 and a 16-byte aligned A.
+// from clamped in-range addresses and A's pieces past K zeroed when read.
+// Requires K % 16 == 0 (K > 0), a 16-byte aligned A and per-batch operands
+// below 2 GB (31-bit buffer offsets).
 //
 // TM = 32 doubles the workgroups for the same output: L2 -> LDS streaming
 // rises with the waves per CU (three 48 KB workgroups fit a CU where two
@@ -709,11 +710,21 @@ __global__ __launch_bounds__(64 * WM * (TN / 32)) void k_mmi_lds(
   const int64_t mt0 = (int64_t)blockIdx.y * TM, nt0 = (int64_t)blockIdx.x * TN;
   const int r16 = lane & 15, q = lane >> 4;
   const uint32_t flip = a_signed ? 0u : 0x80808080u;
-  const uint8_t *apad = pad + (a_signed ? 0 : 1024);
   const int nchunks = (int)((kpad + kMmiKc - 1) / kMmiKc);
+  // the operands as buffer resources (the launcher keeps every offset below
+  // 2^31): DMA through buffer_load_dwordx4 ... lds, which the compiler
+  // counts on vmcnt only.  Through global_load_lds it waited vmcnt(0) before
+  // every step's LDS reads, i.e. for the next chunk's DMA too, so a
+  // workgroup never overlapped a chunk's MFMAs with the next chunk's DMA.
+  const __amdgpu_buffer_rsrc_t a_rs = buf_rsrc(Ab);
+  const __amdgpu_buffer_rsrc_t b_rs = buf_rsrc(Bb);
 
   // DMA of chunk c into slot s: instruction i of a wave fills LDS slots
-  // [64 i, 64 i + 64) of an operand.
+  // [64 i, 64 i + 64) of an operand.  Pieces past K (A) or past kpad (B),
+  // and rows past M, read clamped in-range bytes: A pieces past K are zeroed
+  // when read (so neither the products nor the row sums see them), which
+  // also cancels whatever B holds there; rows past M feed only rows that are
+  // not stored.
   auto issue = [&](int c, int s) {
     const int64_t k0 = (int64_t)c * kMmiKc;
 #pragma unroll
@@ -721,21 +732,18 @@ __global__ __launch_bounds__(64 * WM * (TN / 32)) void k_mmi_lds(
       const int i = wave + NW * u;
       const int slot = i * 64 + lane;
       const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
-      const int64_t kk = k0 + (int64_t)(cs_ ^ (r & 15)) * 16;
-      const int64_t arow = mt0 + r;
-      const uint8_t *ga = (arow < M && kk < K) ? Ab + arow * K + kk : apad;
-      dma16(ga, sA0 + s * kSA + i * 64);
+      const int64_t kk = min(k0 + (int64_t)(cs_ ^ (r & 15)) * 16, K - 16);
+      const int64_t arow = min(mt0 + r, M - 1);
+      dma16_buf(a_rs, (uint32_t)(arow * K + kk), 0u, sA0 + s * kSA + i * 64);
     }
 #pragma unroll
     for (int u = 0; u < kSB / 64 / NW; u++) {
       const int i = wave + NW * u;
       const int slot = i * 64 + lane;
       const int r = slot / kMmiPieces, cs_ = slot % kMmiPieces;
-      const int64_t kk = k0 + (int64_t)(cs_ ^ (r & 15)) * 16;
-      int64_t bcol = nt0 + r;
-      if (bcol >= N) bcol = N - 1;
-      const int8_t *gb = kk < kpad ? Bb + bcol * kpad + kk : (const int8_t *)pad;
-      dma16(gb, sB0 + s * kSB + i * 64);
+      const int64_t kk = min(k0 + (int64_t)(cs_ ^ (r & 15)) * 16, kpad - 16);
+      const int64_t bcol = min(nt0 + r, N - 1);
+      dma16_buf(b_rs, (uint32_t)(bcol * kpad + kk), 0u, sB0 + s * kSB + i * 64);
     }
   };
 
@@ -763,13 +771,23 @@ __global__ __launch_bounds__(64 * WM * (TN / 32)) void k_mmi_lds(
     const uint4 *sA = sA0 + s * kSA, *sB = sB0 + s * kSB;
     const int64_t kc = kpad - (int64_t)c * kMmiKc < kMmiKc ? kpad - (int64_t)c * kMmiKc
                                                             : kMmiKc;  // multiple of 64
+    // chunks reaching past K zero the A pieces there (clamped DMA sources)
+    const bool tail = (int64_t)(c + 1) * kMmiKc > K;
     for (int st = 0; st < kc / 64; st++) {
       int4v av[TI], bv[2];
+      uint32_t keep = ~0u;
+      if (tail) keep = (int64_t)c * kMmiKc + (st * 4 + q) * 16 < K ? ~0u : 0u;
+      // LDS reads as vector-type loads: read through the uint4 struct the
+      // compiler put vmcnt(0) (a wait for every outstanding DMA, the next
+      // chunk's too) before each step's reads; the ring's own vmcnt waits
+      // and barriers already order these reads after their chunk's DMA
+      const u32x4 *sAv = (const u32x4 *)sA, *sBv = (const u32x4 *)sB;
 #pragma unroll
       for (int t = 0; t < TI; t++) {
         const int ra = wm * (16 * TI) + t * 16 + r16;
-        const uint4 x = sA[ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
-        uint32_t w[4] = {x.x ^ flip, x.y ^ flip, x.z ^ flip, x.w ^ flip};
+        const u32x4 x = sAv[ra * kMmiPieces + ((st * 4 + q) ^ (ra & 15))];
+        uint32_t w[4] = {(x.x ^ flip) & keep, (x.y ^ flip) & keep, (x.z ^ flip) & keep,
+                         (x.w ^ flip) & keep};
 #pragma unroll
         for (int d = 0; d < 4; d++)
           rsum[t] = __builtin_amdgcn_sdot4((int)w[d], 0x01010101, rsum[t], false);
@@ -778,7 +796,7 @@ __global__ __launch_bounds__(64 * WM * (TN / 32)) void k_mmi_lds(
 #pragma unroll
       for (int t = 0; t < 2; t++) {
         const int rb = wn * 32 + t * 16 + r16;
-        const uint4 y = sB[rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
+        const u32x4 y = sBv[rb * kMmiPieces + ((st * 4 + q) ^ (rb & 15))];
         bv[t] = (int4v){(int)y.x, (int)y.y, (int)y.z, (int)y.w};
       }
 #pragma unroll
@@ -811,7 +829,10 @@ int launch_matmul_integer(mmnb_ctx *ctx, const mmnb_pack *p, const void *d_a, in
   MmiEpi o = out;
   o.ecol_bstride = p->ecol_bstride;
   if (m <= 0 || n <= 0 || batch <= 0) return MMNB_OK;
-  const int fast = (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0);
+  // the LDS-staged kernel: K a multiple of 16, a 16-byte aligned A, and
+  // per-batch operands small enough for 31-bit buffer offsets
+  const int fast = k > 0 && (k % 16 == 0) && ((((uintptr_t)d_a) & 15) == 0) &&
+                   m * k < ((int64_t)1 << 31) && n * p->kpad < ((int64_t)1 << 31);
   const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((m + 63) / 64), (unsigned)batch);
   if (fast && ctx->d_pad) {
     // 32-row tiles when 64-row ones would leave fewer than three workgroups
