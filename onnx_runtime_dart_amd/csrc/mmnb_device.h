@@ -11,14 +11,6 @@ namespace mmnb {
 // bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// 16-byte global->LDS DMA of one lane (global_load_lds_dwordx4): lane l's
-// 16 bytes from g land at lds + 16 l (lds wave-uniform).  A plain function
-// so that template kernels can use it: the builtin written directly in a
-// template kernel's body makes the host pass drop that kernel's launch stub.
-__device__ __forceinline__ void dma16(const void *g, void *lds) {
-  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
-}
-
 // Buffer resource over raw bytes at base (no range limit: callers clamp
 // their offsets; 32-bit data format, so loads return the bytes as stored).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
@@ -30,7 +22,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
 // wave-uniform).  The compiler counts it on vmcnt only, so LDS reads issued
 // after it keep in-order lgkmcnt waits; after the FLAT form
 // (global_load_lds) it waits for every outstanding LDS read (lgkmcnt(0))
-// before their first use.
+// before their first use.  Read the staged bytes through vector-type
+// pointers (ext_vector_type): a read through a HIP struct type (uint4) makes
+// the compiler wait for every outstanding LDS DMA (vmcnt(0)) first, the
+// prefetched stages' too.  The callers order their reads after the DMA they
+// need with their own vmcnt waits and barriers.  A plain function, so that
+// template kernels can use it (a DMA builtin written directly in a template
+// kernel's body made the host pass drop that kernel's launch stub).
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                           void *lds) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,

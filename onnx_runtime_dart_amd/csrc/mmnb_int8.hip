@@ -657,7 +657,7 @@ __global__ __launch_bounds__(256) void k_mmi_mfma(
 
 
 // MatMulInteger with LDS staging by direct global->LDS DMA
-// (global_load_lds_dwordx4, 16 B per lane, no VGPR round trip).  Workgroup
+// (buffer_load_dwordx4 ... lds, 16 B per lane, no VGPR round trip).  Workgroup
 // tile TM x TN, WM x (TN/32) waves, wave tile (TM/WM) x 32 of 16 x 16 MFMA
 // tiles, K steps of 64 as k_mmi_mfma.  The launcher uses 32 x 64 and 64 x 64
 // on 2 x 2 waves; 64 x 128 on 4 x 4 or 2 x 4 waves, 32 x 128, 64 x 64 on 4 x 2
