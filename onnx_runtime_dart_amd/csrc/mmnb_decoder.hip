@@ -641,6 +641,8 @@ __global__ __launch_bounds__(256) void k_dec_begin(DecState *__restrict__ st,
                                                    const float *__restrict__ cos,
                                                    const float *__restrict__ sin, int half,
                                                    int rows, float *__restrict__ rot) {
+  // every argument in SGPRs up front (one round of scalar loads)
+  kernarg_fence(st, table, H, vocab, x, cos, sin, half, rows, rot, blockDim.x);
   // the token comes from the previous step's argmax, always in range; the
   // clamp only keeps a corrupted state from reading outside the table
   int64_t tok = st->token;
@@ -677,6 +679,7 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
                                                   int nkeys, int32_t *__restrict__ out_tokens,
                                                   int out_cap) {
   __shared__ unsigned long long sk[16];
+  kernarg_fence(st, keys, nkeys, out_tokens, out_cap, blockDim.x);
   const int step = st->step, pos = st->pos;  // read now, not after the reduction
   unsigned long long best = 0ull;
   // eight keys in flight per thread (clamped: a repeated key leaves the
@@ -1025,6 +1028,10 @@ __global__ __launch_bounds__(256) void k_dec_attn(const DecState *__restrict__ s
                                                   DecAttnArgs a, int *counters) {
   __shared__ int s_last;
   const int split = blockIdx.x, kh = blockIdx.y;
+  // every argument the loads need in SGPRs up front (one round of scalar
+  // loads instead of dependent rounds ahead of the first load)
+  kernarg_fence(st, counters, a.qkv, a.nh, a.kvh, a.qn, a.kn, a.eps, a.rot, a.ck, a.cv, a.cap,
+                a.scale, a.part, a.nsmax, a.out);
   // the position through the vector memory path, used only once the
   // partial's loads are out: a scalar load would join the kernel-argument
   // loads' wait, in front of every other load

@@ -11,6 +11,21 @@ namespace mmnb {
 // bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima, i.e. no wait).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// Makes every value given (kernel arguments, the block size) live in SGPRs
+// at this point, so the compiler issues all their scalar loads at once,
+// ahead of the kernel's first memory access, and waits for them once: left
+// to itself it fetched a kernel's arguments in dependent rounds, each a
+// memory round trip, when control flow or the hidden block size split them.
+template <typename T>
+__device__ __forceinline__ void kernarg_fence(const T &v) {
+  asm volatile("" ::"s"(v));
+}
+template <typename T, typename... R>
+__device__ __forceinline__ void kernarg_fence(const T &v, const R &...rest) {
+  asm volatile("" ::"s"(v));
+  kernarg_fence(rest...);
+}
+
 // Buffer resource over raw bytes at base (no range limit: callers clamp
 // their offsets; 32-bit data format, so loads return the bytes as stored).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {

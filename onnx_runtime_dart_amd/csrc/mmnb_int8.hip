@@ -46,11 +46,15 @@ constexpr int kDqlUnroll = 2;
 __global__ __launch_bounds__(kDqlThreads) void k_dql_minmax(const float *__restrict__ x,
                                                             int64_t n,
                                                             float2 *__restrict__ part,
-                                                            int *__restrict__ part_nan) {
+                                                            int *__restrict__ part_nan,
+                                                            int nblocks) {
+  // every argument in SGPRs up front (one round of scalar loads; the grid
+  // size as an argument, gridDim.x being a vector load of the hidden ones)
+  kernarg_fence(x, n, part, part_nan, nblocks);
   float mn = 0.0f, mx = 0.0f;
   bool nan = false;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)nblocks * kDqlThreads;
+  const int64_t tid = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x;
   const bool vec = (((uintptr_t)x) & 15) == 0;
   int64_t done = 0;
   if (vec && n >= 4) {
@@ -120,13 +124,14 @@ __device__ __forceinline__ uint8_t dql_q(float v, float scale, int zp) {
 __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
     const float *__restrict__ x, int64_t n, const float2 *__restrict__ part,
     const int *__restrict__ part_nan, int nparts, uint8_t *__restrict__ y,
-    float *__restrict__ out_scale, int32_t *__restrict__ out_zp) {
+    float *__restrict__ out_scale, int32_t *__restrict__ out_zp, int nblocks) {
   __shared__ float2 s[kDqlThreads / 64];
   __shared__ int s_nan[kDqlThreads / 64];
   __shared__ float s_scale;
   __shared__ int s_zp;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  kernarg_fence(x, n, part, part_nan, nparts, y, out_scale, out_zp, nblocks);
+  const int64_t stride = (int64_t)nblocks * kDqlThreads;
+  const int64_t tid = (int64_t)blockIdx.x * kDqlThreads + threadIdx.x;
   const bool vec = ((((uintptr_t)x) & 15) == 0) && ((((uintptr_t)y) & 3) == 0);
   const int64_t n4 = (vec && n >= 4) ? n >> 2 : 0;
   const float4 *x4 = (const float4 *)x;
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(kDqlThreads) void k_dql_quant(
   }
   float mn = 0.0f, mx = 0.0f;
   bool nan = false;
-  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+  for (int i = threadIdx.x; i < nparts; i += kDqlThreads) {
     const float2 p = part[i];
     mn = p.x < mn ? p.x : mn;
     mx = p.y > mx ? p.y : mx;
@@ -227,14 +232,14 @@ int launch_dql(mmnb_ctx *ctx, const float *d_x, int64_t n, uint8_t *d_y, float *
   if (blocks < 1) blocks = 1;
   if (blocks > kDqlMaxBlocks) blocks = kDqlMaxBlocks;
   if ((rc = launch(ctx, kKernDqlMinmax, k_dql_minmax, dim3((unsigned)blocks), dim3(kDqlThreads),
-                    0, d_x, n, (float2 *)d_part, d_part_nan)))
+                    0, d_x, n, (float2 *)d_part, d_part_nan, (int)blocks)))
     return rc;
   int64_t qblocks = (n + per_block - 1) / per_block;
   if (qblocks < 1) qblocks = 1;
   if (qblocks > 4096) qblocks = 4096;
   return launch(ctx, kKernDqlQuant, k_dql_quant, dim3((unsigned)qblocks), dim3(kDqlThreads), 0,
                 d_x, n, (const float2 *)d_part, (const int *)d_part_nan, (int)blocks, d_y,
-                d_scale, d_zp);
+                d_scale, d_zp, (int)qblocks);
 }
 
 // ---------------------------------------------------------------------------
@@ -699,6 +704,9 @@ __global__ __launch_bounds__(64 * WM * (TN / 32)) void k_mmi_lds(
   // which the LDS epilogue reuses whole
   __shared__ uint4 smem[2 * (kSA + kSB)];
   uint4 *sA0 = smem, *sB0 = smem + 2 * kSA;
+  // the operand arguments in SGPRs up front (one round of scalar loads)
+  kernarg_fence(A, a_signed, a_bstride, M, K, Bt, b_bstride, kpad, colsum, cs_bstride, ecol, N,
+                azp, azp_len);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;

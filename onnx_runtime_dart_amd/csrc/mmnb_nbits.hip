@@ -208,6 +208,10 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void k_gemv_valu(
     const float *__restrict__ S, const uint8_t *__restrict__ Z, int nb, int bs_log2, int K,
     int N, float *__restrict__ Y, int C, int iters) {
   __shared__ float red[kGemvMaxWaves][2 * R];
+  // every kernel argument (and the block size) in SGPRs before anything
+  // else: left to itself the compiler fetched them in two dependent rounds
+  // of scalar loads ahead of the first weight load
+  kernarg_fence(A, W, col_bytes, S, Z, nb, bs_log2, K, N, Y, C, iters, blockDim.x);
   const int nw = blockDim.x >> 6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int h = l >> 5, t = l & 31;
@@ -366,6 +370,8 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   __shared__ float red[kDecMaxWaves][2 * R];
   __shared__ float nrm[kDecMaxWaves];
   __shared__ float outv[2 * R];
+  kernarg_fence(X, gamma, eps, W, col_bytes, S, nb, bs_log2, K, N, resid, Y, argmax, C,
+                blockDim.x);
   const int nw = blockDim.x >> 6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int h = l >> 5, t = l & 31;
@@ -600,6 +606,8 @@ __global__ __launch_bounds__(512) void k_gemv_lds(
     int vec) {
   extern __shared__ float4 sact[];
   __shared__ float red[8][M][2 * R];
+  kernarg_fence(A, lda, W, col_bytes, S, Z, nb, bs_log2, K, N, Y, C, kw, iters, groups, vec,
+                blockDim.x, gridDim.x);
   const int cs = 32 * kw * iters;  // staged chunk slots
   const int P = cs + 1;            // slot pitch (float4)
   const int nthr = blockDim.x;
@@ -918,15 +926,20 @@ constexpr int kPrepChunk = 4096;  // k per pass of a row's waves
 
 __global__ __launch_bounds__(64 * kPrepWaves) void k_prep_a(
     const float *__restrict__ A, int64_t lda, int64_t M, int64_t K, int64_t segsp,
-    int *__restrict__ row_exp, uint4 *__restrict__ out, int *__restrict__ clear, int nclear) {
+    int *__restrict__ row_exp, uint4 *__restrict__ out, int *__restrict__ clear, int nclear,
+    int nblocks) {
+  // every argument in SGPRs up front (one round of scalar loads); the grid
+  // size comes as an argument: gridDim.x was a vector load of the hidden
+  // arguments, waited for (vmcnt(0)) before the first load of A
+  kernarg_fence(A, lda, M, K, segsp, row_exp, out, clear, nclear, nblocks);
   // the GEMM's K-slice counters when they live in a caller's workspace:
   // zeroed here, before the GEMM (the next launch on the stream) counts in
   if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < nclear; i += blockDim.x) clear[i] = 0;
+    for (int i = threadIdx.x; i < nclear; i += 64 * kPrepWaves) clear[i] = 0;
   __shared__ float wmax[kPrepWaves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int b = blockIdx.x;
-  const int64_t row = b / 64 < (int)gridDim.x / 64
+  const int64_t row = b / 64 < nblocks / 64
                           ? (int64_t)(b / 64 * 8 + b % 8) * 8 + (b % 64) / 8
                           : (int64_t)b;
   const int64_t kp = segsp * kSegK;  // padded K
@@ -995,7 +1008,7 @@ static int launch_prep_a(mmnb_ctx *ctx, const float *d_a, int64_t lda, int64_t m
                          int64_t mpad, int64_t segsp, int *d_exp, uint4 *d_ap, int *clear,
                          int nclear) {
   return launch(ctx, kKernPrep, k_prep_a, dim3((unsigned)mpad), dim3(64 * kPrepWaves), 0, d_a,
-                lda, m, k, segsp, d_exp, d_ap, clear, nclear);
+                lda, m, k, segsp, d_exp, d_ap, clear, nclear, (int)mpad);
 }
 
 // ---------------------------------------------------------------------------
@@ -1055,6 +1068,8 @@ __global__ __launch_bounds__(256 * GROUPS) __attribute__((amdgpu_waves_per_eu(2,
   const int cl = lane & 31, g = lane >> 5;
   const uint32_t magic = 0x64006400u;
   uint4 *smem = smem_all + grp * NST * kStageU4;
+  kernarg_fence(Ap, row_exp, segs, segsp, W, col_bytes, ST, ldsz, nb, bs_log2, M, N, grid_x,
+                grid_y, Y, ksplit, part, tile_cnt);
 
   // XCD-aware tile order: consecutive workgroup ids go to different XCDs
   // (round robin), so regroup them into contiguous chunks per XCD, then walk
