@@ -722,14 +722,24 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 // wait), so the norms run while the tile is in flight.  Each wave then owns
 // 8 keys: scores (8 lanes per key, DPP reduction), a softmax over its keys
 // (the 8 scores read out with readlane, so wave-uniform) and p.v with no
-// LDS round trip; one barrier later the 4 waves' (max, sum, o) are merged
-// into the split's partial per query head.  The last split of a KV head to
-// finish (counter, reset by it) merges the partials.  Partials and counters
-// go through agent-scope atomics.  The split holding position pos uses the
-// new k / v directly and also writes them into the cache; no workgroup
-// reads an entry written in the same launch.
-constexpr int kDecKS = 32;          // keys per split
-constexpr int kDecKW = kDecKS / 4;  // keys per wave
+// LDS round trip; one barrier later the 8 waves' (max, sum, o) are merged
+// into the split's partial per query head.  Where the o projection can
+// take them (caches of up to kDecAttnMaxSplits splits, heads * head_dim <=
+// kDecAttnMaxK) the partials are left for its prologue to merge
+// (launch_dec_gemv_attn), so this launch ends with its partial stores.
+// Otherwise the last split of a KV head to finish (counter, reset by it)
+// merges them, partials and counters going through agent-scope atomics.
+// At the Qwen3-0.6B shape (position ~300, decode step as a graph) leaving
+// the merge to the o projection takes 0.611 -> 0.586 ms per token: the
+// count and last-arriver merge are three memory round trips after the
+// partial, the prologue's merge overlaps the projection's weight loads.  The
+// split holding position pos uses the new k / v directly and also writes
+// them into the cache; no workgroup reads an entry written in the same
+// launch.
+constexpr int kDecKS = 64;                 // keys per split
+constexpr int kDecKW = 8;                  // keys per wave
+constexpr int kDecAttnWaves = kDecKS / kDecKW;
+constexpr int kDecAttnThreads = 64 * kDecAttnWaves;
 constexpr int kDecMaxGroup = 4;     // query heads per KV head
 constexpr int kDecMaxLen = 8192;    // longest cache of a decoder session
 
@@ -769,8 +779,9 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
 
-// Operands of one layer's decode attention.  Partials live at
-// part[((kh*group + g) * nsmax + split) * (HD + 2)]: max, sum, o[HD].
+// Operands of one layer's decode attention.  The partial of query head
+// qh = kh * group + g over split s: o[HD] at po + (qh * nsmax + s) * HD and
+// (max, sum) at pml + 2 * (qh * nsmax + s).
 struct DecAttnArgs {
   const float *qkv;
   int nh, kvh;
@@ -780,7 +791,7 @@ struct DecAttnArgs {
   float *ck, *cv;
   int64_t cap;
   float scale;
-  float *part;
+  float *po, *pml;
   int nsmax;
   float *out;
 };
@@ -790,16 +801,16 @@ struct DecAttnArgs {
 // a softmax and o = sum p v per wave of kDecKW keys, then the split's
 // partial (max, sum, o) of every query head of the group.  The split
 // holding pos also writes the new k / v into the cache.  Whole workgroup,
-// 256 threads (4 waves).
-template <int HD>
+// kDecAttnThreads threads (kDecAttnWaves waves).
+template <int HD, bool COH>
 __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, int kh) {
   constexpr int kDpk = HD / 8;  // K dims per lane (a multiple of 4)
   constexpr int kHr = HD / 2;   // rotary half; norm lanes hold dims l, l + kHr
   __shared__ __align__(16) float sq[kDecMaxGroup][HD];
   __shared__ __align__(16) float skn[HD];
   __shared__ __align__(16) float svn[HD];
-  __shared__ __align__(16) float so[4][kDecMaxGroup][HD];
-  __shared__ float sm[4][kDecMaxGroup], sl[4][kDecMaxGroup];
+  __shared__ __align__(16) float so[kDecAttnWaves][kDecMaxGroup][HD];
+  __shared__ float sm[kDecAttnWaves][kDecMaxGroup], sl[kDecAttnWaves][kDecMaxGroup];
   const int nh = a.nh, kvh = a.kvh, group = nh / kvh;
   const int t = threadIdx.x, w = t >> 6, l = t & 63;
   const int jk = t >> 3, p8 = t & 7;  // K layout: key, dim slice
@@ -946,23 +957,26 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
   {
     const int g = t / kHr, dp = t % kHr;
     if (g < group) {
-      const float M = fmaxf(fmaxf(sm[0][g], sm[1][g]), fmaxf(sm[2][g], sm[3][g]));
+      float M = sm[0][g];
+#pragma unroll
+      for (int ww = 1; ww < kDecAttnWaves; ww++) M = fmaxf(M, sm[ww][g]);
       float ls = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-      for (int ww = 0; ww < 4; ww++) {
+      for (int ww = 0; ww < kDecAttnWaves; ww++) {
         const float wt = expf(sm[ww][g] - M);  // 0 for a wave with max -inf
         const float2 ov = *(const float2 *)(&so[ww][g][2 * dp]);
         ls = fmaf(wt, sl[ww][g], ls);
         o0 = fmaf(wt, ov.x, o0);
         o1 = fmaf(wt, ov.y, o1);
       }
-      float *pp = a.part + ((int64_t)(kh * group + g) * a.nsmax + split) * (HD + 2);
+      const int64_t ps = (int64_t)(kh * group + g) * a.nsmax + split;
+      float *pp = a.po + ps * HD;
       if (dp == 0) {
-        st_act<true>(pp, M);
-        st_act<true>(pp + 1, ls);
+        st_act<COH>(a.pml + 2 * ps, M);
+        st_act<COH>(a.pml + 2 * ps + 1, ls);
       }
-      st_act<true>(pp + 2 + 2 * dp, o0);
-      st_act<true>(pp + 3 + 2 * dp, o1);
+      st_act<COH>(pp + 2 * dp, o0);
+      st_act<COH>(pp + 1 + 2 * dp, o1);
     }
   }
   // the split holding position pos writes the new k / v into the cache
@@ -985,19 +999,18 @@ template <int HD>
 __device__ void dec_attn_merge(const DecAttnArgs &a, int pos, int kh) {
   const int group = a.nh / a.kvh, t = threadIdx.x;
   const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
-  const float *pg = a.part + (int64_t)kh * group * a.nsmax * (HD + 2);
-  for (int i = t; i < group * HD; i += 256) {
+  for (int i = t; i < group * HD; i += kDecAttnThreads) {
     const int gi = i / HD, di = i % HD;
-    const float *ph = pg + (int64_t)gi * a.nsmax * (HD + 2);
+    const int64_t p0 = (int64_t)(kh * group + gi) * a.nsmax;
     float M = -INFINITY, den = 0.0f, num = 0.0f;
     for (int s0 = 0; s0 < nsplit; s0 += 16) {
       float mv[16], lv[16], ov[16];
 #pragma unroll
       for (int u = 0; u < 16; u++) {
-        const float *pp = ph + (int64_t)min(s0 + u, nsplit - 1) * (HD + 2);
-        mv[u] = ld_act<true>(pp);
-        lv[u] = ld_act<true>(pp + 1);
-        ov[u] = ld_act<true>(pp + 2 + di);
+        const int64_t ps = p0 + min(s0 + u, nsplit - 1);
+        mv[u] = ld_act<true>(a.pml + 2 * ps);
+        lv[u] = ld_act<true>(a.pml + 2 * ps + 1);
+        ov[u] = ld_act<true>(a.po + ps * HD + di);
       }
       // every split has a key at or before pos, so its max is finite
       float Mb = M;
@@ -1021,23 +1034,27 @@ __device__ void dec_attn_merge(const DecAttnArgs &a, int pos, int kh) {
   }
 }
 
-// Launch form: grid (splits, KV heads); the last split of a KV head to
-// finish (counter, reset by it) merges.
-template <int HD>
-__global__ __launch_bounds__(256) void k_dec_attn(const DecState *__restrict__ st,
+// Launch form: grid (splits, KV heads).  MERGE: the last split of a KV
+// head to finish (counter, reset by it) merges the partials into out;
+// otherwise every split leaves its partial for the next launch (the o
+// projection's prologue, launch_dec_gemv_attn), whose start orders it.
+template <int HD, bool MERGE>
+__global__ __launch_bounds__(kDecAttnThreads) void k_dec_attn(const DecState *__restrict__ st,
                                                   DecAttnArgs a, int *counters) {
   __shared__ int s_last;
   const int split = blockIdx.x, kh = blockIdx.y;
   // every argument the loads need in SGPRs up front (one round of scalar
   // loads instead of dependent rounds ahead of the first load)
-  kernarg_fence(st, counters, a.qkv, a.nh, a.kvh, a.qn, a.kn, a.eps, a.rot, a.ck, a.cv, a.cap,
-                a.scale, a.part, a.nsmax, a.out);
+  kernarg_fence(st, a.qkv, a.nh, a.kvh, a.qn, a.kn, a.eps, a.rot, a.ck, a.cv, a.cap, a.scale,
+                a.po, a.pml, a.nsmax);
+  if constexpr (MERGE) kernarg_fence(counters, a.out);
   // the position through the vector memory path, used only once the
   // partial's loads are out: a scalar load would join the kernel-argument
   // loads' wait, in front of every other load
   const int pos_v = __hip_atomic_load(const_cast<int *>(&st->pos), __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
-  if (!dec_attn_partial<HD>(a, pos_v, split, kh)) return;  // whole workgroup
+  if (!dec_attn_partial<HD, MERGE>(a, pos_v, split, kh)) return;  // whole workgroup
+  if constexpr (!MERGE) return;
   const int pos = __builtin_amdgcn_readfirstlane(pos_v);
   const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
   // ---- publish: the barrier orders every thread's partial stores before
@@ -1210,7 +1227,8 @@ struct mmnb_decoder {
         *gu = nullptr, *act = nullptr, *tmp = nullptr, *logits = nullptr;
   float *cache_k = nullptr, *cache_v = nullptr, *cos = nullptr, *sin = nullptr;
   float *rot = nullptr;     // the decode step's rotary row: cos | sin, hd/2 each
-  float *part = nullptr;    // attention partials [heads, splits, hd + 2]
+  float *part = nullptr;    // attention partials: o [heads, splits, hd], then (max, sum)
+  bool attn_defer = false;  // the o projection merges them (else the attention launch)
   int *counters = nullptr;  // per KV head: attention splits finished
   DecState *state = nullptr;
   unsigned long long *keys = nullptr;  // lm_head workgroups' best (value, ~index)
@@ -1324,6 +1342,9 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
   }
   hipError_t e = hipMemset(d->state, 0, sizeof(DecState));
   if (e == hipSuccess) e = hipMemset(d->counters, 0, (size_t)kvh * 4);
+  d->attn_defer = ctx->dec_attn_defer && nsplit <= kDecAttnMaxSplits &&
+                  nh * hd <= kDecAttnMaxK &&
+                  nh * (nsplit <= 8 ? 8 : 16) <= kDecAttnMergeThreads;
   if (e != hipSuccess) {
     mmnb_decoder_free(d);
     return check_hip(e, "hipMemset");
@@ -1501,6 +1522,12 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
   return MMNB_OK;
 }
 
+// The (max, sum) pairs of the attention partials, after the o parts.
+static float *dec_part_ml(const mmnb_decoder *d) {
+  const mmnb_decoder_config &c = d->cfg;
+  return d->part + c.heads * ((c.max_len + kDecKS - 1) / kDecKS) * c.head_dim;
+}
+
 // Decode attention of one layer: grid (splits of the cache, KV heads);
 // splits past the current position exit at once.
 static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float *ck, float *cv) {
@@ -1510,10 +1537,13 @@ static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float 
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
   DecAttnArgs args{(const float *)d->qkv, (int)c.heads, (int)c.kv_heads, (const float *)L.qn,
                    (const float *)L.kn, c.eps, (const float *)d->rot, ck, cv, c.max_len, scale,
-                   d->part, (int)grid.x, d->attn};
+                   d->part, dec_part_ml(d), (int)grid.x, d->attn};
 #define MMNB_DEC_ATTN(HD)                                                                      \
-  launch(ctx, kKernDecAttn, k_dec_attn<HD>, grid, dim3(256), 0, (const DecState *)d->state,   \
-         args, d->counters)
+  (d->attn_defer                                                                              \
+       ? launch(ctx, kKernDecAttn, k_dec_attn<HD, false>, grid, dim3(kDecAttnThreads), 0,     \
+                (const DecState *)d->state, args, d->counters)                                \
+       : launch(ctx, kKernDecAttn, k_dec_attn<HD, true>, grid, dim3(kDecAttnThreads), 0,      \
+                (const DecState *)d->state, args, d->counters))
   switch (c.head_dim) {
     case 32: return MMNB_DEC_ATTN(32);
     case 64: return MMNB_DEC_ATTN(64);
@@ -1541,8 +1571,15 @@ static int dec_record_step(mmnb_decoder *d) {
       return rc;
     if ((rc = launch_dec_attn(d, L, ck, cv)))
       return rc;
-    if ((rc = launch_dec_gemv(ctx, L.o, d->attn, nullptr, eps, kDecResidual, d->x, d->x, nullptr)))
+    if (d->attn_defer) {
+      const DecAttnPartials pa{&d->state->pos, d->part, dec_part_ml(d),
+                               (int)((Lmax + kDecKS - 1) / kDecKS), (int)hd, kDecKS};
+      if ((rc = launch_dec_gemv_attn(ctx, L.o, pa, d->x, d->x)))
+        return rc;
+    } else if ((rc = launch_dec_gemv(ctx, L.o, d->attn, nullptr, eps, kDecResidual, d->x, d->x,
+                                     nullptr))) {
       return rc;
+    }
     if ((rc = launch_dec_gemv(ctx, L.gu, d->x, L.ln2, eps, kDecSwiglu, nullptr, d->act, nullptr)))
       return rc;
     if ((rc = launch_dec_gemv(ctx, L.down, d->act, nullptr, eps, kDecResidual, d->x, d->x,

@@ -58,6 +58,33 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __builtin_bit_cast(float, moved);
 }
 
+// max(v, v moved by the DPP control CTRL), every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                false);
+  return fmaxf(v, __builtin_bit_cast(float, moved));
+}
+
+// Sum / maximum over each aligned group of G = 8 or 16 lanes, in every lane
+// of the group (quad butterflies, then the half-row and row mirrors).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  if constexpr (G == 16) v = dpp_add<0x140>(v);  // row_mirror
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  v = dpp_max<0xB1>(v);
+  v = dpp_max<0x4E>(v);
+  v = dpp_max<0x141>(v);
+  if constexpr (G == 16) v = dpp_max<0x140>(v);
+  return v;
+}
+
 // Sum over each group of 32 lanes; every lane of the group gets the sum.
 __device__ __forceinline__ float half_wave_sum(float v) {
   v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]

@@ -89,6 +89,10 @@ struct mmnb_ctx {
   // Decoder prefill: norms / SwiGLU write the GEMM's prepared activations
   // (MMNB_PREP_FUSE: 0 keeps fp32 rows + k_prep_a; on by default).
   int prep_fuse = 1;
+  // Decode step: the o projection merges the attention's split partials
+  // (MMNB_DEC_ATTN_DEFER: 0 keeps the attention launch's own count and
+  // merge; on by default where the merge fits).
+  int dec_attn_defer = 1;
   // Prefill GEMM LDS stages (2 or 3; MMNB_GEMM_STAGES tuning override).
   int gemm_stages = 2;
   // Prefill GEMM 128-column blocks per tile (MMNB_GEMM_CB: 1 or 2; 0 = auto).
@@ -243,6 +247,26 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
                     const float *norm_gamma, float eps, int epi, const float *resid,
                     float *d_y, unsigned long long *d_argmax);
 int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n, int64_t k);
+
+// The decode attention's split partials, merged by the o projection's
+// prologue instead of by the attention launch itself.  Query head qh's
+// partial over split s (keys [s * ks, s * ks + ks)): o[hd] at
+// o + (qh * nsmax + s) * hd, (max, sum) at ml + 2 * (qh * nsmax + s); the
+// splits holding positions 0 .. *pos are merged.
+struct DecAttnPartials {
+  const int *pos;
+  const float *o;
+  const float *ml;
+  int nsmax, hd, ks;
+};
+constexpr int kDecAttnMaxSplits = 16;  // splits one merge holds in registers
+constexpr int kDecAttnMaxK = 2048;     // heads * head_dim: one float4 per thread
+constexpr int kDecAttnMergeThreads = kDecAttnMaxK / 4;
+// y[n] = resid[n] + (W * a)[n], a the merged attention output (p->k = heads
+// * hd <= kDecAttnMaxK, nsmax <= kDecAttnMaxSplits, heads * G <=
+// kDecAttnMergeThreads with G = 8 lanes per head for nsmax <= 8, else 16).
+int launch_dec_gemv_attn(mmnb_ctx *ctx, const mmnb_pack *p, const DecAttnPartials &pa,
+                         const float *resid, float *d_y);
 
 // Builds a 4-bit MatMulNBits pack (lock held): b_q [n, ceil(k/bs), bs/2]
 // bytes, scales fp32 [n * ceil(k/bs)], zp packed uint4 with the flat index

@@ -357,21 +357,93 @@ static int launch_gemv_r(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const f
 //          kDecArgmax (lm_head: each workgroup stores the best key
 //          (orderable value << 32 | ~index) of its columns; the greedy
 //          token is the maximum key, ties going to the lowest index).
+//   ATTN   the activations are the decode attention's output, merged here
+//          from its split partials (DecAttnPartials): every workgroup
+//          merges all K of them into LDS, so the attention launch needs no
+//          cross-workgroup count and merge of its own.
 // Lane layout and arithmetic (exact q - 8 per weight) follow k_gemv_valu
 // with M = 1 and one quantisation block per chunk; K is at most 4096 (one chunk per lane).
 // ---------------------------------------------------------------------------
 
-template <int R, bool NORM, int EPI>
-__global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
+// a = the merged attention output, into sx[K] (K <= kDecAttnMaxK, whole
+// workgroup of kDecAttnMergeThreads).  Per query head the splits' maxima
+// give M, and a = sum_s w_s o_s with w_s = e^(m_s - M) / sum_u e^(m_u - M) l_u
+// over the splits holding positions 0 .. pos (at most NS, a static bound on
+// nsmax).  load() issues every load at once, ahead of the position they are
+// filtered by: thread t holds the (max, sum) pair of (head t / G, split
+// t % G) -- a head's splits in one aligned group of G lanes -- and the o
+// parts of the float4 quad t of a.  finish(), after the caller has issued
+// its own loads: each head's maximum and denominator by DPP within its lane
+// group, the weights through LDS (one exponential per pair), then each
+// quad's weighted sum; it ends in a barrier.  One quad per thread over eight
+// waves keeps the merge's serial arithmetic short.
+template <int NS>
+struct DecAttnMerge {
+  static constexpr int G = NS <= 8 ? 8 : 16;  // lanes per head's pairs
+  float4 ov[NS];
+  float2 ml;
+  int qi, qh, pos_v;
+
+  __device__ __forceinline__ void load(const DecAttnPartials &pa, int K) {
+    const int t = threadIdx.x, nq = K >> 2, nh = K / pa.hd;
+    pos_v = __hip_atomic_load(const_cast<int *>(pa.pos), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    ml = *(const float2 *)(pa.ml + 2 * (min(t / G, nh - 1) * pa.nsmax +
+                                        min(t % G, pa.nsmax - 1)));
+    // floor(4q / hd) as (4q + 1/2) / hd in float: the quotient lies at least
+    // 1/(2 hd) from an integer, far beyond the product's rounding error
+    qi = min(t, nq - 1);
+    qh = (int)(((float)(4 * qi) + 0.5f) * (1.0f / (float)pa.hd));
+    const int d = 4 * qi - qh * pa.hd;
+    const int64_t p0 = (int64_t)qh * pa.nsmax;
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+      ov[s] = *(const float4 *)(pa.o + (p0 + min(s, pa.nsmax - 1)) * pa.hd + d);
+  }
+
+  __device__ __forceinline__ void finish(const DecAttnPartials &pa, float *sx) {
+    __shared__ float sw[kDecAttnMergeThreads];
+    const int t = threadIdx.x;
+    const int L = __builtin_amdgcn_readfirstlane(pos_v) + 1;
+    const int nsplit = min((L + pa.ks - 1) / pa.ks, pa.nsmax);
+    // pair (head t / G, split t % G); splits past pos weigh 0.  Every lane
+    // takes part in the group reductions.
+    const bool live = t % G < nsplit;
+    const float M = group_max<G>(live ? ml.x : -INFINITY);
+    const float e = live ? expf(ml.x - M) : 0.0f;
+    const float den = group_sum<G>(e * (live ? ml.y : 0.0f));
+    sw[t] = e / den;
+    __syncthreads();
+    float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+      if (s < nsplit) {  // uniform: splits past pos are skipped, not weighted
+        const float w = sw[qh * G + s];
+        n0 = fmaf(w, ov[s].x, n0);
+        n1 = fmaf(w, ov[s].y, n1);
+        n2 = fmaf(w, ov[s].z, n2);
+        n3 = fmaf(w, ov[s].w, n3);
+      }
+    }
+    if (qi == t) *(float4 *)(sx + 4 * qi) = make_float4(n0, n1, n2, n3);
+    __syncthreads();
+  }
+};
+
+template <int R, bool NORM, int EPI, int ATTN = 0>
+__global__ __launch_bounds__(ATTN ? kDecAttnMergeThreads : 64 * kDecMaxWaves) void k_dec_gemv(
     const float *__restrict__ X, const float *__restrict__ gamma, float eps,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S, int nb,
     int bs_log2, int K, int N, const float *resid, float *Y,
-    unsigned long long *__restrict__ argmax, int C) {
-  __shared__ float red[kDecMaxWaves][2 * R];
-  __shared__ float nrm[kDecMaxWaves];
+    unsigned long long *__restrict__ argmax, int C, DecAttnPartials pa) {
+  constexpr int kWaves = ATTN ? kDecAttnMergeThreads / 64 : kDecMaxWaves;
+  __shared__ float red[kWaves][2 * R];
+  __shared__ float nrm[kWaves];
   __shared__ float outv[2 * R];
+  __shared__ __align__(16) float sx[ATTN ? kDecAttnMaxK : 4];
   kernarg_fence(X, gamma, eps, W, col_bytes, S, nb, bs_log2, K, N, resid, Y, argmax, C,
                 blockDim.x);
+  if constexpr (ATTN) kernarg_fence(pa.pos, pa.o, pa.ml, pa.nsmax, pa.hd, pa.ks);
   const int nw = blockDim.x >> 6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int h = l >> 5, t = l & 31;
@@ -386,9 +458,14 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   const bool cv = c < C;
   const int cc = cv ? c : 0;
   const int s = cc >> 1, g = cc & 1;
-  // ---- loads: activations (and gamma), scales, then weights
+  // ---- loads: activations (and gamma; with ATTN the attention partials),
+  // scales, then weights
   float av[32], gv[32];
-  load_chunk32_paired(X + s * kSegK + 8 * g, h, av);
+  [[maybe_unused]] DecAttnMerge<ATTN ? ATTN : 1> mg;
+  if constexpr (ATTN)
+    mg.load(pa, K);
+  else
+    load_chunk32_paired(X + s * kSegK + 8 * g, h, av);
   if constexpr (NORM) load_chunk32_paired(gamma + s * kSegK + 8 * g, h, gv);
   const int blk = (s * kSegK) >> bs_log2;
   float sraw[R];
@@ -405,6 +482,17 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
     wv[r] = ld_weights16_u4(W + (int64_t)colr[r] * col_bytes + (int64_t)cc * 16);
   // every load above is in flight before any arithmetic (see k_gemv_valu)
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ATTN) {  // merge, then the chunk's runs k = base + 16 j + e out of LDS
+    mg.finish(pa, sx);
+    const float *xr = sx + s * kSegK + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float4 a0 = *(const float4 *)(xr + 16 * j);
+      const float4 a1 = *(const float4 *)(xr + 16 * j + 4);
+      av[8 * j + 0] = a0.x; av[8 * j + 1] = a0.y; av[8 * j + 2] = a0.z; av[8 * j + 3] = a0.w;
+      av[8 * j + 4] = a1.x; av[8 * j + 5] = a1.y; av[8 * j + 6] = a1.z; av[8 * j + 7] = a1.w;
+    }
+  }
   if constexpr (NORM) {
     float ss = 0.0f;
     if (h == 0 && cv) {
@@ -522,7 +610,7 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
 #define MMNB_DEC(RR, NN, EE)                                                                   \
   return launch(ctx, kid, k_dec_gemv<RR, NN, EE>, grid, block, 0, d_x, norm_gamma, eps,         \
                 p->d_w, p->col_bytes, p->d_scales, (int)p->n_blocks, bs_log2, (int)p->k,     \
-                (int)n, resid, d_y, d_argmax, C)
+                (int)n, resid, d_y, d_argmax, C, DecAttnPartials{})
 #define MMNB_DEC_R(NN, EE)              \
   {                                     \
     if (R == 8) MMNB_DEC(8, NN, EE);    \
@@ -538,6 +626,45 @@ int launch_dec_gemv(mmnb_ctx *ctx, const mmnb_pack *p, const float *d_x,
 #undef MMNB_DEC_R
 #undef MMNB_DEC
   return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV: unsupported prologue/epilogue pair");
+}
+
+int launch_dec_gemv_attn(mmnb_ctx *ctx, const mmnb_pack *p, const DecAttnPartials &pa,
+                         const float *resid, float *d_y) {
+  if (p->has_zp || p->block < 64 || p->generic)
+    return fail(MMNB_ERR_UNSUPPORTED,
+                "decoder GEMV: needs a power-of-two block >= 64 and no zero points");
+  if (p->k % kSegK != 0 || p->k > kDecAttnMaxK)
+    return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV (attention merge): K must be a multiple "
+                                      "of 64, <= 2048");
+  if (!pa.pos || !pa.o || !pa.ml || pa.nsmax < 1 || pa.nsmax > kDecAttnMaxSplits ||
+      pa.hd < 4 || pa.hd % 4 != 0 || p->k % pa.hd != 0 || pa.ks < 1 ||
+      p->k / pa.hd * (pa.nsmax <= 8 ? 8 : 16) > kDecAttnMergeThreads)
+    return fail(MMNB_ERR_ARG, "decoder GEMV (attention merge): bad partials");
+  const int C = (int)(p->col_bytes / 16);
+  const int64_t n = p->n;
+  const int R = dec_gemv_r(ctx, n, dec_gemv_waves(p->k));
+  const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
+  const dim3 block((unsigned)kDecAttnMergeThreads);
+  const int bs_log2 = ilog2(p->block);
+#define MMNB_DEC(RR, NS)                                                                      \
+  return launch(ctx, kKernDecGemvRes, k_dec_gemv<RR, false, kDecResidual, NS>, grid, block,   \
+                0, pa.o, nullptr, 0.0f, p->d_w, p->col_bytes, p->d_scales, (int)p->n_blocks,  \
+                bs_log2, (int)p->k, (int)n, resid, d_y, nullptr, C, pa)
+#define MMNB_DEC_NS(RR)                   \
+  {                                       \
+    if (pa.nsmax <= 2) MMNB_DEC(RR, 2);   \
+    if (pa.nsmax <= 4) MMNB_DEC(RR, 4);   \
+    if (pa.nsmax <= 6) MMNB_DEC(RR, 6);   \
+    if (pa.nsmax <= 8) MMNB_DEC(RR, 8);   \
+    if (pa.nsmax <= 12) MMNB_DEC(RR, 12); \
+    MMNB_DEC(RR, 16);                     \
+  }
+  if (R == 8) MMNB_DEC_NS(8);
+  if (R == 4) MMNB_DEC_NS(4);
+  if (R == 2) MMNB_DEC_NS(2);
+  MMNB_DEC_NS(1);
+#undef MMNB_DEC_NS
+#undef MMNB_DEC
 }
 
 // ---------------------------------------------------------------------------

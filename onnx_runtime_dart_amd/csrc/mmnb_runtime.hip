@@ -133,6 +133,10 @@ int mmnb_init(int device, mmnb_ctx **out) {
     const int v = std::atoi(r);
     if (v == 0 || v == 1) ctx->prep_fuse = v;
   }
+  if (const char *r = std::getenv("MMNB_DEC_ATTN_DEFER")) {
+    const int v = std::atoi(r);
+    if (v == 0 || v == 1) ctx->dec_attn_defer = v;
+  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

@@ -22,6 +22,7 @@ the last decode step's logits against a prefill of the same sequence
 (GEMM path, other attention kernel) to FULL_TOL.
 """
 import ctypes
+import dataclasses
 import os
 
 import numpy as np
@@ -277,10 +278,12 @@ SMALL = G.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64,
 QWEN_HEADS = G.DecoderConfig(layers=2, hidden=1024, heads=16, kv_heads=8, head_dim=128,
                              intermediate=3072, vocab=2048, block=128, max_len=96)
 # four query heads per KV head, head sizes 32 and 96; the first decodes past
-# 16 splits of 32 keys (the decode attention's merge then takes its partials
-# in two batches)
+# 16 splits of 64 keys, so its decode attention merges the splits itself
+# (its cache is too long for the o projection's merge) and takes the
+# partials in two batches
 LONG_G4 = G.DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=2, head_dim=32,
-                          intermediate=512, vocab=500, block=64, max_len=640)
+                          intermediate=512, vocab=500, block=64, max_len=1100)
+SHORT_G4 = dataclasses.replace(LONG_G4, max_len=80)
 HD96_G4 = G.DecoderConfig(layers=1, hidden=256, heads=4, kv_heads=1, head_dim=96,
                           intermediate=512, vocab=500, block=64, max_len=64)
 # one and three query heads per KV head
@@ -291,11 +294,39 @@ G3 = G.DecoderConfig(layers=2, hidden=256, heads=6, kv_heads=2, head_dim=64,
 
 
 @pytest.mark.parametrize("cfg,prompt_len,steps",
-                         [(SMALL, 20, 12), (QWEN_HEADS, 48, 8), (LONG_G4, 600, 8),
-                          (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
-                         ids=["small", "qwen_heads", "long_cache_group4_hd32", "hd96_group4",
-                              "mha_group1", "group3"])
+                         [(SMALL, 20, 12), (QWEN_HEADS, 48, 8), (LONG_G4, 1050, 8),
+                          (SHORT_G4, 40, 8), (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
+                         ids=["small", "qwen_heads", "long_cache_group4_hd32",
+                              "short_cache_group4_hd32", "hd96_group4", "mha_group1", "group3"])
 def test_decoder_vs_oracle(ctx, cfg, prompt_len, steps):
+    decoder_vs_oracle(ctx, cfg, prompt_len, steps)
+
+
+@pytest.fixture(scope="module")
+def merge_attn_ctx():
+    # a context whose decode attention merges its splits itself (count and
+    # last-arriver merge) instead of leaving them to the o projection
+    saved = os.environ.get("MMNB_DEC_ATTN_DEFER")
+    os.environ["MMNB_DEC_ATTN_DEFER"] = "0"
+    try:
+        c = _lib.Context(0)
+    finally:
+        if saved is None:
+            os.environ.pop("MMNB_DEC_ATTN_DEFER", None)
+        else:
+            os.environ["MMNB_DEC_ATTN_DEFER"] = saved
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("cfg,prompt_len,steps",
+                         [(QWEN_HEADS, 48, 8), (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
+                         ids=["qwen_heads", "hd96_group4", "mha_group1", "group3"])
+def test_decoder_attention_self_merge_vs_oracle(merge_attn_ctx, cfg, prompt_len, steps):
+    decoder_vs_oracle(merge_attn_ctx, cfg, prompt_len, steps)
+
+
+def decoder_vs_oracle(ctx, cfg, prompt_len, steps):
     w = G.random_weights(cfg, seed=5)
     rng = np.random.default_rng(9)
     prompt = rng.integers(0, cfg.vocab, prompt_len)
