@@ -730,7 +730,7 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 // Otherwise the last split of a KV head to finish (counter, reset by it)
 // merges them, partials and counters going through agent-scope atomics.
 // At the Qwen3-0.6B shape (position ~300, decode step as a graph) leaving
-// the merge to the o projection takes 0.611 -> 0.586 ms per token: the
+// the merge to the o projection takes 0.611 -> 0.577 ms per token: the
 // count and last-arriver merge are three memory round trips after the
 // partial, the prologue's merge overlaps the projection's weight loads.  The
 // split holding position pos uses the new k / v directly and also writes

@@ -260,8 +260,8 @@ struct DecAttnPartials {
   int nsmax, hd, ks;
 };
 constexpr int kDecAttnMaxSplits = 16;  // splits one merge holds in registers
-constexpr int kDecAttnMaxK = 2048;     // heads * head_dim: one float4 per thread
-constexpr int kDecAttnMergeThreads = kDecAttnMaxK / 4;
+constexpr int kDecAttnMaxK = 2048;     // heads * head_dim: two float4 per thread
+constexpr int kDecAttnMergeThreads = 256;
 // y[n] = resid[n] + (W * a)[n], a the merged attention output (p->k = heads
 // * hd <= kDecAttnMaxK, nsmax <= kDecAttnMaxSplits, heads * G <=
 // kDecAttnMergeThreads with G = 8 lanes per head for nsmax <= 8, else 16).

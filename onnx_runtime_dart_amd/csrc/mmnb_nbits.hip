@@ -372,17 +372,23 @@ static int launch_gemv_r(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const f
 // nsmax).  load() issues every load at once, ahead of the position they are
 // filtered by: thread t holds the (max, sum) pair of (head t / G, split
 // t % G) -- a head's splits in one aligned group of G lanes -- and the o
-// parts of the float4 quad t of a.  finish(), after the caller has issued
-// its own loads: each head's maximum and denominator by DPP within its lane
-// group, the weights through LDS (one exponential per pair), then each
-// quad's weighted sum; it ends in a barrier.  One quad per thread over eight
-// waves keeps the merge's serial arithmetic short.
+// parts of the float4 quads t and t + 256 of a.  finish(), after the caller
+// has issued its own loads: each head's maximum and denominator by DPP
+// within its lane group, the weights through LDS (one exponential per
+// pair), then each quad's weighted sum; it ends in a barrier.  Measured on
+// the Qwen3-0.6B-shape decode step (ms per token): two quads per thread on
+// the GEMV's four waves 0.577-0.580; one quad on eight waves 0.584; four
+// quads on two waves 0.592; each lane merging only its own chunk's 32
+// values (no LDS copy, no second barrier; four quads per lane) 0.615.
+static_assert(kDecAttnMergeThreads == 64 * kDecMaxWaves, "the merge runs on the GEMV's block");
+
 template <int NS>
 struct DecAttnMerge {
   static constexpr int G = NS <= 8 ? 8 : 16;  // lanes per head's pairs
-  float4 ov[NS];
+  static constexpr int QP = kDecAttnMaxK / 4 / kDecAttnMergeThreads;  // quads per thread
+  float4 ov[QP][NS];
   float2 ml;
-  int qi, qh, pos_v;
+  int qi[QP], qh[QP], pos_v;
 
   __device__ __forceinline__ void load(const DecAttnPartials &pa, int K) {
     const int t = threadIdx.x, nq = K >> 2, nh = K / pa.hd;
@@ -392,13 +398,17 @@ struct DecAttnMerge {
                                         min(t % G, pa.nsmax - 1)));
     // floor(4q / hd) as (4q + 1/2) / hd in float: the quotient lies at least
     // 1/(2 hd) from an integer, far beyond the product's rounding error
-    qi = min(t, nq - 1);
-    qh = (int)(((float)(4 * qi) + 0.5f) * (1.0f / (float)pa.hd));
-    const int d = 4 * qi - qh * pa.hd;
-    const int64_t p0 = (int64_t)qh * pa.nsmax;
+    const float rhd = 1.0f / (float)pa.hd;
 #pragma unroll
-    for (int s = 0; s < NS; s++)
-      ov[s] = *(const float4 *)(pa.o + (p0 + min(s, pa.nsmax - 1)) * pa.hd + d);
+    for (int i = 0; i < QP; i++) {
+      qi[i] = min(t + kDecAttnMergeThreads * i, nq - 1);
+      qh[i] = (int)(((float)(4 * qi[i]) + 0.5f) * rhd);
+      const int d = 4 * qi[i] - qh[i] * pa.hd;
+      const int64_t p0 = (int64_t)qh[i] * pa.nsmax;
+#pragma unroll
+      for (int s = 0; s < NS; s++)
+        ov[i][s] = *(const float4 *)(pa.o + (p0 + min(s, pa.nsmax - 1)) * pa.hd + d);
+    }
   }
 
   __device__ __forceinline__ void finish(const DecAttnPartials &pa, float *sx) {
@@ -414,31 +424,34 @@ struct DecAttnMerge {
     const float den = group_sum<G>(e * (live ? ml.y : 0.0f));
     sw[t] = e / den;
     __syncthreads();
-    float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
 #pragma unroll
-    for (int s = 0; s < NS; s++) {
-      if (s < nsplit) {  // uniform: splits past pos are skipped, not weighted
-        const float w = sw[qh * G + s];
-        n0 = fmaf(w, ov[s].x, n0);
-        n1 = fmaf(w, ov[s].y, n1);
-        n2 = fmaf(w, ov[s].z, n2);
-        n3 = fmaf(w, ov[s].w, n3);
+    for (int i = 0; i < QP; i++) {
+      float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
+#pragma unroll
+      for (int s = 0; s < NS; s++) {
+        if (s < nsplit) {  // uniform: splits past pos are skipped, not weighted
+          const float w = sw[qh[i] * G + s];
+          n0 = fmaf(w, ov[i][s].x, n0);
+          n1 = fmaf(w, ov[i][s].y, n1);
+          n2 = fmaf(w, ov[i][s].z, n2);
+          n3 = fmaf(w, ov[i][s].w, n3);
+        }
       }
+      if (qi[i] == t + kDecAttnMergeThreads * i)
+        *(float4 *)(sx + 4 * qi[i]) = make_float4(n0, n1, n2, n3);
     }
-    if (qi == t) *(float4 *)(sx + 4 * qi) = make_float4(n0, n1, n2, n3);
     __syncthreads();
   }
 };
 
 template <int R, bool NORM, int EPI, int ATTN = 0>
-__global__ __launch_bounds__(ATTN ? kDecAttnMergeThreads : 64 * kDecMaxWaves) void k_dec_gemv(
+__global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
     const float *__restrict__ X, const float *__restrict__ gamma, float eps,
     const uint8_t *__restrict__ W, int64_t col_bytes, const float *__restrict__ S, int nb,
     int bs_log2, int K, int N, const float *resid, float *Y,
     unsigned long long *__restrict__ argmax, int C, DecAttnPartials pa) {
-  constexpr int kWaves = ATTN ? kDecAttnMergeThreads / 64 : kDecMaxWaves;
-  __shared__ float red[kWaves][2 * R];
-  __shared__ float nrm[kWaves];
+  __shared__ float red[kDecMaxWaves][2 * R];
+  __shared__ float nrm[kDecMaxWaves];
   __shared__ float outv[2 * R];
   __shared__ __align__(16) float sx[ATTN ? kDecAttnMaxK : 4];
   kernarg_fence(X, gamma, eps, W, col_bytes, S, nb, bs_log2, K, N, resid, Y, argmax, C,
@@ -644,7 +657,7 @@ int launch_dec_gemv_attn(mmnb_ctx *ctx, const mmnb_pack *p, const DecAttnPartial
   const int64_t n = p->n;
   const int R = dec_gemv_r(ctx, n, dec_gemv_waves(p->k));
   const dim3 grid((unsigned)((n + 2 * R - 1) / (2 * R)));
-  const dim3 block((unsigned)kDecAttnMergeThreads);
+  const dim3 block((unsigned)kDecAttnMergeThreads);  // = 64 * kDecMaxWaves
   const int bs_log2 = ilog2(p->block);
 #define MMNB_DEC(RR, NS)                                                                      \
   return launch(ctx, kKernDecGemvRes, k_dec_gemv<RR, false, kDecResidual, NS>, grid, block,   \
