@@ -713,7 +713,7 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 }
 
 // Decode attention for one token, spread over the GPU: one workgroup per
-// (split of kDecKS keys, KV head), serving every query head of that KV
+// (split of KS keys, KV head), serving every query head of that KV
 // group, so each cached key and value is read once per layer and the read
 // is shared by many CUs (one CU alone streams only a few tens of GB/s of
 // dependent loads).  The workgroup first issues the loads its per-head
@@ -722,7 +722,7 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 // wait), so the norms run while the tile is in flight.  Each wave then owns
 // 8 keys: scores (8 lanes per key, DPP reduction), a softmax over its keys
 // (the 8 scores read out with readlane, so wave-uniform) and p.v with no
-// LDS round trip; one barrier later the 8 waves' (max, sum, o) are merged
+// LDS round trip; one barrier later the KS / 8 waves' (max, sum, o) are merged
 // into the split's partial per query head.  Where the o projection can
 // take them (caches of up to kDecAttnMaxSplits splits, heads * head_dim <=
 // kDecAttnMaxK) the partials are left for its prologue to merge
@@ -736,10 +736,17 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 // split holding position pos uses the new k / v directly and also writes
 // them into the cache; no workgroup reads an entry written in the same
 // launch.
-constexpr int kDecKS = 64;                 // keys per split
-constexpr int kDecKW = 8;                  // keys per wave
-constexpr int kDecAttnWaves = kDecKS / kDecKW;
-constexpr int kDecAttnThreads = 64 * kDecAttnWaves;
+// Keys per split KS: 32 (4 waves) for caches of up to 512 rows, 64 (8 waves)
+// for longer ones.  At the Qwen3-0.6B shape (cache 320, position ~300) the
+// 32-key launch takes 4.2 us eager against 5.0 us for 64 keys, and the
+// decode step the same time either way (0.578-0.580 ms per token): the o
+// projection merges twice the partials.  Past 512 rows 64-key splits keep
+// the merge in the o projection up to 1024 rows.
+constexpr int kDecKW = 8;  // keys per wave
+constexpr int kDecKSShort = 32, kDecKSLong = 64;
+constexpr int kDecKSShortMaxLen = 512;
+template <int KS>
+constexpr int dec_attn_threads() { return 64 * (KS / kDecKW); }
 constexpr int kDecMaxGroup = 4;     // query heads per KV head
 constexpr int kDecMaxLen = 8192;    // longest cache of a decoder session
 
@@ -796,14 +803,15 @@ struct DecAttnArgs {
   float *out;
 };
 
-// One split of kDecKS keys of KV head kh at position pos: the group's q
+// One split of KS keys of KV head kh at position pos: the group's q
 // heads and the new k (per-head RMSNorm in double, rotary at pos), scores,
 // a softmax and o = sum p v per wave of kDecKW keys, then the split's
 // partial (max, sum, o) of every query head of the group.  The split
 // holding pos also writes the new k / v into the cache.  Whole workgroup,
-// kDecAttnThreads threads (kDecAttnWaves waves).
-template <int HD, bool COH>
+// KS / 8 waves.
+template <int HD, bool COH, int KS>
 __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, int kh) {
+  constexpr int kDecAttnWaves = KS / kDecKW;
   constexpr int kDpk = HD / 8;  // K dims per lane (a multiple of 4)
   constexpr int kHr = HD / 2;   // rotary half; norm lanes hold dims l, l + kHr
   __shared__ __align__(16) float sq[kDecMaxGroup][HD];
@@ -814,7 +822,7 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
   const int nh = a.nh, kvh = a.kvh, group = nh / kvh;
   const int t = threadIdx.x, w = t >> 6, l = t & 63;
   const int jk = t >> 3, p8 = t & 7;  // K layout: key, dim slice
-  const int j0 = split * kDecKS;
+  const int j0 = split * KS;
   const float *Kb = a.ck + (int64_t)kh * a.cap * HD;
   const float *Vb = a.cv + (int64_t)kh * a.cap * HD;
   // ---- loads, in the order they are used.  Norm rows: wave w takes q head
@@ -865,7 +873,7 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
   int pos = pos_in;
   asm volatile("" : "+v"(pos));
   const int L = pos + 1;
-  const int nsplit = (L + kDecKS - 1) / kDecKS;
+  const int nsplit = (L + KS - 1) / KS;
   if (split >= nsplit) {
     asm volatile("" ::"v"(kreg[0]), "v"(vreg[0].x), "v"(x0[0]), "v"(xv.x));
     return false;
@@ -990,16 +998,16 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
 
 // Merges the nsplit partials of KV head kh into out (every query head of the
 // group).  Each thread (head g, dim) loads the (max, sum, o[dim]) of 16
-// splits at once (one memory round trip for caches up to 16 * kDecKS; the
+// splits at once (one memory round trip for caches up to 16 * KS; the
 // (max, sum) addresses are the same across the head's threads) and forms
 // the weights exp(m_s - M) itself, so no barrier is needed; longer caches
 // take further batches of 16, rescaling what is summed so far to the new
 // maximum.  Whole workgroup.
-template <int HD>
+template <int HD, int KS>
 __device__ void dec_attn_merge(const DecAttnArgs &a, int pos, int kh) {
   const int group = a.nh / a.kvh, t = threadIdx.x;
-  const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
-  for (int i = t; i < group * HD; i += kDecAttnThreads) {
+  const int nsplit = (pos + 1 + KS - 1) / KS;
+  for (int i = t; i < group * HD; i += dec_attn_threads<KS>()) {
     const int gi = i / HD, di = i % HD;
     const int64_t p0 = (int64_t)(kh * group + gi) * a.nsmax;
     float M = -INFINITY, den = 0.0f, num = 0.0f;
@@ -1038,8 +1046,8 @@ __device__ void dec_attn_merge(const DecAttnArgs &a, int pos, int kh) {
 // head to finish (counter, reset by it) merges the partials into out;
 // otherwise every split leaves its partial for the next launch (the o
 // projection's prologue, launch_dec_gemv_attn), whose start orders it.
-template <int HD, bool MERGE>
-__global__ __launch_bounds__(kDecAttnThreads) void k_dec_attn(const DecState *__restrict__ st,
+template <int HD, bool MERGE, int KS>
+__global__ __launch_bounds__(dec_attn_threads<KS>()) void k_dec_attn(const DecState *__restrict__ st,
                                                   DecAttnArgs a, int *counters) {
   __shared__ int s_last;
   const int split = blockIdx.x, kh = blockIdx.y;
@@ -1053,10 +1061,10 @@ __global__ __launch_bounds__(kDecAttnThreads) void k_dec_attn(const DecState *__
   // loads' wait, in front of every other load
   const int pos_v = __hip_atomic_load(const_cast<int *>(&st->pos), __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
-  if (!dec_attn_partial<HD, MERGE>(a, pos_v, split, kh)) return;  // whole workgroup
+  if (!dec_attn_partial<HD, MERGE, KS>(a, pos_v, split, kh)) return;  // whole workgroup
   if constexpr (!MERGE) return;
   const int pos = __builtin_amdgcn_readfirstlane(pos_v);
-  const int nsplit = (pos + 1 + kDecKS - 1) / kDecKS;
+  const int nsplit = (pos + 1 + KS - 1) / KS;
   // ---- publish: the barrier orders every thread's partial stores before
   // thread 0's count; its release (agent scope) pairs with the acquire fence
   // of the last split, which reads the count the others' releases wrote, and
@@ -1072,7 +1080,7 @@ __global__ __launch_bounds__(kDecAttnThreads) void k_dec_attn(const DecState *__
   }
   __syncthreads();
   if (!s_last) return;
-  dec_attn_merge<HD>(a, pos, kh);
+  dec_attn_merge<HD, KS>(a, pos, kh);
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1229,6 +1237,7 @@ struct mmnb_decoder {
   float *rot = nullptr;     // the decode step's rotary row: cos | sin, hd/2 each
   float *part = nullptr;    // attention partials: o [heads, splits, hd], then (max, sum)
   bool attn_defer = false;  // the o projection merges them (else the attention launch)
+  int ks = kDecKSLong;      // keys per attention split
   int *counters = nullptr;  // per KV head: attention splits finished
   DecState *state = nullptr;
   unsigned long long *keys = nullptr;  // lm_head workgroups' best (value, ~index)
@@ -1301,7 +1310,8 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
   const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim,
                 I = c.intermediate, Lmax = c.max_len;
   const int64_t QKV = (nh + 2 * kvh) * hd;
-  const int64_t nsplit = (Lmax + kDecKS - 1) / kDecKS;
+  d->ks = Lmax <= kDecKSShortMaxLen ? kDecKSShort : kDecKSLong;
+  const int64_t nsplit = (Lmax + d->ks - 1) / d->ks;
   auto A = [&](size_t bytes, void **p) { return dec_alloc(d, bytes, p); };
   if ((rc = dec_upload(d, embed, (size_t)(c.vocab * H), &d->embed)) ||
       (rc = dec_upload(d, final_norm, (size_t)H, &d->final_norm)) ||
@@ -1525,7 +1535,7 @@ int mmnb_decoder_prefill(mmnb_decoder *d, const int64_t *tokens, int64_t n,
 // The (max, sum) pairs of the attention partials, after the o parts.
 static float *dec_part_ml(const mmnb_decoder *d) {
   const mmnb_decoder_config &c = d->cfg;
-  return d->part + c.heads * ((c.max_len + kDecKS - 1) / kDecKS) * c.head_dim;
+  return d->part + c.heads * ((c.max_len + d->ks - 1) / d->ks) * c.head_dim;
 }
 
 // Decode attention of one layer: grid (splits of the cache, KV heads);
@@ -1533,17 +1543,21 @@ static float *dec_part_ml(const mmnb_decoder *d) {
 static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float *ck, float *cv) {
   mmnb_ctx *ctx = d->ctx;
   const mmnb_decoder_config &c = d->cfg;
-  const dim3 grid((unsigned)((c.max_len + kDecKS - 1) / kDecKS), (unsigned)c.kv_heads);
+  const dim3 grid((unsigned)((c.max_len + d->ks - 1) / d->ks), (unsigned)c.kv_heads);
   const float scale = (float)(1.0 / std::sqrt((double)c.head_dim));
   DecAttnArgs args{(const float *)d->qkv, (int)c.heads, (int)c.kv_heads, (const float *)L.qn,
                    (const float *)L.kn, c.eps, (const float *)d->rot, ck, cv, c.max_len, scale,
                    d->part, dec_part_ml(d), (int)grid.x, d->attn};
-#define MMNB_DEC_ATTN(HD)                                                                      \
+#define MMNB_DEC_ATTN_KS(HD, KS)                                                               \
   (d->attn_defer                                                                              \
-       ? launch(ctx, kKernDecAttn, k_dec_attn<HD, false>, grid, dim3(kDecAttnThreads), 0,     \
-                (const DecState *)d->state, args, d->counters)                                \
-       : launch(ctx, kKernDecAttn, k_dec_attn<HD, true>, grid, dim3(kDecAttnThreads), 0,      \
-                (const DecState *)d->state, args, d->counters))
+       ? launch(ctx, kKernDecAttn, k_dec_attn<HD, false, KS>, grid,                           \
+                dim3(dec_attn_threads<KS>()), 0, (const DecState *)d->state, args,            \
+                d->counters)                                                                  \
+       : launch(ctx, kKernDecAttn, k_dec_attn<HD, true, KS>, grid,                            \
+                dim3(dec_attn_threads<KS>()), 0, (const DecState *)d->state, args,            \
+                d->counters))
+#define MMNB_DEC_ATTN(HD)                                                                      \
+  (d->ks == kDecKSShort ? MMNB_DEC_ATTN_KS(HD, kDecKSShort) : MMNB_DEC_ATTN_KS(HD, kDecKSLong))
   switch (c.head_dim) {
     case 32: return MMNB_DEC_ATTN(32);
     case 64: return MMNB_DEC_ATTN(64);
@@ -1552,6 +1566,7 @@ static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float 
     default: return fail(MMNB_ERR_UNSUPPORTED, "decoder: head_dim");
   }
 #undef MMNB_DEC_ATTN
+#undef MMNB_DEC_ATTN_KS
 }
 
 static int dec_record_step(mmnb_decoder *d) {
@@ -1573,7 +1588,7 @@ static int dec_record_step(mmnb_decoder *d) {
       return rc;
     if (d->attn_defer) {
       const DecAttnPartials pa{&d->state->pos, d->part, dec_part_ml(d),
-                               (int)((Lmax + kDecKS - 1) / kDecKS), (int)hd, kDecKS};
+                               (int)((Lmax + d->ks - 1) / d->ks), (int)hd, d->ks};
       if ((rc = launch_dec_gemv_attn(ctx, L.o, pa, d->x, d->x)))
         return rc;
     } else if ((rc = launch_dec_gemv(ctx, L.o, d->attn, nullptr, eps, kDecResidual, d->x, d->x,

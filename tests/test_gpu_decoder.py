@@ -277,12 +277,16 @@ SMALL = G.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64,
                         intermediate=512, vocab=1000, block=64, max_len=64)
 QWEN_HEADS = G.DecoderConfig(layers=2, hidden=1024, heads=16, kv_heads=8, head_dim=128,
                              intermediate=3072, vocab=2048, block=128, max_len=96)
-# four query heads per KV head, head sizes 32 and 96; the first decodes past
-# 16 splits of 64 keys, so its decode attention merges the splits itself
-# (its cache is too long for the o projection's merge) and takes the
-# partials in two batches
+# four query heads per KV head, head sizes 32 and 96.  Caches of up to 512
+# rows split into 32-key splits, longer ones into 64-key splits; the o
+# projection merges up to 16 splits.  LONG_G4 decodes past 16 splits of 64
+# keys, so its decode attention merges the splits itself and takes the
+# partials in two batches; MID_G4 has 64-key splits merged by the o
+# projection (11 of them), CACHE512_G4 sixteen 32-key splits.
 LONG_G4 = G.DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=2, head_dim=32,
                           intermediate=512, vocab=500, block=64, max_len=1100)
+MID_G4 = dataclasses.replace(LONG_G4, max_len=700)
+CACHE512_G4 = dataclasses.replace(LONG_G4, max_len=512)
 SHORT_G4 = dataclasses.replace(LONG_G4, max_len=80)
 HD96_G4 = G.DecoderConfig(layers=1, hidden=256, heads=4, kv_heads=1, head_dim=96,
                           intermediate=512, vocab=500, block=64, max_len=64)
@@ -295,8 +299,10 @@ G3 = G.DecoderConfig(layers=2, hidden=256, heads=6, kv_heads=2, head_dim=64,
 
 @pytest.mark.parametrize("cfg,prompt_len,steps",
                          [(SMALL, 20, 12), (QWEN_HEADS, 48, 8), (LONG_G4, 1050, 8),
-                          (SHORT_G4, 40, 8), (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
+                          (MID_G4, 650, 8), (CACHE512_G4, 490, 8), (SHORT_G4, 40, 8),
+                          (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
                          ids=["small", "qwen_heads", "long_cache_group4_hd32",
+                              "mid_cache_group4_hd32", "cache512_group4_hd32",
                               "short_cache_group4_hd32", "hd96_group4", "mha_group1", "group3"])
 def test_decoder_vs_oracle(ctx, cfg, prompt_len, steps):
     decoder_vs_oracle(ctx, cfg, prompt_len, steps)
@@ -320,8 +326,10 @@ def merge_attn_ctx():
 
 
 @pytest.mark.parametrize("cfg,prompt_len,steps",
-                         [(QWEN_HEADS, 48, 8), (HD96_G4, 30, 6), (MHA_G1, 40, 8), (G3, 33, 8)],
-                         ids=["qwen_heads", "hd96_group4", "mha_group1", "group3"])
+                         [(QWEN_HEADS, 48, 8), (MID_G4, 650, 8), (HD96_G4, 30, 6),
+                          (MHA_G1, 40, 8), (G3, 33, 8)],
+                         ids=["qwen_heads", "mid_cache_group4_hd32", "hd96_group4", "mha_group1",
+                              "group3"])
 def test_decoder_attention_self_merge_vs_oracle(merge_attn_ctx, cfg, prompt_len, steps):
     decoder_vs_oracle(merge_attn_ctx, cfg, prompt_len, steps)
 
