@@ -876,6 +876,19 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
   const int nsplit = (L + KS - 1) / KS;
   if (split >= nsplit) {
     asm volatile("" ::"v"(kreg[0]), "v"(vreg[0].x), "v"(x0[0]), "v"(xv.x));
+    if constexpr (!COH) {
+      // a split past pos leaves an empty partial (max -inf, sum 0, o 0) for
+      // the o projection's merge, which so needs no position of its own
+      const int t = threadIdx.x;
+      for (int i = t; i < group * HD; i += KS / kDecKW * 64)
+        a.po[((int64_t)(kh * group) * a.nsmax + (int64_t)(i / HD) * a.nsmax + split) * HD +
+             i % HD] = 0.0f;
+      if (t < group) {
+        const int64_t ps = (int64_t)(kh * group + t) * a.nsmax + split;
+        a.pml[2 * ps] = -INFINITY;
+        a.pml[2 * ps + 1] = 0.0f;
+      }
+    }
     return false;
   }
   // ---- per-head RMSNorm (double sums, wave-local) and rotary at pos
@@ -1587,8 +1600,8 @@ static int dec_record_step(mmnb_decoder *d) {
     if ((rc = launch_dec_attn(d, L, ck, cv)))
       return rc;
     if (d->attn_defer) {
-      const DecAttnPartials pa{&d->state->pos, d->part, dec_part_ml(d),
-                               (int)((Lmax + d->ks - 1) / d->ks), (int)hd, d->ks};
+      const DecAttnPartials pa{d->part, dec_part_ml(d), (int)((Lmax + d->ks - 1) / d->ks),
+                               (int)hd};
       if ((rc = launch_dec_gemv_attn(ctx, L.o, pa, d->x, d->x)))
         return rc;
     } else if ((rc = launch_dec_gemv(ctx, L.o, d->attn, nullptr, eps, kDecResidual, d->x, d->x,

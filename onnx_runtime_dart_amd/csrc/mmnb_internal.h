@@ -250,14 +250,13 @@ int64_t dec_gemv_blocks(const mmnb_ctx *ctx, int64_t n, int64_t k);
 
 // The decode attention's split partials, merged by the o projection's
 // prologue instead of by the attention launch itself.  Query head qh's
-// partial over split s (keys [s * ks, s * ks + ks)): o[hd] at
-// o + (qh * nsmax + s) * hd, (max, sum) at ml + 2 * (qh * nsmax + s); the
-// splits holding positions 0 .. *pos are merged.
+// partial over split s: o[hd] at o + (qh * nsmax + s) * hd, (max, sum) at
+// ml + 2 * (qh * nsmax + s); all nsmax splits are merged (a split past the
+// position holds max -inf, sum 0, o 0).
 struct DecAttnPartials {
-  const int *pos;
   const float *o;
   const float *ml;
-  int nsmax, hd, ks;
+  int nsmax, hd;
 };
 constexpr int kDecAttnMaxSplits = 16;  // splits one merge holds in registers
 constexpr int kDecAttnMaxK = 2048;     // heads * head_dim: two float4 per thread

@@ -368,11 +368,12 @@ static int launch_gemv_r(mmnb_ctx *ctx, int nbpc, dim3 grid, dim3 block, const f
 // a = the merged attention output, into sx[K] (K <= kDecAttnMaxK, whole
 // workgroup of kDecAttnMergeThreads).  Per query head the splits' maxima
 // give M, and a = sum_s w_s o_s with w_s = e^(m_s - M) / sum_u e^(m_u - M) l_u
-// over the splits holding positions 0 .. pos (at most NS, a static bound on
-// nsmax).  load() issues every load at once, ahead of the position they are
-// filtered by: thread t holds the (max, sum) pair of (head t / G, split
-// t % G) -- a head's splits in one aligned group of G lanes -- and the o
-// parts of the float4 quads t and t + 256 of a.  finish(), after the caller
+// over all nsmax splits (at most NS, a static bound): a split past the
+// position holds an empty partial (max -inf, sum 0, o 0) that weighs 0, so
+// the merge needs no position.  load() issues every load at once: thread t
+// holds the (max, sum) pair of (head t / G, split t % G) -- a head's splits
+// in one aligned group of G lanes -- and the o parts of the float4 quads t
+// and t + 256 of a.  finish(), after the caller
 // has issued its own loads: each head's maximum and denominator by DPP
 // within its lane group, the weights through LDS (one exponential per
 // pair), then each quad's weighted sum; it ends in a barrier.  Measured on
@@ -388,12 +389,10 @@ struct DecAttnMerge {
   static constexpr int QP = kDecAttnMaxK / 4 / kDecAttnMergeThreads;  // quads per thread
   float4 ov[QP][NS];
   float2 ml;
-  int qi[QP], qh[QP], pos_v;
+  int qi[QP], qh[QP];
 
   __device__ __forceinline__ void load(const DecAttnPartials &pa, int K) {
     const int t = threadIdx.x, nq = K >> 2, nh = K / pa.hd;
-    pos_v = __hip_atomic_load(const_cast<int *>(pa.pos), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
     ml = *(const float2 *)(pa.ml + 2 * (min(t / G, nh - 1) * pa.nsmax +
                                         min(t % G, pa.nsmax - 1)));
     // floor(4q / hd) as (4q + 1/2) / hd in float: the quotient lies at least
@@ -413,12 +412,10 @@ struct DecAttnMerge {
 
   __device__ __forceinline__ void finish(const DecAttnPartials &pa, float *sx) {
     __shared__ float sw[kDecAttnMergeThreads];
-    const int t = threadIdx.x;
-    const int L = __builtin_amdgcn_readfirstlane(pos_v) + 1;
-    const int nsplit = min((L + pa.ks - 1) / pa.ks, pa.nsmax);
-    // pair (head t / G, split t % G); splits past pos weigh 0.  Every lane
-    // takes part in the group reductions.
-    const bool live = t % G < nsplit;
+    const int t = threadIdx.x, nsplit = pa.nsmax;
+    // pair (head t / G, split t % G); lanes past nsmax and empty partials
+    // weigh 0.  Every lane takes part in the group reductions.
+    const bool live = t % G < nsplit && ml.x != -INFINITY;
     const float M = group_max<G>(live ? ml.x : -INFINITY);
     const float e = live ? expf(ml.x - M) : 0.0f;
     const float den = group_sum<G>(e * (live ? ml.y : 0.0f));
@@ -429,7 +426,7 @@ struct DecAttnMerge {
       float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
 #pragma unroll
       for (int s = 0; s < NS; s++) {
-        if (s < nsplit) {  // uniform: splits past pos are skipped, not weighted
+        if (s < nsplit) {  // uniform: lanes past nsmax are skipped, not weighted
           const float w = sw[qh[i] * G + s];
           n0 = fmaf(w, ov[i][s].x, n0);
           n1 = fmaf(w, ov[i][s].y, n1);
@@ -456,7 +453,7 @@ __global__ __launch_bounds__(64 * kDecMaxWaves) void k_dec_gemv(
   __shared__ __align__(16) float sx[ATTN ? kDecAttnMaxK : 4];
   kernarg_fence(X, gamma, eps, W, col_bytes, S, nb, bs_log2, K, N, resid, Y, argmax, C,
                 blockDim.x);
-  if constexpr (ATTN) kernarg_fence(pa.pos, pa.o, pa.ml, pa.nsmax, pa.hd, pa.ks);
+  if constexpr (ATTN) kernarg_fence(pa.o, pa.ml, pa.nsmax, pa.hd);
   const int nw = blockDim.x >> 6;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int h = l >> 5, t = l & 31;
@@ -649,8 +646,8 @@ int launch_dec_gemv_attn(mmnb_ctx *ctx, const mmnb_pack *p, const DecAttnPartial
   if (p->k % kSegK != 0 || p->k > kDecAttnMaxK)
     return fail(MMNB_ERR_UNSUPPORTED, "decoder GEMV (attention merge): K must be a multiple "
                                       "of 64, <= 2048");
-  if (!pa.pos || !pa.o || !pa.ml || pa.nsmax < 1 || pa.nsmax > kDecAttnMaxSplits ||
-      pa.hd < 4 || pa.hd % 4 != 0 || p->k % pa.hd != 0 || pa.ks < 1 ||
+  if (!pa.o || !pa.ml || pa.nsmax < 1 || pa.nsmax > kDecAttnMaxSplits ||
+      pa.hd < 4 || pa.hd % 4 != 0 || p->k % pa.hd != 0 ||
       p->k / pa.hd * (pa.nsmax <= 8 ? 8 : 16) > kDecAttnMergeThreads)
     return fail(MMNB_ERR_ARG, "decoder GEMV (attention merge): bad partials");
   const int C = (int)(p->col_bytes / 16);
