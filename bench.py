@@ -48,7 +48,7 @@ MFMA_FP16_PEAK_TFLOPS = 2500.0
 MFMA_FP32_PEAK_TFLOPS = 157.3
 INT8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 320 * 1024 * 1024
-HOST_CPU_SHARE = 16  # host cores the GPU box allots to one GPU's jobs
+HOST_CPU_SHARE = 16  # host cores a single-GPU MI355X node allots to one GPU's jobs
 TRAFFIC_SOURCE = ("committed rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE) of the same "
                   "workload, profiles/traffic.json; not measured in this run")
 
@@ -560,8 +560,8 @@ def cpu_baseline(synth, budget_s):
     (DynamicQuantizeLinear -> MatMulInteger -> rescale, one thread)."""
     from oracle import refcpu
 
-    # The GPU box gives each GPU's jobs a share of 16 host cores, whatever the
-    # machine's own count: the multi-threaded legs use that share (or fewer
+    # A single-GPU MI355X node gives each GPU's jobs a share of 16 host cores,
+    # whatever the machine's own count: the multi-threaded legs use that share (or fewer
     # if fewer CPUs are allowed to this process), and both counts are stated.
     nproc = os.cpu_count() or 1
     allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
