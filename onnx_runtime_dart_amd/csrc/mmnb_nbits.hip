@@ -1167,7 +1167,7 @@ static int launch_prep_a(mmnb_ctx *ctx, const float *d_a, int64_t lda, int64_t m
 // trip.  (The buffer form rather than global_load_lds: after a pending FLAT
 // DMA the compiler waits for every outstanding LDS read before the first
 // MFMA of a matrix phase; with buffer loads it waits per fragment.  M = 512,
-// K = N = 4096 kernel, one box: block 128 39.7 -> 36.5 us, block 32
+// K = N = 4096 kernel, one device: block 128 39.7 -> 36.5 us, block 32
 // 41.0 -> 40.8 us.)
 // Every thread issues the same number of DMA loads per stage (kL), so "stage
 // s has landed" is vmcnt <= (NST-2)*kL once the next stages are issued; a
