@@ -942,29 +942,30 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
       if (jv >= pos) vreg[u] = jv == pos ? vnew : make_float2(0.0f, 0.0f);
     }
   }
-  // ---- softmax over the wave's keys (scores read out of lanes 8u, so
-  // wave-uniform) and o = sum_u p_u v_u; a wave whose keys are all past pos
-  // contributes max -inf and nothing else
+  // ---- softmax over the wave's keys and o = sum_u p_u v_u.  The maximum
+  // from the scores read out of lanes 8u (wave-uniform); each lane then
+  // forms the probability of its own key, one exponential per lane in
+  // parallel, and the 8 probabilities are read out of lanes 8u in turn (the
+  // wave-uniform scores fed 8 dependent exponentials per lane: ~2 us per
+  // layer of the decode step).  A wave whose keys are all past pos
+  // contributes max -inf and nothing else.
 #pragma unroll
   for (int g = 0; g < kDecMaxGroup; g++) {
     if (g < group) {
-      float s[kDecKW];
       float mx = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < kDecKW; u++) {
-        s[u] = __builtin_bit_cast(float,
-                                  __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc[g]), 8 * u));
-        mx = fmaxf(mx, s[u]);
-      }
+      for (int u = 0; u < kDecKW; u++)
+        mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                     __builtin_bit_cast(int, sc[g]), 8 * u)));
+      const float pl = mx != -INFINITY ? expf(sc[g] - mx) : 0.0f;  // 0 past pos
       float ls = 0.0f, o0 = 0.0f, o1 = 0.0f;
-      if (mx != -INFINITY) {
 #pragma unroll
-        for (int u = 0; u < kDecKW; u++) {
-          const float pu = expf(s[u] - mx);
-          ls += pu;
-          o0 = fmaf(pu, vreg[u].x, o0);
-          o1 = fmaf(pu, vreg[u].y, o1);
-        }
+      for (int u = 0; u < kDecKW; u++) {
+        const float pu = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pl), 8 * u));
+        ls += pu;
+        o0 = fmaf(pu, vreg[u].x, o0);
+        o1 = fmaf(pu, vreg[u].y, o1);
       }
       if (2 * l < HD) *(float2 *)(&so[w][g][2 * l]) = make_float2(o0, o1);
       if (l == 0) {
