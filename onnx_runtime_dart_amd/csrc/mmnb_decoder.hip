@@ -736,15 +736,13 @@ __global__ __launch_bounds__(1024) void k_dec_end(DecState *__restrict__ st,
 // split holding position pos uses the new k / v directly and also writes
 // them into the cache; no workgroup reads an entry written in the same
 // launch.
-// Keys per split KS: 32 (4 waves) for caches of up to 512 rows, 64 (8 waves)
-// for longer ones.  At the Qwen3-0.6B shape (cache 320, position ~300) the
-// 32-key launch takes 4.2 us eager against 5.0 us for 64 keys, and the
-// decode step the same time either way (0.578-0.580 ms per token): the o
-// projection merges twice the partials.  Past 512 rows 64-key splits keep
-// the merge in the o projection up to 1024 rows.
+// Keys per split kDecKS = 64 (8 waves).  At the Qwen3-0.6B shape (cache 320,
+// position ~300, decode step as a graph): 32-key splits 0.568 ms per token,
+// 64 0.559-0.561, 128 0.612; the o projection merges half the partials of
+// 32-key splits, and 64-key splits keep that merge (<= 16 splits) up to
+// 1024 rows.
 constexpr int kDecKW = 8;  // keys per wave
-constexpr int kDecKSShort = 32, kDecKSLong = 64;
-constexpr int kDecKSShortMaxLen = 512;
+constexpr int kDecKS = 64;
 template <int KS>
 constexpr int dec_attn_threads() { return 64 * (KS / kDecKW); }
 constexpr int kDecMaxGroup = 4;     // query heads per KV head
@@ -1251,7 +1249,7 @@ struct mmnb_decoder {
   float *rot = nullptr;     // the decode step's rotary row: cos | sin, hd/2 each
   float *part = nullptr;    // attention partials: o [heads, splits, hd], then (max, sum)
   bool attn_defer = false;  // the o projection merges them (else the attention launch)
-  int ks = kDecKSLong;      // keys per attention split
+  int ks = kDecKS;          // keys per attention split
   int *counters = nullptr;  // per KV head: attention splits finished
   DecState *state = nullptr;
   unsigned long long *keys = nullptr;  // lm_head workgroups' best (value, ~index)
@@ -1324,7 +1322,7 @@ int mmnb_decoder_create(mmnb_ctx *ctx, const mmnb_decoder_config *cfg, const flo
   const int64_t H = c.hidden, nh = c.heads, kvh = c.kv_heads, hd = c.head_dim,
                 I = c.intermediate, Lmax = c.max_len;
   const int64_t QKV = (nh + 2 * kvh) * hd;
-  d->ks = Lmax <= kDecKSShortMaxLen ? kDecKSShort : kDecKSLong;
+  d->ks = kDecKS;
   const int64_t nsplit = (Lmax + d->ks - 1) / d->ks;
   auto A = [&](size_t bytes, void **p) { return dec_alloc(d, bytes, p); };
   if ((rc = dec_upload(d, embed, (size_t)(c.vocab * H), &d->embed)) ||
@@ -1571,7 +1569,7 @@ static int launch_dec_attn(mmnb_decoder *d, const mmnb_decoder::Layer &L, float 
                 dim3(dec_attn_threads<KS>()), 0, (const DecState *)d->state, args,            \
                 d->counters))
 #define MMNB_DEC_ATTN(HD)                                                                      \
-  (d->ks == kDecKSShort ? MMNB_DEC_ATTN_KS(HD, kDecKSShort) : MMNB_DEC_ATTN_KS(HD, kDecKSLong))
+  MMNB_DEC_ATTN_KS(HD, kDecKS)
   switch (c.head_dim) {
     case 32: return MMNB_DEC_ATTN(32);
     case 64: return MMNB_DEC_ATTN(64);

@@ -277,12 +277,11 @@ SMALL = G.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64,
                         intermediate=512, vocab=1000, block=64, max_len=64)
 QWEN_HEADS = G.DecoderConfig(layers=2, hidden=1024, heads=16, kv_heads=8, head_dim=128,
                              intermediate=3072, vocab=2048, block=128, max_len=96)
-# four query heads per KV head, head sizes 32 and 96.  Caches of up to 512
-# rows split into 32-key splits, longer ones into 64-key splits; the o
-# projection merges up to 16 splits.  LONG_G4 decodes past 16 splits of 64
-# keys, so its decode attention merges the splits itself and takes the
-# partials in two batches; MID_G4 has 64-key splits merged by the o
-# projection (11 of them), CACHE512_G4 sixteen 32-key splits.
+# four query heads per KV head, head sizes 32 and 96.  The decode attention
+# splits the cache into 64-key splits; the o projection merges up to 16 of
+# them.  LONG_G4 decodes past 16 splits, so its decode attention merges the
+# splits itself and takes the partials in two batches; MID_G4 has 11 splits
+# merged by the o projection, CACHE512_G4 8.
 LONG_G4 = G.DecoderConfig(layers=1, hidden=256, heads=8, kv_heads=2, head_dim=32,
                           intermediate=512, vocab=500, block=64, max_len=1100)
 MID_G4 = dataclasses.replace(LONG_G4, max_len=700)
