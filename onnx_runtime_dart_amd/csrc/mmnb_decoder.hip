@@ -976,14 +976,20 @@ __device__ bool dec_attn_partial(const DecAttnArgs &a, int pos_in, int split, in
   // ---- the split's partial: thread (head g, dim pair dp) merges the waves
   {
     const int g = t / kHr, dp = t % kHr;
-    if (g < group) {
-      float M = sm[0][g];
+    // the waves' weights e^(m_w - M): lane dp forms that of wave dp % NW
+    // (one exponential per lane) and takes the others from the lanes of its
+    // aligned group of NW, which share g (NW divides kHr)
+    static_assert(kHr % kDecAttnWaves == 0, "wave weights by lane groups");
+    float M = sm[0][g < group ? g : 0];
 #pragma unroll
-      for (int ww = 1; ww < kDecAttnWaves; ww++) M = fmaxf(M, sm[ww][g]);
+    for (int ww = 1; ww < kDecAttnWaves; ww++) M = fmaxf(M, sm[ww][g < group ? g : 0]);
+    const float mine = expf(sm[dp % kDecAttnWaves][g < group ? g : 0] - M);  // 0: max -inf
+    const int base = (threadIdx.x & 63) & ~(kDecAttnWaves - 1);
+    if (g < group) {
       float ls = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
       for (int ww = 0; ww < kDecAttnWaves; ww++) {
-        const float wt = expf(sm[ww][g] - M);  // 0 for a wave with max -inf
+        const float wt = __shfl(mine, base + ww, 64);
         const float2 ov = *(const float2 *)(&so[ww][g][2 * dp]);
         ls = fmaf(wt, sl[ww][g], ls);
         o0 = fmaf(wt, ov.x, o0);
