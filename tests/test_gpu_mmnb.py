@@ -155,6 +155,14 @@ def test_prefill_full_size_row_sample(ctx, m, n, block):
     (33, 5000, 130, 256, True),  # block 256: group ranges aligned to 4 segments
     (128, 1024, 256, 512, False),  # block 512: 8 segments per block
     (100, 1100, 96, 32, True),
+    # boundaries: the first M on the GEMM path, a small-batch prefill on the
+    # headline's weights, one output column, K of a single block
+    (9, 1000, 65, 32, True),
+    (16, 4096, 4096, 32, True),
+    (1, 1024, 1, 32, True),
+    (20, 1024, 1, 64, False),
+    (12, 16, 5, 16, False),
+    (1, 32, 3, 32, True),
 ])
 def test_edge_shapes(ctx, m, k, n, block, zp):
     p = synth.mmnb_problem(m, k, n, block, zp, seed=11 + m + n)
